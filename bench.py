@@ -1,0 +1,239 @@
+"""Benchmark of the GEMM-family hot path on one MI355X.
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME] [--no-cpu]``
+
+A "step" is one call of an operator on one batch of synthetic, seeded inputs that
+are resident in HBM before timing starts.  The headline (``value``) is the fp8
+a8w8 block-scaled GEMM at M=2048, N=7168, K=4096 -- the first configuration named
+by the metric; every other BASELINE configuration (bf16 GEMM 4096^3 and 1024^3,
+fp16 GEMM+bias+{GELU,ReLU,SiLU} 4096^3, batched GEMM, the fp8 M sweep, MoE decode
+T=64 and prefill T=4096) is reported in ``configs`` with the same fields.
+
+Per configuration: W warm-up steps, then K steps bracketed by
+``torch.cuda.synchronize()``; ``ms_per_step`` is wall time / K and ``kernel_ms`` the
+mean of per-step HIP events recorded on the stream the kernels are launched on
+(torch's current stream).  ``cold_ms`` is the reference drivers' protocol: median of
+events around a step preceded by a 512 MiB cache flush (``kore/tasks/_genops.py:787-813``
+flushes 256 MiB; MI355X has 256 MiB of Infinity Cache).  Roofline fractions use
+the algorithmic FLOPs/bytes of ``kore_amd.roofline`` and MI355X peaks (bf16 2.5 PF,
+fp8 5.0 PF, HBM 8 TB/s).
+
+``cpu_baseline`` times the CPU oracle (the restated torch-fp32 reference) on a row
+sample of the headline workload, on all host cores; it is a reported baseline.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+
+def _parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--only", default=None, help="comma-separated config names to run")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    p.add_argument("--cold-iters", type=int, default=10)
+    return p.parse_args()
+
+
+class Timer:
+    def __init__(self, steps: int, warmup: int, cold_iters: int):
+        self.steps, self.warmup, self.cold_iters = steps, warmup, cold_iters
+        self._flush = None
+
+    def run(self, fn):
+        for _ in range(self.warmup):
+            fn()
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(self.steps)]
+        t0 = time.perf_counter()
+        for s, e in ev:
+            s.record()
+            fn()
+            e.record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3 / self.steps
+        kern = statistics.fmean(s.elapsed_time(e) for s, e in ev)
+        cold = []
+        if self.cold_iters:
+            if self._flush is None:
+                self._flush = torch.empty(512 * 1024 * 1024, dtype=torch.int8, device="cuda")
+            for _ in range(self.cold_iters):
+                self._flush.zero_()
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record()
+                fn()
+                e.record()
+                torch.cuda.synchronize()
+                cold.append(s.elapsed_time(e))
+        return wall, kern, (statistics.median(cold) if cold else None)
+
+
+def _entry(name, op, dims, dtype, wall, kern, cold, extra=None):
+    from kore_amd import roofline as R
+
+    rf = R.roofline(op, dims, dtype)
+    t = kern * 1e-3
+    out = {
+        "name": name, "op": op, "dims": dims, "dtype": dtype,
+        "ms_per_step": round(wall, 5), "kernel_ms": round(kern, 5),
+        "cold_ms": round(cold, 5) if cold is not None else None,
+        "tflops": round(rf.flops / t / 1e12, 2),
+        "tb_per_s": round(rf.bytes / t / 1e12, 3),
+        "bound": rf.bound,
+        "frac_of_bound": round(rf.t_min_s / t, 4),
+        "frac_mfma_peak": round(rf.flops / t / rf.peak_flops, 4),
+        "frac_hbm_peak": round(rf.bytes / t / rf.peak_bw, 4),
+    }
+    if extra:
+        out.update(extra)
+    return out
+
+
+def build_configs(dev):
+    import kore_amd
+    from kore_amd import workloads as W
+
+    cfg = {}
+
+    def fp8(M):
+        xq, wq, xs, ws = W.fp8_inputs(M, 7168, 4096, seed=0, device=dev)
+        return (lambda: kore_amd.gemm_a8w8_blockscale(xq, wq, xs, ws)), ("gemm_fp8", {"M": M, "N": 7168, "K": 4096}, "fp8")
+
+    cfg["fp8_blockscale_2048x7168x4096"] = lambda: fp8(2048)
+
+    def dense(n):
+        a, b = W.dense_inputs(n, n, n, seed=0, device=dev)
+        return (lambda: kore_amd.gemm(a, b)), ("gemm", {"M": n, "N": n, "K": n}, "bf16")
+
+    cfg["bf16_gemm_4096"] = lambda: dense(4096)
+    cfg["bf16_gemm_1024"] = lambda: dense(1024)
+
+    def fused(act):
+        a, b, bias = W.fused_inputs(4096, 4096, 4096, seed=0, device=dev)
+        return (lambda: kore_amd.gemm_fused(a, b, bias, act)), ("gemm", {"M": 4096, "N": 4096, "K": 4096}, "fp16")
+
+    for act in ("gelu", "relu", "silu"):
+        cfg[f"fp16_gemm_bias_{act}_4096"] = (lambda a=act: fused(a))
+
+    def batched():
+        a, b = W.batched_inputs(64, 1024, 1024, 128, seed=0, device=dev)
+        return (lambda: kore_amd.batched_gemm(a, b)), ("batched_gemm", {"B": 64, "M": 1024, "N": 1024, "K": 128}, "bf16")
+
+    cfg["bf16_batched_64x1024x1024x128"] = batched
+    for M in (512, 128, 16):
+        cfg[f"fp8_blockscale_{M}x7168x4096"] = (lambda m=M: fp8(m))
+
+    def moe(T):
+        args = W.moe_inputs(T, 8, 2, 4096, 14336, seed=0, device=dev)
+        return (lambda: kore_amd.fused_moe(*args)), ("fused_moe", {"M": T, "E": 8, "topk": 2, "D": 4096, "I": 14336}, "bf16")
+
+    cfg["moe_decode_T64"] = lambda: moe(64)
+    cfg["moe_prefill_T4096"] = lambda: moe(4096)
+    return cfg
+
+
+def cpu_baseline(seconds_budget: float = 20.0):
+    """Time the CPU oracle (restated torch-fp32 reference) on a row sample of the
+    headline fp8 workload: rows [0, m) of X against the full W [7168, 4096]."""
+    from kore_amd import workloads as W
+    from oracle.quant import matmul_blockscale_ref
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    m = 128
+    xq, wq, xs, ws = W.fp8_inputs(2048, 7168, 4096, seed=0, device="cpu")
+    xq, xs = xq[:m].contiguous(), xs[:m].contiguous()
+    matmul_blockscale_ref(xq, wq, xs, ws)  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 and time.perf_counter() - t_start < seconds_budget:
+        t0 = time.perf_counter()
+        matmul_blockscale_ref(xq, wq, xs, ws)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": round(2.0 * m * 7168 * 4096 / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle.quant.matmul_blockscale_ref on rows 0..{m} of the 2048x7168x4096 workload "
+                      f"(fp32 dequant + torch CPU matmul), median of {len(times)} runs, "
+                      f"{t * 1e3:.1f} ms per run"}
+
+
+def main():
+    args = _parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on exactly one GPU; --gpus {args.gpus} is not supported "
+              "(the GEMM family shards without communication -- see DESIGN.md).", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 1
+    import kore_amd._lib as L
+
+    L.load()
+    dev = torch.device("cuda:0")
+    timer = Timer(args.steps, args.warmup, args.cold_iters)
+    cfgs = build_configs(dev)
+    names = list(cfgs)
+    if args.only:
+        names = [n for n in names if n in args.only.split(",")]
+    results = {}
+    for name in names:
+        fn, (op, dims, dtype) = cfgs[name]()
+        wall, kern, cold = timer.run(fn)
+        results[name] = _entry(name, op, dims, dtype, wall, kern, cold)
+        print(f"# {name}: {results[name]['tflops']} TFLOP/s, {results[name]['tb_per_s']} TB/s, "
+              f"kernel {kern * 1e3:.1f} us, frac_of_bound {results[name]['frac_of_bound']}",
+              file=sys.stderr, flush=True)
+        del fn
+        torch.cuda.empty_cache()
+    head_name = "fp8_blockscale_2048x7168x4096"
+    head = results.get(head_name) or next(iter(results.values()))
+    peak_unit = "TFLOP/s" if head["bound"] == "mfma" else "GB/s"
+    if head["bound"] == "mfma":
+        achieved, peak = head["tflops"], (5000.0 if "fp8" in head["dtype"] else 2500.0)
+    else:
+        achieved, peak = head["tb_per_s"] * 1000.0, 8000.0
+    line = {
+        "metric": "TFLOP/s + % MFMA peak, fp8 blockscale GEMM 2048x7168x4096 and bf16 GEMM 4096^3",
+        "value": round(2.0 * 2048 * 7168 * 4096 / (head["ms_per_step"] * 1e-3) / 1e12, 2)
+        if head["name"] == head_name else head["tflops"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3 (fp32 accumulate, bf16 out)" if "fp8" in head["dtype"] else head["dtype"],
+        "data": "synthetic (seeded N(0,1) inputs, quantised 1x128 / 128x128 to OCP e4m3)",
+        "config": {"workload": head["name"], "M": 2048, "N": 7168, "K": 4096, "parallelism": "single-gpu"},
+        "frac_mfma_peak": head["frac_mfma_peak"],
+        "roofline": {"bound": head["bound"], "achieved": achieved, "peak": peak, "unit": peak_unit,
+                     "frac": round(achieved / peak, 4), "traffic": None,
+                     "kernel": "gemm_fp8_bs_kernel", "kernel_ms": head["kernel_ms"]},
+        "configs": results,
+    }
+    if "bf16_gemm_4096" in results:
+        r = results["bf16_gemm_4096"]
+        line["bf16_gemm_4096"] = {"tflops": r["tflops"], "frac_mfma_peak": r["frac_mfma_peak"],
+                                  "kernel_ms": r["kernel_ms"]}
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

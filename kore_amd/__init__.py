@@ -1,0 +1,27 @@
+"""kore_amd -- MI355X (gfx950) native GEMM family for the KORE operator task suite.
+
+Operators (all on HIP device tensors, launched on torch's current stream):
+dense bf16/fp16 GEMM with fused bias + activation epilogues, batched GEMM, OCP-e4m3
+fp8 a8w8 block-scaled GEMM, and the fused top-k MoE SiLU grouped GEMM.  The kernels
+live in ``libkore_amd.so`` (built by ``python -m kore_amd.build``); see
+``include/kore_amd.h`` for its C ABI.
+"""
+
+from .ops import (  # noqa: F401
+    ACT_CODE,
+    GEMM_FUSION_OPS,
+    batched_gemm,
+    fused_moe,
+    gemm,
+    gemm_a8w8_blockscale,
+    gemm_fused,
+    moe_align,
+    moe_gated_silu,
+)
+from . import ops as _ops
+
+for _name in _ops.GEMM_FUSION_OPS:
+    globals()[_name] = getattr(_ops, _name)
+
+__all__ = ["gemm", "gemm_fused", "batched_gemm", "gemm_a8w8_blockscale", "fused_moe", "moe_gated_silu", "moe_align",
+           *_ops.GEMM_FUSION_OPS]

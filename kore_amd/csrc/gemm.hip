@@ -1,0 +1,322 @@
+// Dense and batched bf16/fp16 GEMM with fused bias + activation epilogue (gfx950).
+//
+// C[M,N] = act(A[M,K] @ B[K,N] + bias[N]) with fp32 accumulation, one RNE cast.
+//
+// Fast path ("tile kernel"): 256 threads = 4 waves in a 2x2 grid, macro tile BM x BN
+// (256x256 or 128x128), K step 64.  A is K-contiguous; B is either K-contiguous (the
+// A.B^T / A.W^T case) or N-contiguous (natural [K,N]).  Global -> VGPR 16-byte loads
+// are issued for tile k+1 while tile k is multiplied out of the other LDS buffer
+// (double buffering, one barrier per K step).  LDS rows are 128 bytes (64 x 16-bit)
+// with an XOR swizzle of the 16-byte chunks so the MFMA fragment reads
+// (ds_read_b128, 32 consecutive rows per half-wave) are bank-conflict free.  An
+// N-contiguous B tile is transposed in registers (8x8 blocks of 16-bit values with
+// v_perm_b32) before it is written to LDS in the same K-contiguous layout.
+// The MFMA is issued with the B fragment as the first operand, so each lane ends up
+// holding 4 N-consecutive outputs of one row; the epilogue applies bias and the
+// activation in fp32, packs, stages the wave's tile in LDS and writes C with
+// 16-byte row-contiguous stores.
+//
+// Generic path: any strides and any K, fp32 FMA on 64x64 tiles staged through LDS.
+#include "../../include/kore_amd.h"
+#include "kore_common.hpp"
+#include "tile_engine.hpp"
+
+#include <type_traits>
+
+namespace kore {
+namespace {
+
+struct TileParams {
+  const uint16_t* a;
+  const uint16_t* b;
+  const uint16_t* bias;
+  uint16_t* c;
+  int M, N, K;
+  int64_t lda;  // A row stride (elements); A is K-contiguous
+  int64_t ldb;  // B_KC: stride between n rows of B^T;  B_NC: stride between k rows of B
+  int64_t ldc;  // C row stride; C is N-contiguous
+  int64_t sa, sb, sc;  // batch strides (elements)
+  int tiles_m, tiles_n, tiles_per_batch;
+  int act;
+  int vec_store;  // 16-byte C stores allowed (ldc % 8 == 0, aligned)
+};
+
+constexpr int kGroupM = 4;
+
+template <typename T, int BL, int BM, int BN>
+__global__ void __launch_bounds__(kEngineThreads)
+    gemm_tile_kernel(const TileParams p) {
+  using E = TileEngine<T, BM, BN, 2, 2, BL>;
+  using Op = MfmaOp<T>;
+  constexpr int MI = E::MI, NI = E::NI;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // ---- tile coordinates: XCD-aware remap, then grouped raster per batch ----
+  const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int batch = bid / p.tiles_per_batch;
+  const int t = bid - batch * p.tiles_per_batch;
+  const int width = kGroupM * p.tiles_n;
+  const int grp = t / width;
+  const int first_m = grp * kGroupM;
+  const int gsz = min(p.tiles_m - first_m, kGroupM);
+  const int tl = t - grp * width;
+  const int m0 = (first_m + tl % gsz) * BM;
+  const int n0 = (tl / gsz) * BN;
+
+  const uint16_t* A = p.a + batch * p.sa;
+  const uint16_t* B = p.b + batch * p.sb;
+  uint16_t* C = p.c + batch * p.sc;
+  const int M = p.M, N = p.N, K = p.K;
+
+  E eng;
+  const int ch8 = (tid & 7) * 8;
+#pragma unroll
+  for (int j = 0; j < E::LA; ++j) eng.a_src[j] = A + (int64_t)min(m0 + E::a_row_of(tid, j), M - 1) * p.lda + ch8;
+  if constexpr (BL == B_KC) {
+#pragma unroll
+    for (int j = 0; j < E::LB; ++j) eng.b_src[j] = B + (int64_t)min(n0 + E::b_row_of(tid, j), N - 1) * p.ldb + ch8;
+  } else {
+#pragma unroll
+    for (int j = 0; j < E::LB; ++j)
+      eng.b_src[j] = B + (int64_t)(E::nc_kb(tid, j) * 8) * p.ldb + min(n0 + E::nc_nb(tid, j) * 8, N - 8);
+  }
+  eng.ldb = p.ldb;
+
+  f32x16_t acc[MI][NI];
+  E::zero(acc);
+  eng.mainloop(lds, K, acc);
+
+  // ---- epilogue: bias + activation in fp32, pack, stage per wave, 16-byte stores ----
+  using St = Stager<E::WROWS, E::WCOLS>;
+  uint16_t* stg = lds + wave * (E::WROWS * E::WCOLS);
+  const int mw0 = m0 + wm * E::WROWS, nw0 = n0 + wn * E::WCOLS;
+  auto epi = [&](auto act_tag) {
+    constexpr int ACT = decltype(act_tag)::value;
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int nl = out_col(j, g, lane);
+        float bv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (p.bias != nullptr) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int n = nw0 + nl + e;
+            bv[e] = n < N ? Op::to_f32(p.bias[n]) : 0.0f;
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = apply_act<ACT>(acc[i][j][4 * g + e] + bv[e]);
+          St::put(stg, out_row(i, lane), nl, u32x2_t{Op::pack2(v[0], v[1]), Op::pack2(v[2], v[3])});
+        }
+      }
+    }
+  };
+  switch (p.act) {
+    case ACT_RELU: epi(std::integral_constant<int, ACT_RELU>{}); break;
+    case ACT_GELU: epi(std::integral_constant<int, ACT_GELU>{}); break;
+    case ACT_SILU: epi(std::integral_constant<int, ACT_SILU>{}); break;
+    case ACT_TANH: epi(std::integral_constant<int, ACT_TANH>{}); break;
+    case ACT_SIGMOID: epi(std::integral_constant<int, ACT_SIGMOID>{}); break;
+    default: epi(std::integral_constant<int, ACT_NONE>{}); break;
+  }
+  __syncthreads();
+  const bool vec = p.vec_store != 0;
+  St::drain(stg, lane, [&](int row, int col, u32x4_t v) {
+    const int gm = mw0 + row, gn = nw0 + col;
+    if (gm < M) store_row8(C + (int64_t)gm * p.ldc + gn, gn, N, vec, v);
+  });
+}
+
+// ---------------------------------------------------------------------------------
+// Generic-stride kernel: 64x64 tile, BK 16, fp32 FMA, any strides / K / alignment.
+// ---------------------------------------------------------------------------------
+struct GenericParams {
+  const uint16_t* a;
+  const uint16_t* b;
+  const uint16_t* bias;
+  uint16_t* c;
+  int M, N, K;
+  int64_t sam, sak, sbk, sbn, scm;
+  int64_t sa, sb, sc;
+  int act;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(256) gemm_generic_kernel(const GenericParams p) {
+  using Op = MfmaOp<T>;
+  __shared__ float sA[16][64 + 1];
+  __shared__ float sB[16][64 + 1];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64, z = blockIdx.z;
+  const uint16_t* A = p.a + z * p.sa;
+  const uint16_t* B = p.b + z * p.sb;
+  uint16_t* C = p.c + z * p.sc;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < p.K; k0 += 16) {
+    for (int q = tid; q < 16 * 64; q += 256) {
+      const int kk = q / 64, mm = q % 64;
+      const int gm = m0 + mm, gk = k0 + kk;
+      sA[kk][mm] = (gm < p.M && gk < p.K) ? Op::to_f32(A[gm * p.sam + gk * p.sak]) : 0.0f;
+      const int gn = n0 + mm;
+      sB[kk][mm] = (gn < p.N && gk < p.K) ? Op::to_f32(B[gk * p.sbk + gn * p.sbn]) : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      float av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = sA[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = sB[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int gm = m0 + ty * 4 + i;
+    if (gm >= p.M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int gn = n0 + tx * 4 + j;
+      if (gn >= p.N) continue;
+      float v = acc[i][j] + (p.bias ? Op::to_f32(p.bias[gn]) : 0.0f);
+      switch (p.act) {
+        case ACT_RELU: v = apply_act<ACT_RELU>(v); break;
+        case ACT_GELU: v = apply_act<ACT_GELU>(v); break;
+        case ACT_SILU: v = apply_act<ACT_SILU>(v); break;
+        case ACT_TANH: v = apply_act<ACT_TANH>(v); break;
+        case ACT_SIGMOID: v = apply_act<ACT_SIGMOID>(v); break;
+        default: break;
+      }
+      C[gm * p.scm + gn] = (uint16_t)(Op::pack2(v, 0.0f) & 0xffffu);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Host dispatch
+// ---------------------------------------------------------------------------------
+struct GemmDesc {
+  int dtype, act;
+  const void *a, *b, *bias;
+  void* c;
+  int64_t M, N, K, batch;
+  int64_t sam, sak, sbk, sbn, scm;  // element strides; B given as (k, n)
+  int64_t sa, sb, sc;               // batch strides
+};
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+template <typename T, int BL, int BM, int BN>
+int launch_tile(const GemmDesc& d, hipStream_t stream) {
+  TileParams p;
+  p.a = (const uint16_t*)d.a;
+  p.b = (const uint16_t*)d.b;
+  p.bias = (const uint16_t*)d.bias;
+  p.c = (uint16_t*)d.c;
+  p.M = (int)d.M;
+  p.N = (int)d.N;
+  p.K = (int)d.K;
+  p.lda = d.sam;
+  p.ldb = (BL == B_KC) ? d.sbn : d.sbk;
+  p.ldc = d.scm;
+  p.sa = d.sa;
+  p.sb = d.sb;
+  p.sc = d.sc;
+  p.tiles_m = (int)((d.M + BM - 1) / BM);
+  p.tiles_n = (int)((d.N + BN - 1) / BN);
+  p.tiles_per_batch = p.tiles_m * p.tiles_n;
+  p.act = d.act;
+  p.vec_store = (d.scm % 8 == 0) && aligned16(d.c) && (d.sc % 8 == 0);
+  const int64_t blocks = (int64_t)p.tiles_per_batch * d.batch;
+  if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "gemm: grid too large");
+  hipLaunchKernelGGL((gemm_tile_kernel<T, BL, BM, BN>), dim3((unsigned)blocks), dim3(kEngineThreads), 0, stream, p);
+  return check_launch("gemm_tile_kernel");
+}
+
+template <typename T>
+int launch_generic(const GemmDesc& d, hipStream_t stream) {
+  GenericParams p;
+  p.a = (const uint16_t*)d.a;
+  p.b = (const uint16_t*)d.b;
+  p.bias = (const uint16_t*)d.bias;
+  p.c = (uint16_t*)d.c;
+  p.M = (int)d.M;
+  p.N = (int)d.N;
+  p.K = (int)d.K;
+  p.sam = d.sam;
+  p.sak = d.sak;
+  p.sbk = d.sbk;
+  p.sbn = d.sbn;
+  p.scm = d.scm;
+  p.sa = d.sa;
+  p.sb = d.sb;
+  p.sc = d.sc;
+  p.act = d.act;
+  if (d.batch > 65535) return set_error(KORE_EUNSUPPORTED, "gemm: batch > 65535 on the generic path");
+  dim3 grid((unsigned)((d.N + 63) / 64), (unsigned)((d.M + 63) / 64), (unsigned)d.batch);
+  hipLaunchKernelGGL(gemm_generic_kernel<T>, grid, dim3(256), 0, stream, p);
+  return check_launch("gemm_generic_kernel");
+}
+
+template <typename T>
+int dispatch_typed(const GemmDesc& d, hipStream_t stream) {
+  // Fast-path preconditions: A K-contiguous with 16-byte aligned rows, K % 8 == 0,
+  // B K- or N-contiguous with 16-byte aligned rows, C N-contiguous.
+  const bool a_ok = d.sak == 1 && d.sam % 8 == 0 && aligned16(d.a) && d.sa % 8 == 0 && d.K % 8 == 0;
+  const bool b_kc = d.sbk == 1 && d.sbn % 8 == 0 && aligned16(d.b) && d.sb % 8 == 0;
+  const bool b_nc = d.sbn == 1 && d.sbk % 8 == 0 && aligned16(d.b) && d.sb % 8 == 0 && d.N % 8 == 0;
+  const bool fits32 = d.M < (1ll << 31) && d.N < (1ll << 31) && d.K < (1ll << 31);
+  if (a_ok && (b_kc || b_nc) && fits32) {
+    // Macro tile: 256x256 when it still gives >= ~1 wave of tiles, else 128x128.
+    const int64_t big_tiles = ((d.M + 255) / 256) * ((d.N + 255) / 256) * d.batch;
+    const bool big = big_tiles >= 192;
+    if (b_kc) return big ? launch_tile<T, B_KC, 256, 256>(d, stream) : launch_tile<T, B_KC, 128, 128>(d, stream);
+    return big ? launch_tile<T, B_NC, 256, 256>(d, stream) : launch_tile<T, B_NC, 128, 128>(d, stream);
+  }
+  return launch_generic<T>(d, stream);
+}
+
+int run_gemm(const GemmDesc& d, void* stream) {
+  if (d.c == nullptr || (d.K > 0 && (d.a == nullptr || d.b == nullptr)))
+    return set_error(KORE_EINVAL, "gemm: null pointer");
+  if (d.M <= 0 || d.N <= 0 || d.K < 0 || d.batch <= 0)
+    return set_error(KORE_EINVAL, "gemm: need M, N, batch >= 1 and K >= 0 (M=%lld N=%lld K=%lld batch=%lld)", (long long)d.M,
+                     (long long)d.N, (long long)d.K, (long long)d.batch);
+  if (d.act < KORE_ACT_NONE || d.act > KORE_ACT_SIGMOID) return set_error(KORE_EINVAL, "gemm: unknown act %d", d.act);
+  if (d.scm < d.N) return set_error(KORE_EINVAL, "gemm: ldc_m (%lld) < N (%lld)", (long long)d.scm, (long long)d.N);
+  hipStream_t s = (hipStream_t)stream;
+  if (d.dtype == KORE_DT_BF16) return dispatch_typed<BF16>(d, s);
+  if (d.dtype == KORE_DT_FP16) return dispatch_typed<F16>(d, s);
+  return set_error(KORE_EINVAL, "gemm: unsupported dtype code %d", d.dtype);
+}
+
+}  // namespace
+}  // namespace kore
+
+extern "C" int kore_gemm(int dtype, int act, const void* a, int64_t lda_m, int64_t lda_k, const void* b,
+                         int64_t ldb_k, int64_t ldb_n, const void* bias, void* c, int64_t ldc_m, int64_t M,
+                         int64_t N, int64_t K, void* stream) {
+  kore::GemmDesc d{dtype, act, a, b, bias, c, M, N, K, 1, lda_m, lda_k, ldb_k, ldb_n, ldc_m, 0, 0, 0};
+  return kore::run_gemm(d, stream);
+}
+
+extern "C" int kore_batched_gemm(int dtype, const void* a, int64_t sa_b, int64_t sa_m, int64_t sa_k, const void* b,
+                                 int64_t sb_b, int64_t sb_n, int64_t sb_k, void* c, int64_t sc_b, int64_t sc_m,
+                                 int64_t batch, int64_t M, int64_t N, int64_t K, void* stream) {
+  // C[i] = A[i] @ B[i]^T: B[i] is [N,K], i.e. the (k, n) strides are (sb_k, sb_n).
+  kore::GemmDesc d{dtype, KORE_ACT_NONE, a, b, nullptr, c, M, N, K, batch, sa_m, sa_k, sb_k, sb_n, sc_m,
+                   sa_b, sb_b, sc_b};
+  return kore::run_gemm(d, stream);
+}

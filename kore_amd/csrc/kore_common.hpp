@@ -1,0 +1,126 @@
+// Shared device/host helpers for the gfx950 (CDNA4) GEMM-family kernels.
+//
+// Lane layouts used throughout (verified on MI355X with an in-bounds probe of the
+// compiler builtins):
+//   v_mfma_f32_32x32x16_{bf16,f16}: lane l holds 8 K-consecutive values of row
+//     (l % 32) of each operand, K offset 8*(l/32); output register i of lane l is
+//     D[8*(i/4) + 4*(l/32) + (i%4)][l % 32].
+//   v_mfma_f32_32x32x64_f8f6f4 (e4m3): lane l holds 32 K-consecutive bytes of row
+//     (l % 32), K offset 32*(l/32); same output layout.
+//   v_mfma_f32_16x16x32_bf16: lane l holds 8 K values of row (l % 16) at K offset
+//     8*(l/16); output register i is D[4*(l/16) + i][l % 16].
+// Only the pairing of A and B K-slots matters for a product, and both operands are
+// always staged with the same K mapping.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kore {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// Element tags: the 16-bit float types share all staging code and differ only in
+// the MFMA opcode and the final conversion.
+struct BF16 {};
+struct F16 {};
+
+template <typename T> struct MfmaOp;
+template <> struct MfmaOp<BF16> {
+  static __device__ __forceinline__ f32x16_t mma32(u32x4_t a, u32x4_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4_t mma16(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+  // Two fp32 -> two packed bf16 (round to nearest even, overflow -> inf, NaN kept).
+  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
+    __bf16 a = (__bf16)x, b = (__bf16)y;
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  }
+  static __device__ __forceinline__ float to_f32(uint16_t v) {
+    return __builtin_bit_cast(float, (uint32_t)v << 16);
+  }
+};
+template <> struct MfmaOp<F16> {
+  static __device__ __forceinline__ f32x16_t mma32(u32x4_t a, u32x4_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4_t mma16(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
+    _Float16 a = (_Float16)x, b = (_Float16)y;
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  }
+  static __device__ __forceinline__ float to_f32(uint16_t v) {
+    return (float)__builtin_bit_cast(_Float16, v);
+  }
+};
+
+// fp8 (OCP e4m3) 32x32x64 MFMA with unit scales.  The scaled builtin with zero
+// scale operands lowers to the unscaled v_mfma_f32_32x32x64_f8f6f4 opcode.
+__device__ __forceinline__ f32x16_t mma32_fp8(i32x8_t a, i32x8_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4_t mma16_fp8(i32x8_t a, i32x8_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// Epilogue activations (fp32), KORE act codes.  gelu is the tanh approximation
+// written as x*sigmoid(2u), u = sqrt(2/pi)*(x + 0.044715 x^3), which equals
+// 0.5x(1+tanh(u)) and stays finite-safe: x -> -inf gives -0, x -> +inf gives x.
+enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2, ACT_SILU = 3, ACT_TANH = 4, ACT_SIGMOID = 5 };
+
+template <int ACT>
+__device__ __forceinline__ float apply_act(float x) {
+  if constexpr (ACT == ACT_RELU) {
+    return x < 0.0f ? 0.0f : x;  // NaN passes through like torch.relu
+  } else if constexpr (ACT == ACT_GELU) {
+    const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
+    const float u = k0 * (x + 0.044715f * x * x * x);
+    return x / (1.0f + expf(-2.0f * u));
+  } else if constexpr (ACT == ACT_SILU) {
+    return x / (1.0f + expf(-x));
+  } else if constexpr (ACT == ACT_TANH) {
+    return tanhf(x);
+  } else if constexpr (ACT == ACT_SIGMOID) {
+    return 1.0f / (1.0f + expf(-x));
+  } else {
+    return x;
+  }
+}
+
+// XOR swizzle of 16-byte chunks inside a 128-byte LDS row.  Rows r and r+8 get
+// different keys, so 8 consecutive rows (32 banks) and 16 consecutive rows split
+// by row parity (64 banks) both hit distinct banks for one chunk column.
+__device__ __forceinline__ int swz8(int r) { return (r ^ (r >> 3)) & 7; }
+
+// XCD-aware remap of a 1-D launch: workgroups are dispatched round-robin over the
+// 8 XCDs, so consecutive tile ids are handed to one XCD (one L2) when possible.
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+  if ((nblocks & 7) != 0) return bid;
+  const int per = nblocks >> 3;
+  return (bid & 7) * per + (bid >> 3);
+}
+
+__device__ __forceinline__ void lds_fence_barrier() { __syncthreads(); }
+
+}  // namespace kore
+
+// ---- host-side error plumbing (defined in status.cpp) ----
+namespace kore {
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace kore

@@ -1,0 +1,437 @@
+// Fused top-k MoE with SiLU gated MLP (bf16) for gfx950.
+//
+// Pipeline (all on the caller's stream, no host synchronisation):
+//  1. moe_align_kernel: expert histogram -> block-padded offsets -> stable,
+//     expert-sorted slot list (slot s = t*topk + k) and the expert of every
+//     BM-row block.  One workgroup; ranks come from wave ballots, so the result is
+//     deterministic and ascending in slot order inside each expert.
+//  2. moe_gateup_kernel: for every BM-row block of sorted slots (one expert e) and
+//     every 128/BN-wide column tile of the intermediate dim, A rows are the gathered
+//     tokens hidden[s/topk] and B rows are w1[e] gate and up rows interleaved so that
+//     every wave owns gate and up for the same columns; the epilogue computes
+//     h = silu(gate) * up in fp32 and writes it as two bf16 planes in sorted order,
+//     Hhi = bf16(h) and Hlo = bf16(h - Hhi), so h survives to ~2^-17 relative.
+//  3. moe_down_kernel: Y = (Hhi + Hlo)[block] @ w2[e]^T -- both planes multiply the
+//     same w2 fragments (two MFMAs per fragment, w2 streamed once); the epilogue
+//     scales each row by its router weight and writes fp32 rows Yw[slot, :] (padding
+//     slots are skipped).
+//  4. moe_combine_kernel: out[t] = bf16(sum_k Yw[t*topk + k]) in fixed k order over
+//     the slots whose id is in [0, E): no atomics, bit-reproducible.
+// Grids are sized for the worst case (every expert adds < 1 block of padding) and
+// blocks past the real end exit after reading offsets[E].
+#include "../../include/kore_amd.h"
+#include "kore_common.hpp"
+#include "tile_engine.hpp"
+
+namespace kore {
+namespace {
+
+// ------------------------------------------------------------------------------
+// 1. sort / align
+// ------------------------------------------------------------------------------
+constexpr int kAlignThreads = 1024;
+constexpr int kAlignMaxE = 1024;
+
+__global__ void __launch_bounds__(kAlignThreads)
+    moe_align_kernel(const int32_t* __restrict__ ids, int S, int E, int block, int32_t* __restrict__ offsets,
+                     int32_t* __restrict__ sorted, int32_t* __restrict__ block_expert, int cap) {
+  __shared__ int cnt[kAlignMaxE];
+  __shared__ int base[kAlignMaxE];
+  __shared__ int wcnt[kAlignThreads / 64][64];
+  __shared__ int s_total;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int NW = kAlignThreads / 64;
+  for (int e = tid; e < E; e += kAlignThreads) cnt[e] = 0;
+  __syncthreads();
+  // pass 1: histogram (integer LDS atomics: order-independent result)
+  for (int s = tid; s < S; s += kAlignThreads) {
+    const int e = ids[s];
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int e = 0; e < E; ++e) {
+      offsets[e] = run;
+      base[e] = run;
+      run += (cnt[e] + block - 1) / block * block;
+    }
+    offsets[E] = run;
+    s_total = run;
+  }
+  __syncthreads();
+  const int total = s_total;
+  // padding sentinels and block owners
+  for (int e = 0; e < E; ++e) {
+    const int beg = base[e] + cnt[e];
+    const int end = (e + 1 < E) ? base[e + 1] : total;
+    for (int i = beg + tid; i < end; i += kAlignThreads) sorted[i] = S;
+  }
+  for (int i = total + tid; i < cap; i += kAlignThreads) sorted[i] = S;
+  const int nblk = cap / block;
+  for (int b = tid; b < nblk; b += kAlignThreads) {
+    int owner = -1;
+    if (b * block < total) {
+      int lo = 0, hi = E - 1;  // last expert whose offset <= b*block
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (base[mid] <= b * block) lo = mid; else hi = mid - 1;
+      }
+      owner = lo;
+    }
+    block_expert[b] = owner;
+  }
+  // pass 2: stable placement, chunk by chunk; rank = earlier same-expert slots.
+  const unsigned long long lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int c0 = 0; c0 < S; c0 += kAlignThreads) {
+    const int s = c0 + tid;
+    const int e = (s < S) ? ids[s] : -1;
+    const bool valid = e >= 0 && e < E;
+    int rank = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      for (int e2 = e0; e2 < min(E, e0 + 64); ++e2) {
+        const unsigned long long m = __ballot(valid && e == e2);
+        if (lane == 0) wcnt[wave][e2 - e0] = __popcll(m);
+        if (valid && e == e2) rank = __popcll(m & lt_mask);
+      }
+      __syncthreads();
+      // exclusive scan over waves for experts e0 .. e0+63 (thread per expert)
+      if (tid < 64 && e0 + tid < E) {
+        int run = base[e0 + tid];
+        for (int w = 0; w < NW; ++w) {
+          const int v = wcnt[w][tid];
+          wcnt[w][tid] = run;
+          run += v;
+        }
+        base[e0 + tid] = run;
+      }
+      __syncthreads();
+      if (valid && e >= e0 && e < e0 + 64) sorted[wcnt[wave][e - e0] + rank] = s;
+      __syncthreads();
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------
+// 2/3. grouped GEMMs on the tile engine
+// ------------------------------------------------------------------------------
+struct MoeGemmParams {
+  const uint16_t* x;      // gate_up: hidden [T, D] (row stride ldx); down: H [cap, I]
+  const uint16_t* w;      // gate_up: w1 [E, 2I, D]; down: w2 [E, D, I]
+  const int32_t* offsets;
+  const int32_t* sorted;
+  const int32_t* block_expert;
+  const float* tw;        // [S] router weights (down)
+  uint16_t* h;            // H high plane [cap, I] (gate_up output / down input)
+  uint16_t* h_lo;         // H low plane [cap, I]
+  float* yw;              // down output Yw [S, D]
+  int64_t ldx;
+  int E, S, topk;
+  int K;                  // reduction length (D for gate_up, I for down)
+  int Nout;               // output columns (I for gate_up, D for down)
+  int64_t w_estride;      // elements between experts in w
+  int64_t w_rstride;      // elements between rows of w[e]
+  int max_mblocks, ntiles;
+  int abm;                // rows per aligned block of the sorted slot list
+};
+
+enum { MOE_GATEUP = 0, MOE_DOWN = 1 };
+
+template <int MODE, int BM, int BN, int WM, int WN>
+__global__ void __launch_bounds__(kEngineThreads)
+    moe_gemm_kernel(const MoeGemmParams p) {
+  using E = TileEngine<BF16, BM, BN, WM, WN, B_KC, MODE == MOE_DOWN ? 2 : 1>;
+  using Op = MfmaOp<BF16>;
+  constexpr int MI = E::MI, NI = E::NI;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int mb = bid % p.max_mblocks, nt = bid / p.max_mblocks;
+  const int total = p.offsets[p.E];
+  if (mb * BM >= total) return;  // uniform: the whole workgroup leaves
+  const int e = p.block_expert[(mb * BM) / p.abm];  // BM divides abm
+  const uint16_t* W = p.w + (int64_t)e * p.w_estride;
+  const int pos0 = mb * BM;
+
+  E eng;
+  const int ch8 = (tid & 7) * 8;
+#pragma unroll
+  for (int j = 0; j < E::LA; ++j) {
+    const int r = E::a_row_of(tid, j);
+    int64_t row;
+    if constexpr (MODE == MOE_GATEUP) {
+      const int s = p.sorted[pos0 + r];
+      row = (s < p.S) ? s / p.topk : 0;  // padding rows read token 0; never stored
+    } else {
+      row = pos0 + r;
+    }
+    eng.a_src[j] = p.x + row * p.ldx + ch8;
+    if constexpr (MODE == MOE_DOWN) eng.a2_src[j] = p.h_lo + row * p.ldx + ch8;
+  }
+  int n0;
+  if constexpr (MODE == MOE_GATEUP) {
+    // Tile covers BN/2 intermediate columns; inside each wave's WCOLS rows the first
+    // half are gate rows and the second half the matching up rows.
+    n0 = nt * (BN / 2);
+    const int I = p.Nout;
+#pragma unroll
+    for (int j = 0; j < E::LB; ++j) {
+      const int r = E::b_row_of(tid, j);
+      const int q = r / E::WCOLS, within = r % E::WCOLS;
+      const int half = within / (E::WCOLS / 2);
+      const int col = n0 + q * (E::WCOLS / 2) + within % (E::WCOLS / 2);
+      eng.b_src[j] = W + (int64_t)(half * I + col) * p.w_rstride + ch8;
+    }
+  } else {
+    n0 = nt * BN;
+#pragma unroll
+    for (int j = 0; j < E::LB; ++j) eng.b_src[j] = W + (int64_t)(n0 + E::b_row_of(tid, j)) * p.w_rstride + ch8;
+  }
+  eng.ldb = 0;
+
+  f32x16_t acc[MI][NI];
+  E::zero(acc);
+  eng.mainloop(lds, p.K, acc);
+
+  if constexpr (MODE == MOE_GATEUP) {
+    constexpr int HC = E::WCOLS / 2;  // h columns per wave
+    constexpr int NH = NI / 2;
+    using St = Stager<E::WROWS, HC>;
+    uint16_t* stg_hi = lds + wave * (2 * E::WROWS * HC);
+    uint16_t* stg_lo = stg_hi + E::WROWS * HC;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NH; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float hi[4], lo[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float gt = acc[i][j][4 * g + q], up = acc[i][j + NH][4 * g + q];
+            const float h = gt / (1.0f + expf(-gt)) * up;
+            hi[q] = Op::to_f32((uint16_t)(Op::pack2(h, 0.0f) & 0xffffu));
+            lo[q] = h - hi[q];  // exact in fp32
+          }
+          St::put(stg_hi, out_row(i, lane), out_col(j, g, lane),
+                  u32x2_t{Op::pack2(hi[0], hi[1]), Op::pack2(hi[2], hi[3])});
+          St::put(stg_lo, out_row(i, lane), out_col(j, g, lane),
+                  u32x2_t{Op::pack2(lo[0], lo[1]), Op::pack2(lo[2], lo[3])});
+        }
+    __syncthreads();
+    const int rw0 = pos0 + wm * E::WROWS, cw0 = n0 + wn * HC;
+    St::drain(stg_hi, lane, [&](int row, int col, u32x4_t v) {
+      *(u32x4_t*)(p.h + (int64_t)(rw0 + row) * p.Nout + cw0 + col) = v;
+    });
+    St::drain(stg_lo, lane, [&](int row, int col, u32x4_t v) {
+      *(u32x4_t*)(p.h_lo + (int64_t)(rw0 + row) * p.Nout + cw0 + col) = v;
+    });
+  } else {
+    // rows of this lane: pos0 + wm*WROWS + i*32 + lane%32 -> slot; fp32 16-byte stores
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int s = p.sorted[pos0 + wm * E::WROWS + out_row(i, lane)];
+      if (s >= p.S) continue;
+      const float wgt = p.tw[s];
+      float* dst = p.yw + (int64_t)s * p.Nout + n0 + wn * E::WCOLS;
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4_t v = {acc[i][j][4 * g] * wgt, acc[i][j][4 * g + 1] * wgt, acc[i][j][4 * g + 2] * wgt,
+                             acc[i][j][4 * g + 3] * wgt};
+          *(f32x4_t*)(dst + out_col(j, g, lane)) = v;
+        }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------
+// 4. combine
+// ------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+    moe_combine_kernel(const float* __restrict__ yw, const int32_t* __restrict__ ids, uint16_t* __restrict__ out,
+                       int T, int D, int topk, int E) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // one thread per 8 outputs
+  const int per_row = D / 8;
+  if (idx >= (int64_t)T * per_row) return;
+  const int t = (int)(idx / per_row), d0 = (int)(idx % per_row) * 8;
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < topk; ++k) {
+    const int e = ids[t * topk + k];
+    if (e < 0 || e >= E) continue;
+    const float* src = yw + ((int64_t)t * topk + k) * D + d0;
+    const f32x4_t a = *(const f32x4_t*)src, b = *(const f32x4_t*)(src + 4);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      s[q] += a[q];
+      s[4 + q] += b[q];
+    }
+  }
+  using Op = MfmaOp<BF16>;
+  *(u32x4_t*)(out + (int64_t)t * D + d0) =
+      u32x4_t{Op::pack2(s[0], s[1]), Op::pack2(s[2], s[3]), Op::pack2(s[4], s[5]), Op::pack2(s[6], s[7])};
+}
+
+// ------------------------------------------------------------------------------
+// host side
+// ------------------------------------------------------------------------------
+inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+
+// Worst-case padded length: every expert rounds up by < block rows.
+inline int64_t align_capacity(int64_t S, int64_t E, int64_t block) {
+  return align_up(S + E * (block - 1), block);
+}
+
+// Block size of the grouped GEMMs: skinny blocks when experts see few rows.
+inline int moe_block_rows(int64_t S, int64_t E) { return (S <= 32 * E * 2) ? 32 : 256; }
+
+struct MoeWorkspace {
+  int32_t* offsets;
+  int32_t* sorted;
+  int32_t* block_expert;
+  uint16_t* h;
+  uint16_t* h_lo;
+  float* yw;
+  size_t bytes;
+};
+
+inline MoeWorkspace carve(void* base, int64_t T, int64_t topk, int64_t E, int64_t D, int64_t I) {
+  const int64_t S = T * topk;
+  const int BM = moe_block_rows(S, E);
+  const int64_t cap = align_capacity(S, E, BM);
+  MoeWorkspace w{};
+  size_t off = 0;
+  auto take = [&](size_t n) {
+    const size_t o = off;
+    off = (size_t)align_up((int64_t)(off + n), 256);
+    return o;
+  };
+  const size_t o_off = take(sizeof(int32_t) * (E + 1));
+  const size_t o_sorted = take(sizeof(int32_t) * cap);
+  const size_t o_blk = take(sizeof(int32_t) * (cap / BM));
+  const size_t o_h = take(sizeof(uint16_t) * cap * I);
+  const size_t o_hlo = take(sizeof(uint16_t) * cap * I);
+  const size_t o_yw = take(sizeof(float) * S * D);
+  char* b = (char*)base;
+  w.offsets = (int32_t*)(b + o_off);
+  w.sorted = (int32_t*)(b + o_sorted);
+  w.block_expert = (int32_t*)(b + o_blk);
+  w.h = (uint16_t*)(b + o_h);
+  w.h_lo = (uint16_t*)(b + o_hlo);
+  w.yw = (float*)(b + o_yw);
+  w.bytes = off;
+  return w;
+}
+
+template <int MODE, int BM, int BN, int WM, int WN>
+int launch_moe_gemm(MoeGemmParams p, int64_t cap, hipStream_t st) {
+  p.ntiles = (MODE == MOE_GATEUP) ? p.Nout / (BN / 2) : p.Nout / BN;
+  p.max_mblocks = (int)(cap / BM);
+  const int64_t blocks = (int64_t)p.max_mblocks * p.ntiles;
+  if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "fused_moe: grid too large");
+  hipLaunchKernelGGL((moe_gemm_kernel<MODE, BM, BN, WM, WN>), dim3((unsigned)blocks), dim3(kEngineThreads), 0, st, p);
+  return check_launch(MODE == MOE_GATEUP ? "moe_gateup_kernel" : "moe_down_kernel");
+}
+
+}  // namespace
+}  // namespace kore
+
+extern "C" int64_t kore_moe_align_capacity(int64_t T, int64_t topk, int64_t E, int64_t block) {
+  if (T < 0 || topk <= 0 || E <= 0 || block <= 0) return -1;
+  return kore::align_capacity(T * topk, E, block);
+}
+
+extern "C" int kore_moe_align(const int32_t* topk_ids, int64_t T, int64_t topk, int64_t E, int64_t block,
+                              int32_t* offsets, int32_t* sorted_slots, int32_t* block_expert, int64_t cap,
+                              void* stream) {
+  using namespace kore;
+  if (!topk_ids || !offsets || !sorted_slots || !block_expert) return set_error(KORE_EINVAL, "moe_align: null pointer");
+  if (T < 0 || topk <= 0 || E <= 0 || block <= 0) return set_error(KORE_EINVAL, "moe_align: bad sizes");
+  if (E > kAlignMaxE) return set_error(KORE_EUNSUPPORTED, "moe_align: E > %d", kAlignMaxE);
+  if (T * topk >= (1ll << 30)) return set_error(KORE_EUNSUPPORTED, "moe_align: too many slots");
+  if (cap < align_capacity(T * topk, E, block) || cap % block != 0)
+    return set_error(KORE_EINVAL, "moe_align: cap %lld too small or not a multiple of block (need %lld)",
+                     (long long)cap, (long long)align_capacity(T * topk, E, block));
+  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, (hipStream_t)stream, topk_ids,
+                     (int)(T * topk), (int)E, (int)block, offsets, sorted_slots, block_expert, (int)cap);
+  return check_launch("moe_align_kernel");
+}
+
+extern "C" size_t kore_fused_moe_workspace_bytes(int64_t T, int64_t topk, int64_t E, int64_t D, int64_t I) {
+  if (T <= 0 || topk <= 0 || E <= 0 || D <= 0 || I <= 0) return 0;
+  return kore::carve(nullptr, T, topk, E, D, I).bytes;
+}
+
+extern "C" int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, const void* w2,
+                              const float* topk_weight, const int32_t* topk_ids, void* out, int64_t T, int64_t D,
+                              int64_t I, int64_t E, int64_t topk, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  using namespace kore;
+  if (!hidden || !w1 || !w2 || !topk_weight || !topk_ids || !out || !workspace)
+    return set_error(KORE_EINVAL, "fused_moe: null pointer");
+  if (T <= 0 || D <= 0 || I <= 0 || E <= 0 || topk <= 0) return set_error(KORE_EINVAL, "fused_moe: sizes must be >= 1");
+  if (D % 128 != 0 || I % 128 != 0)
+    return set_error(KORE_EUNSUPPORTED, "fused_moe: D and I must be multiples of 128 (D=%lld I=%lld)", (long long)D,
+                     (long long)I);
+  if (E > kAlignMaxE) return set_error(KORE_EUNSUPPORTED, "fused_moe: E > %d", kAlignMaxE);
+  if (ldh < D || ldh % 8 != 0 || ((uintptr_t)hidden & 15u) || ((uintptr_t)w1 & 15u) || ((uintptr_t)w2 & 15u) ||
+      ((uintptr_t)out & 15u))
+    return set_error(KORE_EINVAL, "fused_moe: hidden/w1/w2/out must be 16-byte aligned with ldh %% 8 == 0");
+  const int64_t S = T * topk;
+  if (S >= (1ll << 30) || 2 * I * D >= (1ll << 40)) return set_error(KORE_EUNSUPPORTED, "fused_moe: problem too large");
+  const MoeWorkspace ws = carve(workspace, T, topk, E, D, I);
+  if (workspace_bytes < ws.bytes)
+    return set_error(KORE_EWORKSPACE, "fused_moe: workspace %zu bytes < required %zu", workspace_bytes, ws.bytes);
+  hipStream_t st = (hipStream_t)stream;
+  const int BM = moe_block_rows(S, E);
+  const int64_t cap = align_capacity(S, E, BM);
+  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, st, topk_ids, (int)S, (int)E, BM, ws.offsets,
+                     ws.sorted, ws.block_expert, (int)cap);
+  int rc = check_launch("moe_align_kernel");
+  if (rc) return rc;
+
+  MoeGemmParams p{};
+  p.offsets = ws.offsets;
+  p.sorted = ws.sorted;
+  p.block_expert = ws.block_expert;
+  p.tw = topk_weight;
+  p.h = ws.h;
+  p.h_lo = ws.h_lo;
+  p.yw = ws.yw;
+  p.abm = BM;
+  p.E = (int)E;
+  p.S = (int)S;
+  p.topk = (int)topk;
+  // gate_up: x = hidden, K = D, outputs I columns of H
+  p.x = (const uint16_t*)hidden;
+  p.ldx = ldh;
+  p.w = (const uint16_t*)w1;
+  p.K = (int)D;
+  p.Nout = (int)I;
+  p.w_estride = 2 * I * D;
+  p.w_rstride = D;
+  rc = (BM == 32) ? launch_moe_gemm<MOE_GATEUP, 32, 256, 1, 4>(p, cap, st)
+                  : launch_moe_gemm<MOE_GATEUP, 256, 256, 2, 2>(p, cap, st);
+  if (rc) return rc;
+  // down: x = H, K = I, outputs D columns of Yw
+  p.x = ws.h;
+  p.ldx = I;
+  p.w = (const uint16_t*)w2;
+  p.K = (int)I;
+  p.Nout = (int)D;
+  p.w_estride = D * I;
+  p.w_rstride = I;
+  // two A planes double the A tile: prefill runs 128-row tiles (halves of a 256-row
+  // aligned block) to stay inside the 160 KiB LDS budget.
+  if (BM == 32) rc = launch_moe_gemm<MOE_DOWN, 32, 128, 1, 4>(p, cap, st);
+  else if (D % 256 == 0) rc = launch_moe_gemm<MOE_DOWN, 128, 256, 2, 2>(p, cap, st);
+  else rc = launch_moe_gemm<MOE_DOWN, 128, 128, 2, 2>(p, cap, st);
+  if (rc) return rc;
+  const int64_t threads = T * (D / 8);
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, ws.yw, topk_ids,
+                     (uint16_t*)out, (int)T, (int)D, (int)topk, (int)E);
+  return check_launch("moe_combine_kernel");
+}

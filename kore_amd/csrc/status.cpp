@@ -1,0 +1,31 @@
+// Per-thread error reporting for the C ABI.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/kore_amd.h"
+#include "kore_common.hpp"
+
+namespace kore {
+
+static thread_local char g_last_error[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(KORE_EHIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+  g_last_error[0] = '\0';
+  return KORE_OK;
+}
+
+}  // namespace kore
+
+extern "C" const char* kore_last_error(void) { return kore::g_last_error; }
+extern "C" int kore_abi_version(void) { return 100; }

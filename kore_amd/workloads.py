@@ -1,0 +1,107 @@
+"""Seeded synthetic inputs for the GEMM-family configurations.
+
+Each generator draws fp32 normals from ``torch.Generator(device).manual_seed(seed)``
+and casts/quantises them exactly as the reference's ``get_inputs`` does, in the
+layout the operator's entry takes.  With ``device="cpu"`` the draws are
+reproducible on any machine (tests copy them to the GPU); large benchmark inputs
+are drawn directly on the GPU.
+
+Configurations:
+  dense     A[M,K], B[N,K] ~ N(0,1)*0.1 bf16; entry gets b = B.t()          (C = A.B^T)
+  fused     A[M,K], W[N,K] ~ N(0,1)/sqrt(K) fp16, bias[N] ~ N(0,1)*0.1; b = W.t()
+  batched   A[B,M,K], B[B,K,N] ~ N(0,1)*0.1 bf16; entry gets b = B.transpose(1,2)
+  fp8       X[M,K], W[N,K] ~ N(0,1) fp32, quantised 1x128 / 128x128 to e4m3
+  moe       logits[T,E] ~ N(0,1) -> softmax -> top-k -> renorm; hidden ~ N(0,1) bf16;
+            W_gate, W_up [I,D], W_down [D,I] ~ N(0,1)*0.02 bf16; w1 = cat(gate, up)
+"""
+
+from __future__ import annotations
+
+import torch
+
+FP8 = torch.float8_e4m3fn
+FP8_MAX = 448.0
+BLK = 128
+
+
+def _gen(device, seed: int) -> torch.Generator:
+    return torch.Generator(device=device).manual_seed(seed)
+
+
+def dense_inputs(M: int, N: int, K: int, seed: int = 0, device="cpu", dtype=torch.bfloat16,
+                 scale: float = 0.1):
+    g = _gen(device, seed)
+    a = (torch.randn((M, K), generator=g, device=device) * scale).to(dtype)
+    bt = (torch.randn((N, K), generator=g, device=device) * scale).to(dtype)
+    return a, bt.t()
+
+
+def fused_inputs(M: int, N: int, K: int, seed: int = 0, device="cpu", dtype=torch.float16,
+                 with_bias: bool = True):
+    g = _gen(device, seed)
+    sc = 1.0 / (K ** 0.5)
+    a = (torch.randn((M, K), generator=g, device=device) * sc).to(dtype)
+    w = (torch.randn((N, K), generator=g, device=device) * sc).to(dtype)
+    bias = (torch.randn((N,), generator=g, device=device) * 0.1).to(dtype) if with_bias else None
+    return a, w.t(), bias
+
+
+def batched_inputs(B: int, M: int, N: int, K: int, seed: int = 0, device="cpu",
+                   dtype=torch.bfloat16):
+    g = _gen(device, seed)
+    a = (torch.randn((B, M, K), generator=g, device=device) * 0.1).to(dtype)
+    bm = (torch.randn((B, K, N), generator=g, device=device) * 0.1).to(dtype)
+    return a, bm.transpose(1, 2)
+
+
+def quant_1x128(x: torch.Tensor):
+    """x[M,K] fp32 -> (e4m3 [M,K], fp32 scales [M,K/128]); amax/448 with a 1e-8 floor."""
+    M, K = x.shape
+    xb = x.float().view(M, K // BLK, BLK)
+    s = xb.abs().amax(-1, keepdim=True).clamp(min=1e-8) / FP8_MAX
+    q = (xb / s).clamp(-FP8_MAX, FP8_MAX).to(FP8).view(M, K)
+    return q, s.squeeze(-1).to(torch.float32).contiguous()
+
+
+def quant_128x128(w: torch.Tensor):
+    """w[N,K] fp32 -> (e4m3 [N,K], fp32 scales [N/128,K/128])."""
+    N, K = w.shape
+    wb = w.float().view(N // BLK, BLK, K // BLK, BLK)
+    s = wb.abs().amax(dim=(1, 3), keepdim=True).clamp(min=1e-8) / FP8_MAX
+    q = (wb / s).clamp(-FP8_MAX, FP8_MAX).to(FP8).view(N, K)
+    return q, s.squeeze(1).squeeze(-1).to(torch.float32).contiguous()
+
+
+def fp8_inputs(M: int, N: int, K: int, seed: int = 0, device="cpu", scale: float = 1.0):
+    g = _gen(device, seed)
+    X = torch.randn((M, K), generator=g, device=device) * scale
+    W = torch.randn((N, K), generator=g, device=device) * scale
+    xq, xs = quant_1x128(X)
+    wq, ws = quant_128x128(W)
+    return xq, wq, xs, ws
+
+
+def route(logits: torch.Tensor, topk: int, renorm: bool = True):
+    probs = torch.softmax(logits.float(), dim=-1)
+    tw, ti = torch.topk(probs, topk, dim=-1)
+    if renorm:
+        tw = tw / tw.sum(dim=-1, keepdim=True)
+    return tw.to(torch.float32), ti.to(torch.int32)
+
+
+def moe_inputs(T: int, E: int, topk: int, D: int, I: int, seed: int = 0, device="cpu",
+               wscale: float = 0.02, router_bias: torch.Tensor | None = None):
+    """Returns (hidden[T,D], w1[E,2I,D], w2[E,D,I], topk_weight[T,topk], topk_ids[T,topk])."""
+    g = _gen(device, seed)
+    hidden = torch.randn((T, D), generator=g, device=device).to(torch.bfloat16)
+    w1 = torch.empty((E, 2 * I, D), dtype=torch.bfloat16, device=device)
+    w2 = torch.empty((E, D, I), dtype=torch.bfloat16, device=device)
+    for e in range(E):  # per expert keeps the fp32 temporaries small
+        w1[e, :I] = (torch.randn((I, D), generator=g, device=device) * wscale).to(torch.bfloat16)
+        w1[e, I:] = (torch.randn((I, D), generator=g, device=device) * wscale).to(torch.bfloat16)
+        w2[e] = (torch.randn((D, I), generator=g, device=device) * wscale).to(torch.bfloat16)
+    logits = torch.randn((T, E), generator=g, device=device)
+    if router_bias is not None:
+        logits = logits + router_bias.to(device)
+    tw, ti = route(logits, topk)
+    return hidden, w1, w2, tw, ti

@@ -1,0 +1,46 @@
+"""GPU parity: batched bf16 GEMM ``C[i] = A[i] @ B[i]^T`` vs the CPU oracle."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import kore_amd
+from kore_amd import workloads as W
+from oracle.gemm import batched_gemm_ref
+from tests.fourprong import bit_equal, pair_only, verdict
+
+pytestmark = pytest.mark.gpu
+
+
+def test_batched_config(gpu):
+    """A[64,1024,128], B[64,128,1024] ~ N(0,1)*0.1, b = B.transpose(1,2)."""
+    a, b = W.batched_inputs(64, 1024, 1024, 128, seed=0)
+    out = kore_amd.batched_gemm(a.to(gpu), b.to(gpu))
+    verdict(out, batched_gemm_ref(a, b), "batched_gemm", "bf16", "64x1024x1024x128")
+
+
+@pytest.mark.parametrize("Bn,M,N,K", [(2, 128, 128, 256), (8, 512, 512, 512), (16, 256, 256, 1024),
+                                      (4, 1024, 1024, 512), (8, 512, 513, 512)])
+@pytest.mark.parametrize("seed", range(2))
+def test_batched_task_shapes(gpu, Bn, M, N, K, seed):
+    """genv_batched_gemm_bf16 shapes (kore/tasks/vendor_ops.py:83-89) with the task's
+    [B,N,K] K-contiguous b, both scaled 1/sqrt(K) (vendor_ops.py:365-371)."""
+    g = torch.Generator().manual_seed(seed)
+    sc = 1.0 / K ** 0.5
+    a = (torch.randn((Bn, M, K), generator=g) * sc).bfloat16()
+    b = (torch.randn((Bn, N, K), generator=g) * sc).bfloat16()
+    out = kore_amd.batched_gemm(a.to(gpu), b.to(gpu))
+    ref = batched_gemm_ref(a, b)
+    verdict(out, ref, "batched_gemm", "bf16", f"B{Bn} {M}x{N}x{K}")
+    pair_only(out, ref, "bf16", f"B{Bn} {M}x{N}x{K}")
+
+
+def test_batched_metamorphic_and_determinism(gpu):
+    a, b = W.batched_inputs(12, 256, 384, 128, seed=7)
+    a, b = a.to(gpu), b.to(gpu)
+    full = kore_amd.batched_gemm(a, b)
+    perm = torch.randperm(12, generator=torch.Generator().manual_seed(1)).to(gpu)
+    permuted = kore_amd.batched_gemm(a[perm], b[perm])
+    assert bit_equal(permuted, full[perm]), "batch permutation equivariance"
+    assert bit_equal(kore_amd.batched_gemm(a, b), full), "determinism"

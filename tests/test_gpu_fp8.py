@@ -1,0 +1,66 @@
+"""GPU parity: OCP-e4m3 a8w8 block-scaled GEMM vs the CPU dequant oracle."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import kore_amd
+from kore_amd import workloads as W
+from oracle.quant import matmul_blockscale_ref, quant_128x128_fp8, quant_1x128_fp8
+from tests.fourprong import bit_equal, pair_only, verdict
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(gpu, xq, wq, xs, ws):
+    return kore_amd.gemm_a8w8_blockscale(xq.to(gpu), wq.to(gpu), xs.to(gpu), ws.to(gpu))
+
+
+@pytest.mark.parametrize("M", [2048, 512, 128, 16])
+def test_fp8_config_sweep(gpu, M):
+    """X, W ~ N(0,1), N=7168, K=4096, M in {2048, 512, 128, 16}."""
+    xq, wq, xs, ws = W.fp8_inputs(M, 7168, 4096, seed=0)
+    out = _run(gpu, xq, wq, xs, ws)
+    ref = matmul_blockscale_ref(xq, wq, xs, ws)
+    verdict(out, ref, "blockscale", "fp8", f"M={M}")
+    # |o-r| <= 1e-2 + 1e-2|r| as well as the task tolerance
+    verdict(out, ref, "blockscale_genv", "fp8", f"M={M} (1e-2)")
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 256, 256), (4095, 512, 512), (300, 384, 640)])
+@pytest.mark.parametrize("seed", range(3))
+def test_fp8_task_shapes(gpu, M, N, K, seed):
+    """gemm_fp8_a8w8_blockscale shapes incl. the non-aligned M=4095, task draw N(0,1)*0.2
+    (kore/tasks/gemm_fp8_a8w8_blockscale/reference.py:46-59)."""
+    xq, wq, xs, ws = W.fp8_inputs(M, N, K, seed=seed, scale=0.2)
+    out = _run(gpu, xq, wq, xs, ws)
+    ref = matmul_blockscale_ref(xq, wq, xs, ws)
+    verdict(out, ref, "blockscale", "fp8", f"{M}x{N}x{K} seed {seed}")
+    pair_only(out, ref, "fp8", f"{M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("regime", ["zeros", "ones", "large", "small"])
+def test_fp8_adversarial(gpu, regime):
+    """The task's authored adversarial battery (kore/tasks/vendor_ops.py:526-543)."""
+    M, N, K = 256, 512, 1024
+    val = {"zeros": 0.0, "ones": 1.0, "large": 10.0, "small": 1e-2}[regime]
+    xq, xs = quant_1x128_fp8(torch.full((M, K), val))
+    wq, ws = quant_128x128_fp8(torch.full((N, K), val))
+    out = _run(gpu, xq, wq, xs, ws)
+    verdict(out, matmul_blockscale_ref(xq, wq, xs, ws), "blockscale", "fp8", regime)
+
+
+def test_fp8_scale_invariance_and_determinism(gpu):
+    """Doubling x_scale doubles Y exactly (power-of-two scale invariance)."""
+    xq, wq, xs, ws = W.fp8_inputs(512, 1024, 1024, seed=9)
+    y1 = _run(gpu, xq, wq, xs, ws)
+    y2 = _run(gpu, xq, wq, xs * 2, ws)
+    assert bit_equal(y2, y1 * 2)
+    assert bit_equal(_run(gpu, xq, wq, xs, ws), y1)
+
+
+def test_fp8_rejects_unaligned(gpu):
+    xq, wq, xs, ws = W.fp8_inputs(64, 256, 256, seed=0)
+    with pytest.raises(ValueError):
+        kore_amd.gemm_a8w8_blockscale(xq[:, :200].to(gpu), wq[:, :200].to(gpu), xs.to(gpu), ws.to(gpu))

@@ -1,0 +1,224 @@
+"""CPU tests of the host side: roofline formulas, comparator semantics, the C ABI
+(library loads, exports every declared symbol, validates arguments without a GPU),
+and the drop-in ``kernel.py`` candidates (signatures + the reference's static scanner
+rules).
+"""
+
+from __future__ import annotations
+
+import ast
+import ctypes
+import math
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from kore_amd import roofline as R
+from oracle.compare import compare_outputs, compare_pair, snr_db, tolerance_for
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+# --------------------------------------------------------------------------- #
+# roofline: known-answer vectors restated from the reference's tests
+# (tests/test_rooflines.py:14-24, 81-85 and the MoE formula rooflines.py:235-245)
+# --------------------------------------------------------------------------- #
+def test_roofline_gemm_exact():
+    f, q = R.flops_bytes("gemm", {"M": 512, "N": 1024, "K": 2048}, "bf16")
+    assert f == 2.0 * 512 * 1024 * 2048
+    assert q == (512 * 2048 + 2048 * 1024 + 512 * 1024) * 2
+
+
+def test_roofline_fp8_bytes_mixed():
+    f, q = R.flops_bytes("gemm_fp8", {"M": 256, "N": 256, "K": 256}, "fp8_e4m3fnuz")
+    assert f == 2.0 * 256 ** 3
+    assert q == (256 * 256 + 256 * 256) * 1 + 256 * 256 * 2
+
+
+def test_roofline_batched_exact():
+    f, q = R.flops_bytes("batched_gemm", {"B": 8, "M": 128, "N": 256, "K": 512}, "bf16")
+    assert f == 2.0 * 8 * 128 * 256 * 512
+    assert q == 8 * (128 * 512 + 512 * 256 + 128 * 256) * 2
+
+
+def test_roofline_moe_and_bounds():
+    f, q = R.flops_bytes("fused_moe", {"M": 64, "E": 8, "topk": 2, "D": 4096, "I": 14336}, "bf16")
+    assert f == 64 * 2 * 6.0 * 4096 * 14336 and q == (8 * 3 * 4096 * 14336 + 2 * 64 * 4096) * 2
+    assert R.roofline("fused_moe", {"M": 64, "E": 8, "topk": 2, "D": 4096, "I": 14336}, "bf16").bound == "hbm"
+    r = R.roofline("gemm", {"M": 4096, "N": 4096, "K": 4096}, "bf16")
+    assert r.bound == "mfma" and math.isclose(r.t_min_s, 2 * 4096 ** 3 / 2.5e15)
+    r8 = R.roofline("gemm_fp8", {"M": 2048, "N": 7168, "K": 4096}, "fp8")
+    assert math.isclose(r8.t_min_s, 2 * 2048 * 7168 * 4096 / 5e15)
+
+
+def test_roofline_peak_override(monkeypatch):
+    monkeypatch.setenv("KORE_PEAK_HBM_BW", "9.9e12")
+    monkeypatch.setenv("KORE_PEAK_FP8", "6.0e15")
+    p = R.resolve_peaks()
+    assert p["hbm_bytes_per_s"] == 9.9e12 and p["fp8_flops_per_s"] == 6.0e15
+
+
+# --------------------------------------------------------------------------- #
+# comparator semantics (kore/tasks/_genops.py:906-945, kore/verify/equivalence.py:197-253)
+# --------------------------------------------------------------------------- #
+def test_snr_and_allclose_rules():
+    r = torch.tensor([1.0, 2.0, 3.0])
+    assert snr_db(r, r) == 999.0
+    assert snr_db(r, torch.zeros(3)) == -999.0
+    assert compare_outputs(r, r) == (999.0, 0.0, True)
+    inf = torch.tensor([1.0, float("inf"), float("nan")])
+    assert compare_outputs(inf, inf.clone())[2]                       # matched structure
+    assert not compare_outputs(torch.tensor([1.0, -float("inf"), float("nan")]), inf)[2]   # inf sign
+    assert not compare_outputs(torch.tensor([1.0, 5.0, float("nan")]), inf)[2]             # position
+    s, d, ok = compare_outputs(torch.tensor([1.0, 2.0, 3.02]), r)
+    assert ok and abs(d - 0.02) < 1e-6 and 40 < s < 60
+
+
+def test_four_prong_pair_rule():
+    tol = tolerance_for("bf16")
+    assert (tol.rtol, tol.atol, tol.snr_db_min) == (3e-2, 1e-2, 30.0)
+    e = torch.ones(100)
+    assert compare_pair(e, e, tol).ok and compare_pair(e, e, tol).snr_db == math.inf
+    bad = e.clone()
+    bad[3] = 1.1
+    res = compare_pair(bad, e, tol)
+    assert not res.ok and "rel-err" in res.reason
+    nanc = e.clone()
+    nanc[0] = float("nan")
+    assert not compare_pair(nanc, e, tol).ok
+    assert tolerance_for("fp32").rtol == 3e-3
+
+
+# --------------------------------------------------------------------------- #
+# C ABI: the shared library loads and exports every symbol the header declares
+# --------------------------------------------------------------------------- #
+HEADER = ROOT / "include" / "kore_amd.h"
+LIB = ROOT / "kore_amd" / "libkore_amd.so"
+
+
+def _declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(kore_\w+)\s*\(", text)))
+
+
+def test_header_declarations_are_complete():
+    names = _declared_functions()
+    assert {"kore_gemm", "kore_batched_gemm", "kore_gemm_a8w8_blockscale", "kore_moe_align",
+            "kore_fused_moe", "kore_last_error"} <= set(names)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    assert LIB.exists(), "libkore_amd.so is not built (python -m kore_amd.build)"
+    from kore_amd import _lib
+
+    return _lib.load()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [n for n in _declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    from kore_amd import _lib
+
+    assert set(_declared_functions()) == set(_lib.SIGNATURES)
+    assert lib.kore_abi_version() == 100
+
+
+def test_capi_validation_without_gpu(lib):
+    """Argument checks run before any HIP call, so they are testable on the CPU."""
+    fake = ctypes.c_void_p(256)
+    assert lib.kore_gemm(0, 0, fake, 8, 1, fake, 1, 8, None, fake, 8, 0, 8, 8, None) == 1   # M = 0
+    assert b"M, N, batch >= 1" in lib.kore_last_error()
+    assert lib.kore_gemm(0, 9, fake, 8, 1, fake, 1, 8, None, fake, 8, 8, 8, 8, None) == 1   # bad act
+    assert lib.kore_gemm(7, 0, fake, 8, 1, fake, 1, 8, None, fake, 8, 8, 8, 8, None) == 1   # bad dtype
+    assert lib.kore_gemm(0, 0, fake, 8, 1, fake, 1, 8, None, None, 8, 8, 8, 8, None) == 1   # null C
+    assert lib.kore_gemm_a8w8_blockscale(fake, 4095, fake, 4095, fake, 32, 1, fake, 32, 1, fake, 128,
+                                         16, 128, 4095, None) == 1
+    assert b"multiples of 128" in lib.kore_last_error()
+    assert lib.kore_moe_align(None, 4, 2, 8, 32, None, None, None, 64, None) == 1
+    assert lib.kore_fused_moe(fake, 64, fake, fake, fake, fake, fake, 4, 64, 100, 8, 2, fake, 1 << 30, None) == 2
+    assert lib.kore_moe_align_capacity(64, 2, 8, 32) == 384   # align_up(128 + 8*31, 32)
+    assert lib.kore_moe_align_capacity(0, 2, 8, 32) == 256
+    ws_small = lib.kore_fused_moe_workspace_bytes(64, 2, 8, 4096, 14336)
+    ws_big = lib.kore_fused_moe_workspace_bytes(4096, 2, 8, 4096, 14336)
+    assert 0 < ws_small < ws_big
+    assert lib.kore_fused_moe(fake, 4096, fake, fake, fake, fake, fake, 64, 4096, 14336, 8, 2, fake,
+                              ws_small - 1, None) == 4   # workspace too small
+
+
+# --------------------------------------------------------------------------- #
+# drop-in candidates: signatures and the reference's static scanner rules
+# (kore/reward/reward.py:70-179, restated)
+# --------------------------------------------------------------------------- #
+CAND = ROOT / "kore_amd" / "candidates"
+SCAN_RULES = [
+    r"\b(?:import|from)\s+aiter\b", r"\baiter\.",
+    r"\bimport\s+rocblas\b|\bhipblaslt\b|\brocblas\b|\bmiopen\b|\brocsolver\b|\bhipblas\b",
+    r"torch\.(matmul|mm|bmm|addmm|baddbmm|einsum|softmax|rms_norm|layer_norm|scaled_dot_product_attention)\s*\(",
+    r"torch\.(tensordot|chain_matmul|mv|inner|vdot|dot|kron)\s*\(",
+    r"[\w\)\]][^\S\n]*@=", r"torch\.nn\.functional\.\w+\s*\(",
+    r"\bF\.(scaled_dot_product_attention|linear|softmax|rms_norm|layer_norm|gelu|silu|conv\w*)\s*\(",
+    r"\b(?!tl\.)(?!triton\.)[A-Za-z_]\w*\.(?:matmul|addmm|baddbmm|einsum|scaled_dot_product_attention|softmax|"
+    r"log_softmax|gelu|silu|elu|sigmoid|layer_norm|rms_norm|group_norm|batch_norm|linear|conv\w*)\s*\(",
+    r"\b(?!tl\.)(?!triton\.)[A-Za-z_]\w*\.(?:bmm|mm)\s*\(",
+    r"\bfrom\s+torch(?:\.\w+)*\s+import\b", r"\bimport\s+torch(?:\.\w+)*\s+as\s+\w+",
+    r"getattr\s*\(\s*(?:torch|np|numpy|F|nn|aiter|__builtins__|builtins)\b",
+    r"\batexit\b|signal\.signal|\bfaulthandler\b|sys\.excepthook|def\s+__del__\b",
+    r"\.(flash_attn\w*|fused_moe|paged_attention)\s*\(",
+    r"\b(?:import\s+reference|from\s+reference\s+import)\b",
+    r"\b(?:reference|ref_program|ref_impl|matmul_ref|\w+_oracle|oracle)\s*\(",
+    r"\b(?:import\s+kore\b|from\s+kore\b|kore\.tasks)", r"\b(?:import|from)\s+(?:driver|reference)\b",
+    r"\b(?:ref_fn|baseline_fn|matmul_ref)\s*\(", r"\bimportlib\b|__import__\s*\(|\bexec\s*\(|\beval\s*\(",
+    r"\bctypes\b|\bcffi\b|\bCDLL\b|dlopen|LoadLibrary", r"(?:SNR|allclose|median_ms|wall_ms)\s*:",
+    r"\bsys\.argv\b|\bargparse\b|\bgetopt\b", r"\btime\.sleep\s*\(|\basyncio\.sleep\s*\(",
+    r"\bsubprocess\b|\bmultiprocessing\b|\bthreading\b|os\.system|os\.popen|os\.fork",
+    r"[\w\)\]][^\S\n]*@[^\S\n]*[\w\(]", r"\bsys\.modules\b", r"\bos\.environ\b|\bos\.getenv\b|\bgetenv\s*\(",
+]
+
+
+def _strip(src: str) -> str:
+    src = re.sub(r'("""|\'\'\')(?:.|\n)*?\1', "", src)
+    return "\n".join(line.split("#", 1)[0] for line in src.splitlines())
+
+
+EXPECTED_ENTRIES = {
+    "gemm_bf16": ("gemm", 2), "genv_batched_gemm_bf16": ("batched_gemm", 2),
+    "moe_batched_gemm_bf16": ("batched_gemm", 2), "gemm_fp8_a8w8_blockscale": ("gemm", 4),
+    "genv_gemm_a8w8_blockscale_fp8": ("gemm_a8w8_blockscale", 4),
+    "fused_moe_silu_bf16": ("fused_moe", 5),
+}
+
+
+@pytest.mark.parametrize("task", sorted(p.name for p in CAND.iterdir() if p.is_dir() and not p.name.startswith("_")))
+def test_candidate_passes_scanner_and_signature(task):
+    src = (CAND / task / "kernel.py").read_text()
+    code = _strip(src)
+    for pat in SCAN_RULES:
+        assert not re.search(pat, code), f"{task}: scanner rule {pat!r} fires"
+    assert not re.search(r"except\s*[\w. ,()]*:\s*(?:\n\s*)*(?:return|pass|out\s*=)", code)
+    tree = ast.parse(src)
+    funcs = {n.name: len(n.args.args) for n in tree.body if isinstance(n, ast.FunctionDef)}
+    if task in EXPECTED_ENTRIES:
+        name, arity = EXPECTED_ENTRIES[task]
+    else:  # gen_<op>_<dtype>
+        name = task[len("gen_"):].rsplit("_", 1)[0]
+        arity = 3 if "bias" in name else 2
+    assert funcs.get(name) == arity, (task, funcs)
+
+
+def test_every_fusion_op_has_candidates():
+    import kore_amd
+
+    for op in kore_amd.GEMM_FUSION_OPS:
+        for dt in ("bf16", "fp16"):
+            assert (CAND / f"gen_{op}_{dt}" / "kernel.py").exists()
+
+
+def test_ops_fail_loudly_without_device_tensors():
+    import kore_amd
+
+    a = torch.zeros((4, 8), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="HIP device"):
+        kore_amd.gemm(a, a.t())
