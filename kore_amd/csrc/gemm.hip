@@ -43,56 +43,16 @@ struct TileParams {
 
 constexpr int kGroupM = 4;
 
-template <typename T, int BL, int BM, int BN>
-__global__ void __launch_bounds__(kEngineThreads)
-    gemm_tile_kernel(const TileParams p) {
-  using E = TileEngine<T, BM, BN, 2, 2, BL>;
+// Bias + activation in fp32, RNE pack, per-wave LDS staging, 16-byte row stores.
+// Must be entered after a barrier that ends all reads of the K-loop buffers.
+template <typename T, int MI, int NI, int WROWS, int WCOLS>
+__device__ __forceinline__ void dense_epilogue(f32x16_t (&acc)[MI][NI], uint16_t* lds, const TileParams& p, int m0,
+                                               int n0, int wm, int wn, int wave, int lane, uint16_t* C) {
   using Op = MfmaOp<T>;
-  constexpr int MI = E::MI, NI = E::NI;
-  __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-
-  // ---- tile coordinates: XCD-aware remap, then grouped raster per batch ----
-  const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-  const int batch = bid / p.tiles_per_batch;
-  const int t = bid - batch * p.tiles_per_batch;
-  const int width = kGroupM * p.tiles_n;
-  const int grp = t / width;
-  const int first_m = grp * kGroupM;
-  const int gsz = min(p.tiles_m - first_m, kGroupM);
-  const int tl = t - grp * width;
-  const int m0 = (first_m + tl % gsz) * BM;
-  const int n0 = (tl / gsz) * BN;
-
-  const uint16_t* A = p.a + batch * p.sa;
-  const uint16_t* B = p.b + batch * p.sb;
-  uint16_t* C = p.c + batch * p.sc;
-  const int M = p.M, N = p.N, K = p.K;
-
-  E eng;
-  const int ch8 = (tid & 7) * 8;
-#pragma unroll
-  for (int j = 0; j < E::LA; ++j) eng.a_src[j] = A + (int64_t)min(m0 + E::a_row_of(tid, j), M - 1) * p.lda + ch8;
-  if constexpr (BL == B_KC) {
-#pragma unroll
-    for (int j = 0; j < E::LB; ++j) eng.b_src[j] = B + (int64_t)min(n0 + E::b_row_of(tid, j), N - 1) * p.ldb + ch8;
-  } else {
-#pragma unroll
-    for (int j = 0; j < E::LB; ++j)
-      eng.b_src[j] = B + (int64_t)(E::nc_kb(tid, j) * 8) * p.ldb + min(n0 + E::nc_nb(tid, j) * 8, N - 8);
-  }
-  eng.ldb = p.ldb;
-
-  f32x16_t acc[MI][NI];
-  E::zero(acc);
-  eng.mainloop(lds, K, acc);
-
-  // ---- epilogue: bias + activation in fp32, pack, stage per wave, 16-byte stores ----
-  using St = Stager<E::WROWS, E::WCOLS>;
-  uint16_t* stg = lds + wave * (E::WROWS * E::WCOLS);
-  const int mw0 = m0 + wm * E::WROWS, nw0 = n0 + wn * E::WCOLS;
+  using St = Stager<WROWS, WCOLS>;
+  const int M = p.M, N = p.N;
+  uint16_t* stg = lds + wave * (WROWS * WCOLS);
+  const int mw0 = m0 + wm * WROWS, nw0 = n0 + wn * WCOLS;
   auto epi = [&](auto act_tag) {
     constexpr int ACT = decltype(act_tag)::value;
 #pragma unroll
@@ -132,6 +92,96 @@ __global__ void __launch_bounds__(kEngineThreads)
     const int gm = mw0 + row, gn = nw0 + col;
     if (gm < M) store_row8(C + (int64_t)gm * p.ldc + gn, gn, N, vec, v);
   });
+}
+
+// Tile coordinates: XCD-aware remap, then grouped raster per batch.
+__device__ __forceinline__ void tile_coords(const TileParams& p, int BM, int BN, int& batch, int& m0, int& n0) {
+  const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  batch = bid / p.tiles_per_batch;
+  const int t = bid - batch * p.tiles_per_batch;
+  const int width = kGroupM * p.tiles_n;
+  const int grp = t / width;
+  const int first_m = grp * kGroupM;
+  const int gsz = min(p.tiles_m - first_m, kGroupM);
+  const int tl = t - grp * width;
+  m0 = (first_m + tl % gsz) * BM;
+  n0 = (tl / gsz) * BN;
+}
+
+template <typename T, int BL, int BM, int BN>
+__global__ void __launch_bounds__(kEngineThreads)
+    gemm_tile_kernel(const TileParams p) {
+  using E = TileEngine<T, BM, BN, 2, 2, BL>;
+  using Op = MfmaOp<T>;
+  constexpr int MI = E::MI, NI = E::NI;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  int batch, m0, n0;
+  tile_coords(p, BM, BN, batch, m0, n0);
+
+  const uint16_t* A = p.a + batch * p.sa;
+  const uint16_t* B = p.b + batch * p.sb;
+  uint16_t* C = p.c + batch * p.sc;
+  const int M = p.M, N = p.N, K = p.K;
+
+  E eng;
+  const int ch8 = (tid & 7) * 8;
+#pragma unroll
+  for (int j = 0; j < E::LA; ++j) eng.a_src[j] = A + (int64_t)min(m0 + E::a_row_of(tid, j), M - 1) * p.lda + ch8;
+  if constexpr (BL == B_KC) {
+#pragma unroll
+    for (int j = 0; j < E::LB; ++j) eng.b_src[j] = B + (int64_t)min(n0 + E::b_row_of(tid, j), N - 1) * p.ldb + ch8;
+  } else {
+#pragma unroll
+    for (int j = 0; j < E::LB; ++j)
+      eng.b_src[j] = B + (int64_t)(E::nc_kb(tid, j) * 8) * p.ldb + min(n0 + E::nc_nb(tid, j) * 8, N - 8);
+  }
+  eng.ldb = p.ldb;
+
+  f32x16_t acc[MI][NI];
+  E::zero(acc);
+  eng.mainloop(lds, K, acc);
+
+  dense_epilogue<T, MI, NI, E::WROWS, E::WCOLS>(acc, lds, p, m0, n0, wm, wn, wave, lane, C);
+}
+
+
+// Buffer-load pipelined variant for K-contiguous A and B (the A.B^T / A.W^T layouts)
+// with K % 64 == 0.
+template <typename T, int BM, int BN>
+__global__ void __launch_bounds__(256)
+    gemm_buf_kernel(const TileParams p) {
+  using E = BufPipeEngine<T, BM, BN>;
+  constexpr int MI = E::MI, NI = E::NI;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / E::WN, wn = wave % E::WN;
+  int batch, m0, n0;
+  tile_coords(p, BM, BN, batch, m0, n0);
+  const uint16_t* A = p.a + batch * p.sa + (int64_t)m0 * p.lda;
+  const uint16_t* B = p.b + batch * p.sb + (int64_t)n0 * p.ldb;
+  uint16_t* C = p.c + batch * p.sc;
+  const int rows_a = min(BM, p.M - m0), rows_b = min(BN, p.N - n0);
+  E eng;
+  eng.ra = make_rsrc(A, (uint32_t)(((int64_t)(rows_a - 1) * p.lda + p.K) * 2));
+  eng.rb = make_rsrc(B, (uint32_t)(((int64_t)(rows_b - 1) * p.ldb + p.K) * 2));
+#pragma unroll
+  for (int j = 0; j < E::AJ; ++j) {
+    const int r = E::a_row(wave, lane, j);
+    eng.a_voff[j] = (uint32_t)(((int64_t)min(r, rows_a - 1) * p.lda + 8 * E::chunk(r, lane)) * 2);
+  }
+#pragma unroll
+  for (int j = 0; j < E::BJ; ++j) {
+    const int r = E::b_row(wave, lane, j);
+    eng.b_voff[j] = (uint32_t)(((int64_t)min(r, rows_b - 1) * p.ldb + 8 * E::chunk(r, lane)) * 2);
+  }
+  f32x16_t acc[MI][NI];
+  E::zero(acc);
+  eng.mainloop(lds, p.K, acc);
+  dense_epilogue<T, MI, NI, E::WROWS, E::WCOLS>(acc, lds, p, m0, n0, wm, wn, wave, lane, C);
 }
 
 // ---------------------------------------------------------------------------------
@@ -245,6 +295,34 @@ int launch_tile(const GemmDesc& d, hipStream_t stream) {
   return check_launch("gemm_tile_kernel");
 }
 
+
+template <typename T, int BM, int BN>
+int launch_buf(const GemmDesc& d, hipStream_t stream) {
+  TileParams p;
+  p.a = (const uint16_t*)d.a;
+  p.b = (const uint16_t*)d.b;
+  p.bias = (const uint16_t*)d.bias;
+  p.c = (uint16_t*)d.c;
+  p.M = (int)d.M;
+  p.N = (int)d.N;
+  p.K = (int)d.K;
+  p.lda = d.sam;
+  p.ldb = d.sbn;
+  p.ldc = d.scm;
+  p.sa = d.sa;
+  p.sb = d.sb;
+  p.sc = d.sc;
+  p.tiles_m = (int)((d.M + BM - 1) / BM);
+  p.tiles_n = (int)((d.N + BN - 1) / BN);
+  p.tiles_per_batch = p.tiles_m * p.tiles_n;
+  p.act = d.act;
+  p.vec_store = (d.scm % 8 == 0) && aligned16(d.c) && (d.sc % 8 == 0);
+  const int64_t blocks = (int64_t)p.tiles_per_batch * d.batch;
+  if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "gemm: grid too large");
+  hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+  return check_launch("gemm_buf_kernel");
+}
+
 template <typename T>
 int launch_generic(const GemmDesc& d, hipStream_t stream) {
   GenericParams p;
@@ -282,6 +360,10 @@ int dispatch_typed(const GemmDesc& d, hipStream_t stream) {
     // Macro tile: 256x256 when it still gives >= ~1 wave of tiles, else 128x128.
     const int64_t big_tiles = ((d.M + 255) / 256) * ((d.N + 255) / 256) * d.batch;
     const bool big = big_tiles >= 192;
+    // Buffer-load engine: each operand tile must span < 4 GiB of bytes.
+    const bool buf_ok = d.K % 64 == 0 && d.sam * 2 * 256 + d.K * 2 < (1ll << 31) &&
+                        d.sbn * 2 * 256 + d.K * 2 < (1ll << 31);
+    if (b_kc && big && buf_ok) return launch_buf<T, 256, 256>(d, stream);
     if (b_kc) return big ? launch_tile<T, B_KC, 256, 256>(d, stream) : launch_tile<T, B_KC, 128, 128>(d, stream);
     return big ? launch_tile<T, B_NC, 256, 256>(d, stream) : launch_tile<T, B_NC, 128, 128>(d, stream);
   }
