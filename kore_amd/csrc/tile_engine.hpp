@@ -876,7 +876,8 @@ struct BufPipeEngine {
   // K must be a multiple of 64.
   __device__ __forceinline__ void mainloop(uint16_t* lds, int K, f32x16_t (&acc)[MI][NI]) {
     using Op = MfmaOp<T>;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // wave index as a scalar so LDS destinations (M0) are pure scalar arithmetic
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
     const int lr = lane & 31, hh = lane >> 5;
     int offA[2][4], offB[2][4];
@@ -900,6 +901,14 @@ struct BufPipeEngine {
 #pragma unroll
       for (int j = 0; j < NI; ++j) bf[j] = *(const u32x4_t*)(sB + j * 32 * kBK + offB[j & 1][ks]);
     };
+    auto read_one = [&](int slot, int ks, int f, u32x4_t (&af)[MI], u32x4_t (&bf)[NI]) {
+      if (f < MI) {
+        af[f] = *(const u32x4_t*)(lds + slot * STAGE + rowA0 * kBK + f * 32 * kBK + offA[f & 1][ks]);
+      } else {
+        const int j = f - MI;
+        bf[j] = *(const u32x4_t*)(lds + slot * STAGE + A_ELEMS + rowB0 * kBK + j * 32 * kBK + offB[j & 1][ks]);
+      }
+    };
     const int nk = K / kBK;
     if (nk == 0) return;
     constexpr int HALF = LPS / 2;
@@ -920,31 +929,40 @@ struct BufPipeEngine {
     exec_barrier();
     u32x4_t fa[2][MI], fb[2][NI];
     read(0, 0, fa[0], fb[0]);
+    // Per sub-step the instruction order is pinned: the next sub-step's fragment
+    // reads (and, in sub-steps 0 and 3, half a stage of direct loads) are interleaved
+    // one per MFMA over the first half of the MFMAs, so LDS latency is covered by
+    // the second half.
+    constexpr int NRD = MI + NI;  // fragment reads per sub-step
+    static_assert(NRD <= NMMA && HALF <= NMMA, "interleave needs enough MFMAs");
     for (int s = 0; s < nk; ++s) {
       const int slot = s & 1;
       const uint32_t soff1 = soff_of(s + 1), soff2 = soff_of(s + 2);
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const int c = ks & 1;
-        if (ks < 3) {
-          read(slot, ks + 1, fa[c ^ 1], fb[c ^ 1]);
-        } else {
+        if (ks == 3) {
           asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
           wait_vmcnt<0>();
           exec_barrier();
-          read(slot ^ 1, 0, fa[c ^ 1], fb[c ^ 1]);  // stage s+1 (re-read of s at the end: unused)
         }
+        // MFMA m, then (m < NRD) one fragment read of the next sub-step, then
+        // (sub-steps 0 and 3, m < HALF) one direct load; hard scheduling fences keep
+        // this order.
+        const int rslot = ks < 3 ? slot : (slot ^ 1);
+        const int rks = ks < 3 ? ks + 1 : 0;
 #pragma unroll
         for (int m = 0; m < NMMA; ++m) {
-          if ((ks == 0 || ks == 3) && m % EVERY == 0 && m / EVERY < HALF) {
-            __builtin_amdgcn_sched_barrier(0);
-            if (ks == 0) issue_one(lds, slot ^ 1, soff1, wave, HALF + m / EVERY);  // 2nd half of s+1
-            else issue_one(lds, slot, soff2, wave, m / EVERY);                      // 1st half of s+2
-            __builtin_amdgcn_sched_barrier(0);
-          }
+          __builtin_amdgcn_sched_barrier(0);
           const int i = m / NI, j = m % NI;
           acc[i][j] = Op::mma32(fb[c][j], fa[c][i], acc[i][j]);
+          if (m < NRD) read_one(rslot, rks, m, fa[c ^ 1], fb[c ^ 1]);
+          if (m < HALF) {
+            if (ks == 0) issue_one(lds, slot ^ 1, soff1, wave, HALF + m);  // 2nd half of s+1
+            else if (ks == 3) issue_one(lds, slot, soff2, wave, m);       // 1st half of s+2
+          }
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     wait_vmcnt<0>();  // drain the clamped trailing loads before LDS is reused
