@@ -39,6 +39,7 @@ struct TileParams {
   int tiles_m, tiles_n, tiles_per_batch;
   int act;
   int vec_store;  // 16-byte C stores allowed (ldc % 8 == 0, aligned)
+  int bias_vec;   // bias is 8-byte aligned: 4-wide bias loads allowed
 };
 
 constexpr int kGroupM = 4;
@@ -62,10 +63,16 @@ __device__ __forceinline__ void dense_epilogue(f32x16_t (&acc)[MI][NI], uint16_t
         const int nl = out_col(j, g, lane);
         float bv[4] = {0.f, 0.f, 0.f, 0.f};
         if (p.bias != nullptr) {
+          const int n = nw0 + nl;
+          if (p.bias_vec && n + 4 <= N) {  // 4 consecutive bias values in one 8-byte load
+            const u32x2_t w = *(const u32x2_t*)(p.bias + n);
+            bv[0] = Op::to_f32((uint16_t)(w[0] & 0xffffu));
+            bv[1] = Op::to_f32((uint16_t)(w[0] >> 16));
+            bv[2] = Op::to_f32((uint16_t)(w[1] & 0xffffu));
+            bv[3] = Op::to_f32((uint16_t)(w[1] >> 16));
+          } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int n = nw0 + nl + e;
-            bv[e] = n < N ? Op::to_f32(p.bias[n]) : 0.0f;
+            for (int e = 0; e < 4; ++e) bv[e] = n + e < N ? Op::to_f32(p.bias[n + e]) : 0.0f;
           }
         }
 #pragma unroll
@@ -289,6 +296,7 @@ int launch_tile(const GemmDesc& d, hipStream_t stream) {
   p.tiles_per_batch = p.tiles_m * p.tiles_n;
   p.act = d.act;
   p.vec_store = (d.scm % 8 == 0) && aligned16(d.c) && (d.sc % 8 == 0);
+  p.bias_vec = d.bias != nullptr && ((uintptr_t)d.bias & 7u) == 0;
   const int64_t blocks = (int64_t)p.tiles_per_batch * d.batch;
   if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "gemm: grid too large");
   hipLaunchKernelGGL((gemm_tile_kernel<T, BL, BM, BN>), dim3((unsigned)blocks), dim3(kEngineThreads), 0, stream, p);
@@ -317,6 +325,7 @@ int launch_buf(const GemmDesc& d, hipStream_t stream) {
   p.tiles_per_batch = p.tiles_m * p.tiles_n;
   p.act = d.act;
   p.vec_store = (d.scm % 8 == 0) && aligned16(d.c) && (d.sc % 8 == 0);
+  p.bias_vec = d.bias != nullptr && ((uintptr_t)d.bias & 7u) == 0;
   const int64_t blocks = (int64_t)p.tiles_per_batch * d.batch;
   if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "gemm: grid too large");
   hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN>), dim3((unsigned)blocks), dim3(256), 0, stream, p);

@@ -78,25 +78,35 @@ __device__ __forceinline__ f32x4_t mma16_fp8(i32x8_t a, i32x8_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
-// Epilogue activations (fp32), KORE act codes.  gelu is the tanh approximation
-// written as x*sigmoid(2u), u = sqrt(2/pi)*(x + 0.044715 x^3), which equals
-// 0.5x(1+tanh(u)) and stays finite-safe: x -> -inf gives -0, x -> +inf gives x.
+// Epilogue activations (fp32), KORE act codes, built on the hardware exp2 and
+// reciprocal (v_exp_f32 / v_rcp_f32, ~1 ulp): e^x = 2^(x*log2(e)).
+//   sigmoid(x) = 1 / (1 + e^-x)
+//   silu(x)    = x * sigmoid(x)
+//   gelu(x)    = x * sigmoid(2u), u = sqrt(2/pi)*(x + 0.044715 x^3), which equals
+//                0.5x(1 + tanh(u)) (tanh approximation of GELU)
+//   tanh(x)    = 2 * sigmoid(2x) - 1
+// Saturation is exact: e^-x -> inf gives rcp(inf) = 0, e^-x -> 0 gives 1, so
+// gelu(-inf-like) = -0, gelu(+large) = x and no NaN appears for finite x.
 enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2, ACT_SILU = 3, ACT_TANH = 4, ACT_SIGMOID = 5 };
+
+__device__ __forceinline__ float fast_sigmoid(float x) {
+  const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);
+  return __builtin_amdgcn_rcpf(1.0f + e);
+}
 
 template <int ACT>
 __device__ __forceinline__ float apply_act(float x) {
   if constexpr (ACT == ACT_RELU) {
     return x < 0.0f ? 0.0f : x;  // NaN passes through like torch.relu
   } else if constexpr (ACT == ACT_GELU) {
-    const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
-    const float u = k0 * (x + 0.044715f * x * x * x);
-    return x / (1.0f + expf(-2.0f * u));
+    const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+    return x * fast_sigmoid(2.0f * u);
   } else if constexpr (ACT == ACT_SILU) {
-    return x / (1.0f + expf(-x));
+    return x * fast_sigmoid(x);
   } else if constexpr (ACT == ACT_TANH) {
-    return tanhf(x);
+    return 2.0f * fast_sigmoid(2.0f * x) - 1.0f;
   } else if constexpr (ACT == ACT_SIGMOID) {
-    return 1.0f / (1.0f + expf(-x));
+    return fast_sigmoid(x);
   } else {
     return x;
   }

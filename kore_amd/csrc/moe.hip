@@ -126,7 +126,7 @@ struct MoeGemmParams {
   uint16_t* h_lo;         // H low plane [cap, I]
   float* yw;              // down output Yw [S, D]
   int64_t ldx;
-  int E, S, topk;
+  int E, S, topk, T;
   int K;                  // reduction length (D for gate_up, I for down)
   int Nout;               // output columns (I for gate_up, D for down)
   int64_t w_estride;      // elements between experts in w
@@ -136,6 +136,63 @@ struct MoeGemmParams {
 };
 
 enum { MOE_GATEUP = 0, MOE_DOWN = 1 };
+
+template <int MODE, int MI, int NI, int WROWS, int WCOLS>
+__device__ __forceinline__ void moe_epilogue(f32x16_t (&acc)[MI][NI], uint16_t* lds, const MoeGemmParams& p, int pos0,
+                                             int n0, int wm, int wn, int wave, int lane) {
+  using Op = MfmaOp<BF16>;
+  if constexpr (MODE == MOE_GATEUP) {
+    constexpr int HC = WCOLS / 2;  // h columns per wave
+    constexpr int NH = NI / 2;
+    using St = Stager<WROWS, HC>;
+    uint16_t* stg_hi = lds + wave * (2 * WROWS * HC);
+    uint16_t* stg_lo = stg_hi + WROWS * HC;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NH; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float hi[4], lo[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float gt = acc[i][j][4 * g + q], up = acc[i][j + NH][4 * g + q];
+            const float h = gt * fast_sigmoid(gt) * up;
+            hi[q] = Op::to_f32((uint16_t)(Op::pack2(h, 0.0f) & 0xffffu));
+            lo[q] = h - hi[q];  // exact in fp32
+          }
+          St::put(stg_hi, out_row(i, lane), out_col(j, g, lane),
+                  u32x2_t{Op::pack2(hi[0], hi[1]), Op::pack2(hi[2], hi[3])});
+          St::put(stg_lo, out_row(i, lane), out_col(j, g, lane),
+                  u32x2_t{Op::pack2(lo[0], lo[1]), Op::pack2(lo[2], lo[3])});
+        }
+    __syncthreads();
+    const int rw0 = pos0 + wm * WROWS, cw0 = n0 + wn * HC;
+    St::drain(stg_hi, lane, [&](int row, int col, u32x4_t v) {
+      *(u32x4_t*)(p.h + (int64_t)(rw0 + row) * p.Nout + cw0 + col) = v;
+    });
+    St::drain(stg_lo, lane, [&](int row, int col, u32x4_t v) {
+      *(u32x4_t*)(p.h_lo + (int64_t)(rw0 + row) * p.Nout + cw0 + col) = v;
+    });
+  } else {
+    // rows of this lane: pos0 + wm*WROWS + i*32 + lane%32 -> slot; fp32 16-byte stores
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int s = p.sorted[pos0 + wm * WROWS + out_row(i, lane)];
+      if (s >= p.S) continue;
+      const float wgt = p.tw[s];
+      float* dst = p.yw + (int64_t)s * p.Nout + n0 + wn * WCOLS;
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4_t v = {acc[i][j][4 * g] * wgt, acc[i][j][4 * g + 1] * wgt, acc[i][j][4 * g + 2] * wgt,
+                             acc[i][j][4 * g + 3] * wgt};
+          *(f32x4_t*)(dst + out_col(j, g, lane)) = v;
+        }
+    }
+  }
+}
 
 template <int MODE, int BM, int BN, int WM, int WN>
 __global__ void __launch_bounds__(kEngineThreads)
@@ -195,57 +252,77 @@ __global__ void __launch_bounds__(kEngineThreads)
   E::zero(acc);
   eng.mainloop(lds, p.K, acc);
 
+  moe_epilogue<MODE, MI, NI, E::WROWS, E::WCOLS>(acc, lds, p, pos0, n0, wm, wn, wave, lane);
+}
+
+
+// Prefill path on the buffer-load pipelined engine: A rows (gathered tokens for
+// gate_up, H planes for down) and B rows (interleaved gate/up rows of w1[e], rows of
+// w2[e]) become per-lane byte offsets of buffer resources, fixed for the whole K loop.
+template <int MODE, int BM, int BN>
+__global__ void __launch_bounds__(256)
+    moe_buf_kernel(const MoeGemmParams p) {
+  constexpr int AP = (MODE == MOE_DOWN) ? 2 : 1;
+  using E = BufPipeEngine<BF16, BM, BN, 2, 2, AP>;
+  using Op = MfmaOp<BF16>;
+  constexpr int MI = E::MI, NI = E::NI;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / E::WN, wn = wave % E::WN;
+
+  const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int mb = bid % p.max_mblocks, nt = bid / p.max_mblocks;
+  const int total = p.offsets[p.E];
+  if (mb * BM >= total) return;  // uniform: the whole workgroup leaves
+  const int e = p.block_expert[(mb * BM) / p.abm];
+  const int pos0 = mb * BM;
+
+  E eng;
+  int n0;
   if constexpr (MODE == MOE_GATEUP) {
-    constexpr int HC = E::WCOLS / 2;  // h columns per wave
-    constexpr int NH = NI / 2;
-    using St = Stager<E::WROWS, HC>;
-    uint16_t* stg_hi = lds + wave * (2 * E::WROWS * HC);
-    uint16_t* stg_lo = stg_hi + E::WROWS * HC;
+    eng.ra = make_rsrc(p.x, (uint32_t)((int64_t)p.T * p.ldx * 2));
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
+    for (int j = 0; j < E::AJ; ++j) {
+      const int r = E::a_row(wave, lane, j);
+      const int sl = p.sorted[pos0 + r];
+      const int64_t row = (sl < p.S) ? sl / p.topk : 0;  // padding rows read token 0; never stored
+      eng.a_voff[j] = (uint32_t)((row * p.ldx + 8 * E::chunk(r, lane)) * 2);
+    }
+    n0 = nt * (BN / 2);
+    const int I = p.Nout;
+    const uint16_t* W = p.w + (int64_t)e * p.w_estride;
+    eng.rb = make_rsrc(W, (uint32_t)((int64_t)2 * I * p.w_rstride * 2));
 #pragma unroll
-      for (int j = 0; j < NH; ++j)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          float hi[4], lo[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float gt = acc[i][j][4 * g + q], up = acc[i][j + NH][4 * g + q];
-            const float h = gt / (1.0f + expf(-gt)) * up;
-            hi[q] = Op::to_f32((uint16_t)(Op::pack2(h, 0.0f) & 0xffffu));
-            lo[q] = h - hi[q];  // exact in fp32
-          }
-          St::put(stg_hi, out_row(i, lane), out_col(j, g, lane),
-                  u32x2_t{Op::pack2(hi[0], hi[1]), Op::pack2(hi[2], hi[3])});
-          St::put(stg_lo, out_row(i, lane), out_col(j, g, lane),
-                  u32x2_t{Op::pack2(lo[0], lo[1]), Op::pack2(lo[2], lo[3])});
-        }
-    __syncthreads();
-    const int rw0 = pos0 + wm * E::WROWS, cw0 = n0 + wn * HC;
-    St::drain(stg_hi, lane, [&](int row, int col, u32x4_t v) {
-      *(u32x4_t*)(p.h + (int64_t)(rw0 + row) * p.Nout + cw0 + col) = v;
-    });
-    St::drain(stg_lo, lane, [&](int row, int col, u32x4_t v) {
-      *(u32x4_t*)(p.h_lo + (int64_t)(rw0 + row) * p.Nout + cw0 + col) = v;
-    });
+    for (int j = 0; j < E::BJ; ++j) {
+      const int r = E::b_row(wave, lane, j);
+      const int q = r / E::WCOLS, within = r % E::WCOLS;
+      const int half = within / (E::WCOLS / 2);
+      const int col = n0 + q * (E::WCOLS / 2) + within % (E::WCOLS / 2);
+      eng.b_voff[j] = (uint32_t)(((int64_t)(half * I + col) * p.w_rstride + 8 * E::chunk(r, lane)) * 2);
+    }
   } else {
-    // rows of this lane: pos0 + wm*WROWS + i*32 + lane%32 -> slot; fp32 16-byte stores
+    const int64_t tile_bytes = (int64_t)BM * p.ldx * 2;
+    eng.ra = make_rsrc(p.x + (int64_t)pos0 * p.ldx, (uint32_t)tile_bytes);
+    eng.ra2 = make_rsrc(p.h_lo + (int64_t)pos0 * p.ldx, (uint32_t)tile_bytes);
 #pragma unroll
-    for (int i = 0; i < MI; ++i) {
-      const int s = p.sorted[pos0 + wm * E::WROWS + out_row(i, lane)];
-      if (s >= p.S) continue;
-      const float wgt = p.tw[s];
-      float* dst = p.yw + (int64_t)s * p.Nout + n0 + wn * E::WCOLS;
+    for (int j = 0; j < E::AJ; ++j) {
+      const int r = E::a_row(wave, lane, j);
+      eng.a_voff[j] = (uint32_t)(((int64_t)r * p.ldx + 8 * E::chunk(r, lane)) * 2);
+    }
+    n0 = nt * BN;
+    const uint16_t* W = p.w + (int64_t)e * p.w_estride + (int64_t)n0 * p.w_rstride;
+    eng.rb = make_rsrc(W, (uint32_t)((int64_t)BN * p.w_rstride * 2));
 #pragma unroll
-      for (int j = 0; j < NI; ++j)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4_t v = {acc[i][j][4 * g] * wgt, acc[i][j][4 * g + 1] * wgt, acc[i][j][4 * g + 2] * wgt,
-                             acc[i][j][4 * g + 3] * wgt};
-          *(f32x4_t*)(dst + out_col(j, g, lane)) = v;
-        }
+    for (int j = 0; j < E::BJ; ++j) {
+      const int r = E::b_row(wave, lane, j);
+      eng.b_voff[j] = (uint32_t)(((int64_t)r * p.w_rstride + 8 * E::chunk(r, lane)) * 2);
     }
   }
+
+  f32x16_t acc[MI][NI];
+  E::zero(acc);
+  eng.mainloop(lds, p.K, acc);
+  moe_epilogue<MODE, MI, NI, E::WROWS, E::WCOLS>(acc, lds, p, pos0, n0, wm, wn, wave, lane);
 }
 
 // ------------------------------------------------------------------------------
@@ -336,6 +413,17 @@ int launch_moe_gemm(MoeGemmParams p, int64_t cap, hipStream_t st) {
   return check_launch(MODE == MOE_GATEUP ? "moe_gateup_kernel" : "moe_down_kernel");
 }
 
+
+template <int MODE, int BM, int BN>
+int launch_moe_buf(MoeGemmParams p, int64_t cap, hipStream_t st) {
+  p.ntiles = (MODE == MOE_GATEUP) ? p.Nout / (BN / 2) : p.Nout / BN;
+  p.max_mblocks = (int)(cap / BM);
+  const int64_t blocks = (int64_t)p.max_mblocks * p.ntiles;
+  if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "fused_moe: grid too large");
+  hipLaunchKernelGGL((moe_buf_kernel<MODE, BM, BN>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+  return check_launch(MODE == MOE_GATEUP ? "moe_gateup_buf_kernel" : "moe_down_buf_kernel");
+}
+
 }  // namespace
 }  // namespace kore
 
@@ -403,6 +491,7 @@ extern "C" int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, c
   p.yw = ws.yw;
   p.abm = BM;
   p.E = (int)E;
+  p.T = (int)T;
   p.S = (int)S;
   p.topk = (int)topk;
   // gate_up: x = hidden, K = D, outputs I columns of H
@@ -413,7 +502,10 @@ extern "C" int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, c
   p.Nout = (int)I;
   p.w_estride = 2 * I * D;
   p.w_rstride = D;
+  // buffer-load engine needs operand byte ranges below 4 GiB and K % 64 == 0
+  const bool buf_ok = T * ldh * 2 < (1ll << 32) && 2 * I * D * 2 < (1ll << 32) && D % 64 == 0 && I % 64 == 0;
   rc = (BM == 32) ? launch_moe_gemm<MOE_GATEUP, 32, 256, 1, 4>(p, cap, st)
+       : buf_ok   ? launch_moe_buf<MOE_GATEUP, 256, 256>(p, cap, st)
                   : launch_moe_gemm<MOE_GATEUP, 256, 256, 2, 2>(p, cap, st);
   if (rc) return rc;
   // down: x = H, K = I, outputs D columns of Yw
@@ -427,6 +519,7 @@ extern "C" int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, c
   // two A planes double the A tile: prefill runs 128-row tiles (halves of a 256-row
   // aligned block) to stay inside the 160 KiB LDS budget.
   if (BM == 32) rc = launch_moe_gemm<MOE_DOWN, 32, 128, 1, 4>(p, cap, st);
+  else if (buf_ok && D % 256 == 0) rc = launch_moe_buf<MOE_DOWN, 128, 256>(p, cap, st);
   else if (D % 256 == 0) rc = launch_moe_gemm<MOE_DOWN, 128, 256, 2, 2>(p, cap, st);
   else rc = launch_moe_gemm<MOE_DOWN, 128, 128, 2, 2>(p, cap, st);
   if (rc) return rc;

@@ -833,38 +833,46 @@ __device__ __forceinline__ void buf_lds16(__amdgpu_buffer_rsrc_t r, uint32_t vof
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_dst, 16, (int)voff, (int)soff, 0, 0);
 }
 
-template <typename T, int BM, int BN>
+template <typename T, int BM, int BN, int WM_ = 2, int WN_ = 2, int AP = 1>
 struct BufPipeEngine {
-  static constexpr int WM = 2, WN = 2, NW = 4;
+  static constexpr int WM = WM_, WN = WN_, NW = WM * WN;
+  static_assert(NW == 4, "4 waves");
+  static_assert(AP == 1 || AP == 2, "one or two A planes");
   static constexpr int WROWS = BM / WM, WCOLS = BN / WN;
   static constexpr int MI = WROWS / 32, NI = WCOLS / 32;
   static_assert(WROWS % 32 == 0 && WCOLS % 32 == 0 && MI >= 1 && NI >= 1, "wave tile");
   static constexpr int A_ELEMS = BM * kBK, B_ELEMS = BN * kBK;
-  static constexpr int STAGE = A_ELEMS + B_ELEMS;
+  static constexpr int B_OFF = AP * A_ELEMS;
+  static constexpr int STAGE = AP * A_ELEMS + B_ELEMS;
   static constexpr int LDS_ELEMS = 2 * STAGE;
   static constexpr int AJ = BM / 8 / NW, BJ = BN / 8 / NW;
   static_assert(AJ * 8 * NW == BM && BJ * 8 * NW == BN, "8-row wave loads must cover the tile");
-  static constexpr int LPS = AJ + BJ;
+  static constexpr int LPS = AP * AJ + BJ;
+  static_assert(LPS % 2 == 0, "loads of a stage are issued in two equal halves");
 
   static __device__ __forceinline__ int a_row(int wave, int lane, int j) { return (wave + NW * j) * 8 + (lane >> 3); }
   static __device__ __forceinline__ int b_row(int wave, int lane, int j) { return (wave + NW * j) * 8 + (lane >> 3); }
   // Logical 16-byte chunk lane `lane` fetches for `row` (element offset 8 * chunk).
   static __device__ __forceinline__ int chunk(int row, int lane) { return (lane & 7) ^ swz8(row); }
 
-  __amdgpu_buffer_rsrc_t ra, rb;
-  uint32_t a_voff[AJ], b_voff[BJ];  // bytes: row * row_stride + 16 * chunk
+  __amdgpu_buffer_rsrc_t ra, ra2, rb;  // ra2: second A plane (same offsets), AP == 2
+  uint32_t a_voff[AJ], b_voff[BJ];      // bytes: row * row_stride + 16 * chunk
 
   __device__ __forceinline__ void issue_one(uint16_t* lds, int slot, uint32_t soff, int wave, int q) {
     uint16_t* sA = lds + slot * STAGE;
     if (q < AJ) {
       buf_lds16(ra, a_voff[q], soff, sA + (wave + NW * q) * 8 * kBK);
-    } else {
+    } else if (AP == 2 && q < 2 * AJ) {
       const int j = q - AJ;
-      buf_lds16(rb, b_voff[j], soff, sA + A_ELEMS + (wave + NW * j) * 8 * kBK);
+      buf_lds16(ra2, a_voff[j], soff, sA + A_ELEMS + (wave + NW * j) * 8 * kBK);
+    } else {
+      const int j = q - AP * AJ;
+      buf_lds16(rb, b_voff[j], soff, sA + B_OFF + (wave + NW * j) * 8 * kBK);
     }
   }
 
   static __device__ __forceinline__ void zero(f32x16_t (&acc)[MI][NI]) {
+    static_assert(MI >= 1, "");
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -893,26 +901,24 @@ struct BufPipeEngine {
       }
     }
     const int rowA0 = wm * WROWS, rowB0 = wn * WCOLS;
-    auto read = [&](int slot, int ks, u32x4_t (&af)[MI], u32x4_t (&bf)[NI]) {
-      const uint16_t* sA = lds + slot * STAGE + rowA0 * kBK;
-      const uint16_t* sB = lds + slot * STAGE + A_ELEMS + rowB0 * kBK;
-#pragma unroll
-      for (int i = 0; i < MI; ++i) af[i] = *(const u32x4_t*)(sA + i * 32 * kBK + offA[i & 1][ks]);
-#pragma unroll
-      for (int j = 0; j < NI; ++j) bf[j] = *(const u32x4_t*)(sB + j * 32 * kBK + offB[j & 1][ks]);
-    };
-    auto read_one = [&](int slot, int ks, int f, u32x4_t (&af)[MI], u32x4_t (&bf)[NI]) {
-      if (f < MI) {
-        af[f] = *(const u32x4_t*)(lds + slot * STAGE + rowA0 * kBK + f * 32 * kBK + offA[f & 1][ks]);
+    // Fragment f of a sub-step: f < AP*MI -> A plane f/MI block f%MI, else B block.
+    auto read_one = [&](int slot, int ks, int f, u32x4_t (&af)[AP * MI], u32x4_t (&bf)[NI]) {
+      if (f < AP * MI) {
+        const int pl = f / MI, i = f % MI;
+        af[f] = *(const u32x4_t*)(lds + slot * STAGE + pl * A_ELEMS + rowA0 * kBK + i * 32 * kBK + offA[i & 1][ks]);
       } else {
-        const int j = f - MI;
-        bf[j] = *(const u32x4_t*)(lds + slot * STAGE + A_ELEMS + rowB0 * kBK + j * 32 * kBK + offB[j & 1][ks]);
+        const int j = f - AP * MI;
+        bf[j] = *(const u32x4_t*)(lds + slot * STAGE + B_OFF + rowB0 * kBK + j * 32 * kBK + offB[j & 1][ks]);
       }
+    };
+    auto read = [&](int slot, int ks, u32x4_t (&af)[AP * MI], u32x4_t (&bf)[NI]) {
+#pragma unroll
+      for (int f = 0; f < AP * MI + NI; ++f) read_one(slot, ks, f, af, bf);
     };
     const int nk = K / kBK;
     if (nk == 0) return;
     constexpr int HALF = LPS / 2;
-    constexpr int NMMA = MI * NI;
+    constexpr int NMMA = AP * MI * NI;  // MFMAs per sub-step
     constexpr int EVERY = NMMA / HALF > 0 ? NMMA / HALF : 1;  // MFMAs per load inside a sub-step
     static_assert(HALF * EVERY <= NMMA, "a half stage of loads must fit in one sub-step");
     // Loads of a stage go out in two halves: the first right after the barrier that
@@ -927,13 +933,13 @@ struct BufPipeEngine {
     for (int q = 0; q < HALF; ++q) issue_one(lds, 1, soff_of(1), wave, q);
     wait_vmcnt<HALF>();
     exec_barrier();
-    u32x4_t fa[2][MI], fb[2][NI];
+    u32x4_t fa[2][AP * MI], fb[2][NI];
     read(0, 0, fa[0], fb[0]);
     // Per sub-step the instruction order is pinned: the next sub-step's fragment
     // reads (and, in sub-steps 0 and 3, half a stage of direct loads) are interleaved
     // one per MFMA over the first half of the MFMAs, so LDS latency is covered by
     // the second half.
-    constexpr int NRD = MI + NI;  // fragment reads per sub-step
+    constexpr int NRD = AP * MI + NI;  // fragment reads per sub-step
     static_assert(NRD <= NMMA && HALF <= NMMA, "interleave needs enough MFMAs");
     for (int s = 0; s < nk; ++s) {
       const int slot = s & 1;
@@ -954,8 +960,8 @@ struct BufPipeEngine {
 #pragma unroll
         for (int m = 0; m < NMMA; ++m) {
           __builtin_amdgcn_sched_barrier(0);
-          const int i = m / NI, j = m % NI;
-          acc[i][j] = Op::mma32(fb[c][j], fa[c][i], acc[i][j]);
+          const int pl = m / (MI * NI), i = (m / NI) % MI, j = m % NI;
+          acc[i][j] = Op::mma32(fb[c][j], fa[c][pl * MI + i], acc[i][j]);
           if (m < NRD) read_one(rslot, rks, m, fa[c ^ 1], fb[c ^ 1]);
           if (m < HALF) {
             if (ks == 0) issue_one(lds, slot ^ 1, soff1, wave, HALF + m);  // 2nd half of s+1

@@ -50,6 +50,18 @@ def test_fused_moe_task_shapes(gpu, T, E, topk, D, I, seed):
     verdict(out, ref, "north_star", "bf16", f"T{T} E{E} (1e-2)")
 
 
+@pytest.mark.parametrize("T,E,topk,D,I", [(640, 4, 2, 512, 384), (700, 4, 3, 384, 256), (520, 2, 1, 256, 640)])
+def test_fused_moe_prefill_tiles(gpu, T, E, topk, D, I):
+    """Slot counts above 64 per expert select the 256-row prefill tiles (buffer-load
+    pipeline for gate_up; two-plane down on 128x256 tiles when D % 256 == 0, else the
+    128x128 register-staged tiles); ragged per-expert counts leave padding rows."""
+    hidden, w1, w2, tw, ti = W.moe_inputs(T, E, topk, D, I, seed=T, wscale=0.05)
+    out = kore_amd.fused_moe(*[t.to(gpu) for t in (hidden, w1, w2, tw, ti)])
+    ref = moe_ref(hidden, w1, w2, tw, ti)
+    verdict(out, ref, "fused_moe", "bf16", f"prefill tiles T{T} E{E} k{topk} D{D} I{I}")
+    verdict(out, ref, "north_star", "bf16", f"prefill tiles T{T} (1e-2)")
+
+
 def test_fused_moe_decode_config(gpu):
     """BASELINE config 5 decode variant: T=64, E=8, top-2, D=4096, I=14336, weights
     N(0,1)*0.02, plain softmax/top-2/renorm router."""
