@@ -37,15 +37,24 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-source extra flags.  The fp8 block-scaled kernel promotes each MFMA partial
+# with VALU FMAs; MFMA results must then live in VGPRs (VALU cannot read AGPRs), so
+# that file selects the VGPR form of the MFMA instructions.
+EXTRA_FLAGS = {
+    "gemm_fp8_blockscale.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def _sources() -> list[Path]:
     return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
 
 
 def _compile(src: Path, verbose: bool) -> tuple[Path, float]:
     obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    flags = COMMON_FLAGS + EXTRA_FLAGS.get(src.name, [])
+    cmd = [HIPCC, *flags, "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
-        cmd = [HIPCC, *COMMON_FLAGS, "-x", "hip", "-c", str(src), "-o", str(obj)]
+        cmd = [HIPCC, *flags, "-x", "hip", "-c", str(src), "-o", str(obj)]
     t0 = time.time()
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:

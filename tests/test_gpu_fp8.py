@@ -28,7 +28,7 @@ def test_fp8_config_sweep(gpu, M):
     verdict(out, ref, "blockscale_genv", "fp8", f"M={M} (1e-2)")
 
 
-@pytest.mark.parametrize("M,N,K", [(128, 256, 256), (4095, 512, 512), (300, 384, 640)])
+@pytest.mark.parametrize("M,N,K", [(128, 256, 256), (4095, 512, 512), (300, 384, 640), (256, 128, 128), (200, 256, 128)])
 @pytest.mark.parametrize("seed", range(3))
 def test_fp8_task_shapes(gpu, M, N, K, seed):
     """gemm_fp8_a8w8_blockscale shapes incl. the non-aligned M=4095, task draw N(0,1)*0.2
