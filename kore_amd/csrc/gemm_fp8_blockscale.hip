@@ -167,30 +167,70 @@ __global__ void __launch_bounds__(kEngineThreads)
 
 
 // ------------------------------------------------------------------------------
-// Pipelined kernel: direct-to-LDS buffer loads, three LDS slots.
+// Pipelined kernel: direct-to-LDS buffer loads into a ring of LDS slots.
 //
-// Per slot (one K step = one 128-wide scale block): A 256 rows x 128 B, B 128 rows x
-// 128 B, the 256 activation scales of the tile rows and one copy per wave of the
-// block's weight scale -- scales travel through the same DMA pipeline as the
-// operands, so their waits are the operands' waits.  Rows are XOR-swizzled in 32-byte
-// units, key 2*((row >> 1) & 3): a lane's 32 K-consecutive bytes stay adjacent (two
-// ds_read_b128 at +0/+16) and the 8 rows read by 8 lanes land on distinct 16-byte
-// bank groups.  Each wave owns 128 x 64 outputs as 4 x 2 tiles of 32x32.  A tile's
-// two MFMAs (K 0..63, 64..127) accumulate into one of two rotating partials; the
-// promotion acc += partial * (xs * ws) of tile t-1 is issued between the two MFMAs
-// of tile t, so the VALU work runs under the matrix pipe.
+// Per slot (one K step = one 128-wide scale block): A 256 rows x 128 B, B BN rows x
+// 128 B, and the scales of the step -- scales travel through the same DMA pipeline
+// as the operands, so their waits are the operands' waits.  Activation scales: 256
+// fp32 per step, or, when the scale rows are contiguous in K (XS4), one 16-byte load
+// per row bringing four K steps into a two-deep ring (the per-step column of xs is
+// 256 strided 4-byte reads, each its own L2 request).  Weight scales: 64 copies per
+// 128-column block (16-byte copies of an aligned group of four steps for XS4).  Every
+// wave issues the same number of loads per stage; which scale a wave loads is chosen
+// with scalar selects, not branches: a branch would split the tile loop into blocks
+// and let the compiler sink the promotion FMAs away from the MFMAs they overlap.
 //
-// Slot lifecycle (stage s in slot s % 3): after the barrier in tile 6 of stage s
-// every wave has finished reading slot s % 3 and stage s+1 has landed; the loads of
-// stage s+3 go out in tiles 6-7 of stage s and tiles 0-4 of stage s+1, two per tile,
-// so each load has between one and two stages to arrive.
+// The 16-byte chunks of a 128-byte row are XOR-swizzled with key(r) = ((r >> 1) & 7)
+// ^ ((r >> 4) & 1), r = row % 32: the 16 rows read by a 16-lane group (64 banks) and
+// the 8 rows of equal r % 4 in a 32-lane group (128 banks) all hit distinct 16-byte
+// bank groups, and the key does not depend on which 32-row block a fragment is in.
+//
+// NW waves in a WGM x WGN grid, each owning (256/WGM) x 64 outputs as MI x 2 tiles of
+// 32x32.  A tile's two MFMAs (K 0..63, 64..127) accumulate into one of two rotating
+// partials; the promotion acc += partial * (xs * ws) of tile t-1 is issued between
+// the two MFMAs of tile t.  With 8 waves two share a SIMD, so one wave's promotion
+// FMAs run while the other's MFMAs occupy the matrix core (a wave's own VALU work
+// does not overlap its own MFMAs).
+//
+// Slot lifecycle (stage s in slot s % NSLOT): the barrier at tile TB (first tile of
+// the last block row) guarantees every wave has finished reading slot s % NSLOT and
+// stage s+1 has landed.  The loads of stage s + NSLOT then go into that slot, spread
+// over the next W tiles (W = NT with three slots: one to two stages of latency; the
+// remaining tiles of the stage with two slots: one stage).
 // ------------------------------------------------------------------------------
-constexpr int kF8BM = 256, kF8BN = 128, kF8Slots = 3;
-constexpr int kF8ABytes = kF8BM * 128, kF8BBytes = kF8BN * 128;
-constexpr int kF8XOff = kF8ABytes + kF8BBytes;           // 256 fp32 activation scales
-constexpr int kF8WOff = kF8XOff + 1024;                   // 4 waves x 64 copies of ws
-constexpr int kF8Slot = kF8WOff + 1024;
-constexpr int kF8Loads = 14;  // per wave per stage: 8 A, 4 B, 1 xs, 1 ws
+template <int BN_, int NW_, int NSLOT_, bool XS4_>
+struct F8Cfg {
+  static constexpr int BM = 256, BN = BN_, NW = NW_, NSLOT = NSLOT_;
+  static constexpr bool XS4 = XS4_;
+  static constexpr int NB = BN / 128;         // weight-scale blocks per tile
+  static constexpr int WGN = BN / 64, WGM = NW / WGN;
+  static_assert(WGM * WGN == NW && WGM >= 1, "wave grid");
+  static constexpr int WROWS = BM / WGM;
+  static constexpr int MI = WROWS / 32, NI = 2;
+  static constexpr int NT = MI * NI;
+  static constexpr int TB = (MI - 1) * NI;
+  static_assert(MI >= 2, "the barrier tile follows the last read of the current slot");
+  static constexpr int AQ = (BM / 8) / NW, BQ = (BN / 8) / NW;  // 8-row loads per wave
+  static_assert(AQ * NW * 8 == BM && BQ * NW * 8 == BN, "row loads cover the tile");
+  // scale loads per wave: 4 waves each load 64 xs rows and the ws copies; 8 waves:
+  // waves 0-3 xs, waves 4-7 ws (block (w-4) % NB)
+  static constexpr int SQ = NW == 4 ? 2 : 1;
+  static_assert(NW == 8 || NB == 1, "4-wave tiles have one weight-scale block");
+  static constexpr int LPS = AQ + BQ + SQ;
+  static constexpr int W = NSLOT >= 3 ? NT : NT - TB;  // load window in tiles
+  static constexpr int PER = (LPS + W - 1) / W;
+  static constexpr int WAITN = (NSLOT - 2) * LPS;    // loads allowed in flight at the barrier
+  // LDS layout of a slot
+  static constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
+  static constexpr int XOFF = A_BYTES + B_BYTES;          // xs (per-step mode only)
+  static constexpr int WOFF = XOFF + (XS4 ? 0 : 1024);
+  static constexpr int WCOPY = XS4 ? 1024 : 256;           // bytes of one ws block's copies
+  static constexpr int SLOT = WOFF + NB * WCOPY;
+  static constexpr int RING = NSLOT * SLOT;                // XS4 activation-scale ring
+  static constexpr int LDS = RING + (XS4 ? 2 * 4096 : 0);
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+  static_assert(NW * WROWS * 64 * 2 <= LDS, "epilogue staging fits");
+};
 
 __device__ __forceinline__ void buf_lds(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint8_t* lds_dst,
                                         int size) {
@@ -198,21 +238,28 @@ __device__ __forceinline__ void buf_lds(__amdgpu_buffer_rsrc_t r, uint32_t voff,
   else __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_dst, 4, (int)voff, (int)soff, 0, 0);
 }
 
-__device__ __forceinline__ i32x8_t lds_frag32(const uint8_t* p) {
-  const u32x4_t lo = *(const u32x4_t*)p;
-  const u32x4_t hi = *(const u32x4_t*)(p + 16);
+__device__ __forceinline__ int f8_key(int r) { return ((r >> 1) & 7) ^ ((r >> 4) & 1); }
+
+// 32 K-consecutive bytes of one row: two 16-byte chunks at their swizzled positions.
+__device__ __forceinline__ i32x8_t lds_frag32(const uint8_t* row, const int (&off)[2]) {
+  const u32x4_t lo = *(const u32x4_t*)(row + off[0]);
+  const u32x4_t hi = *(const u32x4_t*)(row + off[1]);
   return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
 }
 
-// FULL_M: every row of the M tile exists, so all A loads of a wave share one
-// per-lane offset and differ by a scalar row offset; otherwise rows are clamped per load.
-template <bool FULL_M>
-__global__ void __launch_bounds__(256)
+// FULL_M: every row of the M tile exists, so the A loads of a wave share one per-lane
+// offset and differ by a scalar row offset; otherwise rows are clamped per load.
+template <typename C, bool FULL_M>
+__global__ void __launch_bounds__(C::NW * 64)
     gemm_fp8_pipe_kernel(const Fp8Params p) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kF8Slots * kF8Slot];
+  constexpr int NW = C::NW, MI = C::MI, NI = C::NI, NT = C::NT, TB = C::TB;
+  constexpr int AQ = C::AQ, BQ = C::BQ, LPS = C::LPS, PER = C::PER, NSLOT = C::NSLOT;
+  constexpr bool XS4 = C::XS4;
+
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[C::LDS];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / C::WGN, wn = wave % C::WGN;
   const int lr = lane & 31, hh = lane >> 5;
 
   const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
@@ -221,105 +268,124 @@ __global__ void __launch_bounds__(256)
   const int first_m = grp * kFp8GroupM;
   const int gsz = min(p.tiles_m - first_m, kFp8GroupM);
   const int tl = bid - grp * width;
-  const int m0 = (first_m + tl % gsz) * kF8BM;
-  const int n0 = (tl / gsz) * kF8BN;
-  const int rows_a = min(p.M - m0, kF8BM);
+  const int m0 = (first_m + tl % gsz) * C::BM;
+  const int n0 = (tl / gsz) * C::BN;
+  const int rows_a = min(p.M - m0, C::BM);
   const int nk = p.K / 128;
 
   // ---- buffer resources (tile-based) and per-lane load offsets ----
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.xq + (int64_t)m0 * p.ldx, (uint32_t)(rows_a * p.ldx));
-  const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.wq + (int64_t)n0 * p.ldw, (uint32_t)(kF8BN * p.ldw));
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.wq + (int64_t)n0 * p.ldw, (uint32_t)(C::BN * p.ldw));
   const __amdgpu_buffer_rsrc_t rx =
       make_rsrc(p.xs + (int64_t)m0 * p.xs_m, (uint32_t)(((rows_a - 1) * p.xs_m + (nk - 1) * p.xs_k + 1) * 4));
-  const __amdgpu_buffer_rsrc_t rw =
-      make_rsrc(p.ws + (int64_t)(n0 / 128) * p.ws_n, (uint32_t)(((nk - 1) * p.ws_k + 1) * 4));
-  // 16-byte chunk this lane fetches: row (lane >> 3) of an 8-row group, position lane & 7.
-  const int dchunk = (lane & 7) ^ (2 * ((lane >> 4) & 3));
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(
+      p.ws + (int64_t)(n0 / 128) * p.ws_n, (uint32_t)(((C::NB - 1) * p.ws_n + (nk - 1) * p.ws_k + 1) * 4));
+  // 16-byte chunk this lane fetches: row (lane >> 3) of an 8-row group, position
+  // lane & 7.  Load q of a wave covers rows 8 * (wave + NW * q) + lane / 8, whose
+  // row % 32 is 8 * (wave % 4) + lane / 8 for every q.
   const int lrow = lane >> 3;
-  uint32_t a_voff[FULL_M ? 1 : 8];
+  const int dchunk = (lane & 7) ^ f8_key(8 * (wave & 3) + lrow);
+  uint32_t a_voff[FULL_M ? 1 : AQ];
   if constexpr (FULL_M) {
     a_voff[0] = (uint32_t)((lrow + 8 * wave) * p.ldx + 16 * dchunk);
   } else {
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      a_voff[j] = (uint32_t)(min(lrow + 8 * (wave + 4 * j), rows_a - 1) * p.ldx + 16 * dchunk);
+    for (int q = 0; q < AQ; ++q)
+      a_voff[q] = (uint32_t)(min(lrow + 8 * (wave + NW * q), rows_a - 1) * p.ldx + 16 * dchunk);
   }
   const uint32_t b_voff = (uint32_t)((lrow + 8 * wave) * p.ldw + 16 * dchunk);
-  const uint32_t x_voff = (uint32_t)(min(64 * wave + lane, rows_a - 1) * p.xs_m * 4);
-  const uint32_t a_rstep = (uint32_t)(32 * p.ldx), b_rstep = (uint32_t)(32 * p.ldw);
+  const uint32_t x_voff = (uint32_t)(min(64 * (wave & 3) + lane, rows_a - 1) * p.xs_m * 4);
+  const uint32_t a_rstep = (uint32_t)(8 * NW * p.ldx), b_rstep = (uint32_t)(8 * NW * p.ldw);
   const uint32_t xs_kstep = (uint32_t)(p.xs_k * 4), ws_kstep = (uint32_t)(p.ws_k * 4);
+  // weight-scale block this wave loads (8 waves) and the one its columns use
+  const int wblk_ld = (NW == 8) ? ((wave - 4) & 3) % C::NB : 0;
+  const uint32_t w_soff_blk = (uint32_t)(wblk_ld * p.ws_n * 4);
+  const int wblk_rd = (wn * 64) / 128;
 
   // load q of stage kb (already clamped to nk - 1) into slot
   auto issue = [&](int slot, int kb, int q) {
-    uint8_t* base = lds + slot * kF8Slot;
-    if (q < 8) {
-      const uint32_t v = FULL_M ? a_voff[0] : a_voff[FULL_M ? 0 : q];
+    uint8_t* base = lds + slot * C::SLOT;
+    if (q < AQ) {
+      const uint32_t v = a_voff[FULL_M ? 0 : q];
       const uint32_t so = (uint32_t)kb * 128u + (FULL_M ? (uint32_t)q * a_rstep : 0u);
-      buf_lds(ra, v, so, base + (wave + 4 * q) * 1024, 16);
-    } else if (q < 12) {
-      buf_lds(rb, b_voff, (uint32_t)kb * 128u + (uint32_t)(q - 8) * b_rstep, base + kF8ABytes + (wave + 4 * (q - 8)) * 1024,
-              16);
-    } else if (q == 12) {
-      buf_lds(rx, x_voff, (uint32_t)kb * xs_kstep, base + kF8XOff + wave * 256, 4);
+      buf_lds(ra, v, so, base + (wave + NW * q) * 1024, 16);
+    } else if (q < AQ + BQ) {
+      buf_lds(rb, b_voff, (uint32_t)kb * 128u + (uint32_t)(q - AQ) * b_rstep,
+              base + C::A_BYTES + (wave + NW * (q - AQ)) * 1024, 16);
     } else {
-      buf_lds(rw, 0u, (uint32_t)kb * ws_kstep, base + kF8WOff + wave * 256, 4);
+      // scale load (wave-uniform selects): activation scales, or weight-scale copies
+      const bool xload = (NW == 4 ? q == AQ + BQ : wave < 4) && (!XS4 || (kb & 3) == 0);
+      if constexpr (XS4) {
+        uint8_t* dst = xload ? lds + C::RING + ((kb >> 2) & 1) * 4096 + (wave & 3) * 1024
+                             : base + C::WOFF + wblk_ld * C::WCOPY;
+        buf_lds(xload ? rx : rw, xload ? x_voff : 0u,
+                xload ? (uint32_t)kb * 4u : w_soff_blk + (uint32_t)(kb & ~3) * 4u, dst, 16);
+      } else {
+        uint8_t* dst = xload ? base + C::XOFF + (wave & 3) * 256 : base + C::WOFF + wblk_ld * C::WCOPY;
+        buf_lds(xload ? rx : rw, xload ? x_voff : 0u,
+                xload ? (uint32_t)kb * xs_kstep : w_soff_blk + (uint32_t)kb * ws_kstep, dst, 4);
+      }
     }
   };
 
-  // ---- fragment read offsets: row lr of a 32-row block, K sub-step h ----
-  const int key = 2 * ((lr >> 1) & 3);
-  const int offh0 = lr * 128 + (((2 * hh) ^ key) << 4);
-  const int offh1 = lr * 128 + (((4 + 2 * hh) ^ key) << 4);
-  const int rowA0 = wm * 128, rowB0 = wn * 64;
+  // ---- fragment read offsets: row lr of a 32-row block, K sub-step h, 16-byte half e:
+  // chunk 4h + 2hh + e ----
+  const int key = f8_key(lr);
+  int off[2][2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) off[h][e] = lr * 128 + (((4 * h + 2 * hh + e) ^ key) << 4);
+  const int rowA0 = wm * C::WROWS, rowB0 = wn * 64;
 
-  f32x16_t acc[4][2];
+  f32x16_t acc[MI][NI];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NI; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
   f32x16_t part[2];
 #pragma unroll
   for (int r = 0; r < 16; ++r) part[1][r] = 0.0f;
   const f32x16_t zero = {};
-  float sc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  float xsv[4], wsv;
+  float sc[MI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) sc[i] = 0.0f;
+  float xsv[MI], wsv;
   i32x8_t af[2][2], bf[2][2];  // af[buffer][h], bf[j][h]
 
-  // ---- prologue: stages 0 and 1 in flight, wait for 0, first fragments ----
+  // ---- prologue: stages 0 .. NSLOT-2 in flight, wait for stage 0, first fragments,
+  // then the post-barrier share of stage NSLOT-1 ----
 #pragma unroll
-  for (int q = 0; q < kF8Loads; ++q) issue(0, 0, q);
+  for (int st = 0; st + 1 < NSLOT; ++st)
 #pragma unroll
-  for (int q = 0; q < kF8Loads; ++q) issue(1, min(1, nk - 1), q);
-  wait_vmcnt<kF8Loads>();
+    for (int q = 0; q < LPS; ++q) issue(st, min(st, nk - 1), q);
+  wait_vmcnt<C::WAITN>();
   exec_barrier();
-  {
-    const uint8_t* cur = lds;
-    af[0][0] = lds_frag32(cur + rowA0 * 128 + offh0);
-    af[0][1] = lds_frag32(cur + rowA0 * 128 + offh1);
+  af[0][0] = lds_frag32(lds + rowA0 * 128, off[0]);
+  af[0][1] = lds_frag32(lds + rowA0 * 128, off[1]);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      bf[j][0] = lds_frag32(cur + kF8ABytes + (rowB0 + 32 * j) * 128 + offh0);
-      bf[j][1] = lds_frag32(cur + kF8ABytes + (rowB0 + 32 * j) * 128 + offh1);
-    }
+  for (int j = 0; j < NI; ++j) {
+    bf[j][0] = lds_frag32(lds + C::A_BYTES + (rowB0 + 32 * j) * 128, off[0]);
+    bf[j][1] = lds_frag32(lds + C::A_BYTES + (rowB0 + 32 * j) * 128, off[1]);
   }
 #pragma unroll
-  for (int q = 0; q < 4; ++q) issue(2, min(2, nk - 1), q);
+  for (int q = 0; q < PER * (NT - TB) && q < LPS; ++q) issue(NSLOT - 1, min(NSLOT - 1, nk - 1), q);
 
   int slot = 0;
   for (int s = 0; s < nk; ++s) {
-    const int slot1 = slot == 2 ? 0 : slot + 1;
-    const int slot2 = slot1 == 2 ? 0 : slot1 + 1;
-    const uint8_t* cur = lds + slot * kF8Slot;
-    const uint8_t* nxt = lds + slot1 * kF8Slot;
-    const int kb2 = min(s + 2, nk - 1), kb3 = min(s + 3, nk - 1);
+    const int slot1 = slot + 1 == NSLOT ? 0 : slot + 1;
+    const int slotp = slot == 0 ? NSLOT - 1 : slot - 1;  // slot of stage s + NSLOT - 1
+    const uint8_t* cur = lds + slot * C::SLOT;
+    const uint8_t* nxt = lds + slot1 * C::SLOT;
+    const int kbn = min(s + NSLOT, nk - 1), kbp = min(s + NSLOT - 1, nk - 1);
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int i = t >> 1, j = t & 1;
-      if (t == 6) {
+    for (int t = 0; t < NT; ++t) {
+      const int i = t / NI, j = t % NI;
+      if (t == TB) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        wait_vmcnt<kF8Loads>();
+        wait_vmcnt<C::WAITN>();
         exec_barrier();
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -327,41 +393,57 @@ __global__ void __launch_bounds__(256)
       __builtin_amdgcn_sched_barrier(0);
       if (t == 1) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) sc[q] = xsv[q] * wsv;
+        for (int q = 0; q < MI; ++q) sc[q] = xsv[q] * wsv;
       }
       {
-        // promote the previous tile (t == 0: tile 7 of the previous stage, whose
-        // scale sc[3] is still live; zeros before the first stage)
-        const int pt = (t + 7) & 7;
-        const float f = sc[pt >> 1];
+        // promote the previous tile (t == 0: the last tile of the previous stage,
+        // whose scale sc[MI-1] is still live; zeros before the first stage)
+        const int pt = (t + NT - 1) % NT;
+        const float f = sc[pt / NI];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[pt >> 1][pt & 1][r] = fmaf(part[j ^ 1][r], f, acc[pt >> 1][pt & 1][r]);
+        for (int r = 0; r < 16; ++r) acc[pt / NI][pt % NI][r] = fmaf(part[j ^ 1][r], f, acc[pt / NI][pt % NI][r]);
       }
       __builtin_amdgcn_sched_barrier(0);
       part[j] = mma32_fp8(bf[j][1], af[i & 1][1], part[j]);
       __builtin_amdgcn_sched_barrier(0);
-      // LDS reads: scales of this stage, A of the next row block, B of the next stage
+      // LDS reads: scales of this stage; A block i+1 (both K halves) at the first
+      // tile of block i, two MFMA pairs before its first use; after the barrier A
+      // block 0 of the next stage; B of the next stage right after its last use.
       if (t == 0) {
+        if constexpr (XS4) {
+          const uint8_t* ring = lds + C::RING + ((s >> 2) & 1) * 4096 + (s & 3) * 4;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) xsv[q] = *(const float*)(cur + kF8XOff + (rowA0 + 32 * q + lr) * 4);
-        wsv = *(const float*)(cur + kF8WOff + wave * 256 + lane * 4);
+          for (int q = 0; q < MI; ++q) xsv[q] = *(const float*)(ring + (rowA0 + 32 * q + lr) * 16);
+          wsv = *(const float*)(cur + C::WOFF + wblk_rd * C::WCOPY + lane * 16 + (s & 3) * 4);
+        } else {
+#pragma unroll
+          for (int q = 0; q < MI; ++q) xsv[q] = *(const float*)(cur + C::XOFF + (rowA0 + 32 * q + lr) * 4);
+          wsv = *(const float*)(cur + C::WOFF + wblk_rd * C::WCOPY + lane * 4);
+        }
       }
-      if (t < 6) {
-        const uint8_t* src = cur + (rowA0 + 32 * (i + 1)) * 128 + (j ? offh1 : offh0);
-        af[(i + 1) & 1][j] = lds_frag32(src);
-      } else {
-        const uint8_t* src = nxt + rowA0 * 128 + (j ? offh1 : offh0);
-        af[0][j] = lds_frag32(src);
-        bf[j][0] = lds_frag32(nxt + kF8ABytes + (rowB0 + 32 * j) * 128 + offh0);
-        bf[j][1] = lds_frag32(nxt + kF8ABytes + (rowB0 + 32 * j) * 128 + offh1);
+      if (j == 0 && i + 1 < MI) {
+        af[(i + 1) & 1][0] = lds_frag32(cur + (rowA0 + 32 * (i + 1)) * 128, off[0]);
+        af[(i + 1) & 1][1] = lds_frag32(cur + (rowA0 + 32 * (i + 1)) * 128, off[1]);
+      } else if (t == TB) {
+        af[0][0] = lds_frag32(nxt + rowA0 * 128, off[0]);
+        af[0][1] = lds_frag32(nxt + rowA0 * 128, off[1]);
       }
-      // direct loads: stage s+2 (tiles 0-4, loads 4..13), stage s+3 (tiles 6-7, loads 0..3)
-      if (t <= 4) {
-        issue(slot2, kb2, 4 + 2 * t);
-        issue(slot2, kb2, 5 + 2 * t);
-      } else if (t >= 6) {
-        issue(slot, kb3, 2 * (t - 6));
-        issue(slot, kb3, 2 * (t - 6) + 1);
+      if (t >= TB) {
+        bf[j][0] = lds_frag32(nxt + C::A_BYTES + (rowB0 + 32 * j) * 128, off[0]);
+        bf[j][1] = lds_frag32(nxt + C::A_BYTES + (rowB0 + 32 * j) * 128, off[1]);
+      }
+      // direct loads, PER per tile over the window: tiles TB.. of stage s start stage
+      // s + NSLOT (into the slot just released); with three slots tiles ..TB-1 finish
+      // stage s + NSLOT - 1
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        if (t >= TB) {
+          const int q = PER * (t - TB) + e;
+          if (q < LPS) issue(slot, kbn, q);
+        } else if (NSLOT >= 3) {
+          const int q = PER * (t + NT - TB) + e;
+          if (q < LPS) issue(slotp, kbp, q);
+        }
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -369,18 +451,18 @@ __global__ void __launch_bounds__(256)
   }
   // promote the last tile of the last stage
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[3][1][r] = fmaf(part[1][r], sc[3], acc[3][1][r]);
+  for (int r = 0; r < 16; ++r) acc[MI - 1][NI - 1][r] = fmaf(part[1][r], sc[MI - 1], acc[MI - 1][NI - 1][r]);
   wait_vmcnt<0>();  // the clamped trailing loads must land before LDS is reused
   __syncthreads();
 
   // ---- epilogue: bf16 pack, stage per wave, 16-byte row stores ----
-  using St = Stager<128, 64>;
+  using St = Stager<C::WROWS, 64>;
   using Op = MfmaOp<BF16>;
-  uint16_t* stg = (uint16_t*)lds + wave * (128 * 64);
+  uint16_t* stg = (uint16_t*)lds + wave * (C::WROWS * 64);
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NI; ++j)
 #pragma unroll
       for (int g = 0; g < 4; ++g)
         St::put(stg, out_row(i, lane), out_col(j, g, lane),
@@ -393,6 +475,16 @@ __global__ void __launch_bounds__(256)
     const int gm = mw0 + row, gn = nw0 + col;
     if (gm < p.M) store_row8(p.y + (int64_t)gm * p.ldy + gn, gn, p.N, vec, v);
   });
+}
+
+template <typename C>
+int launch_fp8_pipe(Fp8Params p, hipStream_t st) {
+  p.tiles_m = (p.M + C::BM - 1) / C::BM;
+  p.tiles_n = p.N / C::BN;
+  const dim3 grid((unsigned)((int64_t)p.tiles_m * p.tiles_n)), block(C::NW * 64);
+  if (p.M % C::BM == 0) hipLaunchKernelGGL((gemm_fp8_pipe_kernel<C, true>), grid, block, 0, st, p);
+  else hipLaunchKernelGGL((gemm_fp8_pipe_kernel<C, false>), grid, block, 0, st, p);
+  return check_launch("gemm_fp8_pipe_kernel");
 }
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -435,15 +527,22 @@ extern "C" int kore_gemm_a8w8_blockscale(const void* xq, int64_t ldx, const void
   p.tiles_n = (int)(N / BN);
   p.vec_store = (ldy % 8 == 0) && aligned16(y);
   const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n;
-  // the pipelined kernel addresses each tile through 32-bit buffer offsets
-  const bool pipe_ok = 256 * ldx + K < (1ll << 31) && 128 * ldw + K < (1ll << 31) &&
-                       (M * xs_m + K / 128 * xs_k) * 4 < (1ll << 31) && (K / 128 * ws_k) * 4 < (1ll << 31);
+  // the pipelined kernels address each tile through 32-bit buffer offsets
+  const bool pipe_ok = 256 * ldx + K < (1ll << 31) && 256 * ldw + K < (1ll << 31) &&
+                       (M * xs_m + K / 128 * xs_k) * 4 < (1ll << 31) && (N / 128 * ws_n + K / 128 * ws_k) * 4 < (1ll << 31);
   if (pipe_ok) {
-    if (M % BM == 0)
-      hipLaunchKernelGGL((gemm_fp8_pipe_kernel<true>), dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, p);
-    else
-      hipLaunchKernelGGL((gemm_fp8_pipe_kernel<false>), dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, p);
-    return check_launch("gemm_fp8_pipe_kernel");
+    // four K steps of scales per 16-byte load when scale rows are contiguous, 16-byte
+    // aligned and K/128 is a multiple of 4 (so no load runs past a row)
+    const bool xs4 = xs_k == 1 && xs_m % 4 == 0 && aligned16(xs) && ws_k == 1 && ws_n % 4 == 0 && aligned16(ws) &&
+                     (K / 128) % 4 == 0;
+    hipStream_t st = (hipStream_t)stream;
+    // 256x256 tiles halve LDS and L2 traffic per MFMA but need enough of them to
+    // occupy the 256 CUs; otherwise 256x128 tiles (three LDS slots)
+    const int64_t tiles256 = (M + 255) / 256 * (N / 256);
+    if (N % 256 == 0 && tiles256 >= 192) {
+      return xs4 ? launch_fp8_pipe<F8Cfg<256, 8, 2, true>>(p, st) : launch_fp8_pipe<F8Cfg<256, 8, 2, false>>(p, st);
+    }
+    return xs4 ? launch_fp8_pipe<F8Cfg<128, 8, 3, true>>(p, st) : launch_fp8_pipe<F8Cfg<128, 8, 3, false>>(p, st);
   }
   hipLaunchKernelGGL((gemm_fp8_bs_kernel<BM, BN>), dim3((unsigned)blocks), dim3(kEngineThreads), 0,
                      (hipStream_t)stream, p);

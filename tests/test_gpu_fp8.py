@@ -40,6 +40,18 @@ def test_fp8_task_shapes(gpu, M, N, K, seed):
     pair_only(out, ref, "fp8", f"{M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("M,N,K", [(4000, 3072, 640), (4000, 3072, 512), (3840, 3072, 1024)])
+def test_fp8_wide_tiles(gpu, M, N, K):
+    """Problems with at least 192 tiles of 256x256 run on the 256x256 (two-slot) kernel:
+    a partial last M tile (M=4000), per-step scale loads (K/128 = 5) and four-step
+    scale loads (K/128 = 4, 8)."""
+    xq, wq, xs, ws = W.fp8_inputs(M, N, K, seed=M + K, scale=0.2)
+    out = _run(gpu, xq, wq, xs, ws)
+    ref = matmul_blockscale_ref(xq, wq, xs, ws)
+    verdict(out, ref, "blockscale", "fp8", f"{M}x{N}x{K}")
+    pair_only(out, ref, "fp8", f"{M}x{N}x{K}")
+
+
 @pytest.mark.parametrize("regime", ["zeros", "ones", "large", "small"])
 def test_fp8_adversarial(gpu, regime):
     """The task's authored adversarial battery (kore/tasks/vendor_ops.py:526-543)."""
@@ -58,6 +70,27 @@ def test_fp8_scale_invariance_and_determinism(gpu):
     y2 = _run(gpu, xq, wq, xs * 2, ws)
     assert bit_equal(y2, y1 * 2)
     assert bit_equal(_run(gpu, xq, wq, xs, ws), y1)
+
+
+@pytest.mark.parametrize("M,K", [(512, 4096), (300, 1536), (256, 640)])
+def test_fp8_scale_and_row_layouts(gpu, M, K):
+    """Column-major scale tensors (x_scale stride (1, M), w_scale stride (1, N/128)) and
+    padded operand rows give the same result as the contiguous layout: the kernel reads
+    scales through their strides (per-K-step loads) and the contiguous case batches four
+    K steps of x_scale per load when K/128 % 4 == 0."""
+    N = 384
+    xq, wq, xs, ws = W.fp8_inputs(M, N, K, seed=4)
+    base = _run(gpu, xq, wq, xs, ws)
+    verdict(base, matmul_blockscale_ref(xq, wq, xs, ws), "blockscale", "fp8", f"{M}x{N}x{K}")
+    xs_t = xs.t().contiguous().t()
+    ws_t = ws.t().contiguous().t()
+    assert xs_t.stride() == (1, M)
+    assert bit_equal(_run(gpu, xq, wq, xs_t, ws_t), base)
+    pad = torch.zeros(M, K + 128, dtype=xq.dtype)
+    pad[:, :K] = xq
+    padw = torch.zeros(N, K + 256, dtype=wq.dtype)
+    padw[:, :K] = wq
+    assert bit_equal(_run(gpu, pad[:, :K], padw[:, :K], xs, ws), base)
 
 
 def test_fp8_rejects_unaligned(gpu):
