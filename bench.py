@@ -1,25 +1,28 @@
 """Benchmark of the GEMM-family hot path on one MI355X.
 
-``python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME] [--no-cpu]``
+``python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME,...] [--no-cpu]``
 
 A "step" is one call of an operator on one batch of synthetic, seeded inputs that
 are resident in HBM before timing starts.  The headline (``value``) is the fp8
 a8w8 block-scaled GEMM at M=2048, N=7168, K=4096 -- the first configuration named
 by the metric; every other BASELINE configuration (bf16 GEMM 4096^3 and 1024^3,
 fp16 GEMM+bias+{GELU,ReLU,SiLU} 4096^3, batched GEMM, the fp8 M sweep, MoE decode
-T=64 and prefill T=4096) is reported in ``configs`` with the same fields.
+T=64 and prefill T=4096) is reported under ``configs`` with the same fields.
 
-Per configuration: W warm-up steps, then K steps bracketed by
-``torch.cuda.synchronize()``; ``ms_per_step`` is wall time / K and ``kernel_ms`` the
-mean of per-step HIP events recorded on the stream the kernels are launched on
-(torch's current stream).  ``cold_ms`` is the reference drivers' protocol: median of
-events around a step preceded by a 512 MiB cache flush (``kore/tasks/_genops.py:787-813``
-flushes 256 MiB; MI355X has 256 MiB of Infinity Cache).  Roofline fractions use
-the algorithmic FLOPs/bytes of ``kore_amd.roofline`` and MI355X peaks (bf16 2.5 PF,
-fp8 5.0 PF, HBM 8 TB/s).
+Per configuration: W warm-up steps, then K steps back to back between
+``torch.cuda.synchronize()`` calls.  ``ms_per_step`` is host wall time / K;
+``kernel_ms`` is the HIP-event time over the same K steps / K, with both events
+recorded on the stream the kernels are launched on (torch's current stream).
+``cold_ms`` follows the reference drivers' protocol: median of events around one
+step preceded by a 512 MiB cache flush (``kore/tasks/_genops.py:787-813`` flushes
+256 MiB; MI355X has 256 MiB of Infinity Cache).  Roofline fractions use the
+algorithmic FLOPs/bytes of ``kore_amd.roofline`` and MI355X peaks (bf16 2.5 PF, fp8
+5.0 PF, HBM 8 TB/s).  ``roofline.traffic`` is the HBM traffic per launch of the
+headline kernel recorded by rocprofv3 FETCH_SIZE/WRITE_SIZE runs
+(``profiles/hbm_traffic.md``, written by ``python -m kore_amd.profiling traffic``).
 
 ``cpu_baseline`` times the CPU oracle (the restated torch-fp32 reference) on a row
-sample of the headline workload, on all host cores; it is a reported baseline.
+sample of the headline workload, on the host's cores; it is a reported baseline.
 """
 
 from __future__ import annotations
@@ -32,6 +35,8 @@ import sys
 import time
 
 import torch
+
+HEADLINE = "fp8_blockscale_2048x7168x4096"
 
 
 def _parse():
@@ -50,20 +55,26 @@ class Timer:
         self.steps, self.warmup, self.cold_iters = steps, warmup, cold_iters
         self._flush = None
 
-    def run(self, fn):
-        for _ in range(self.warmup):
+    def run(self, fn, min_warm_s: float = 0.2):
+        # W warm-up steps, and at least min_warm_s of them so the GPU clocks have
+        # ramped before the first timed configuration
+        t_w = time.perf_counter()
+        n = 0
+        while n < self.warmup or time.perf_counter() - t_w < min_warm_s:
             fn()
+            n += 1
+            if n % 8 == 0:
+                torch.cuda.synchronize()
         torch.cuda.synchronize()
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(self.steps)]
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
-        for s, e in ev:
-            s.record()
+        start.record()
+        for _ in range(self.steps):
             fn()
-            e.record()
+        end.record()
         torch.cuda.synchronize()
         wall = (time.perf_counter() - t0) * 1e3 / self.steps
-        kern = statistics.fmean(s.elapsed_time(e) for s, e in ev)
+        kern = start.elapsed_time(end) / self.steps
         cold = []
         if self.cold_iters:
             if self._flush is None:
@@ -79,12 +90,12 @@ class Timer:
         return wall, kern, (statistics.median(cold) if cold else None)
 
 
-def _entry(name, op, dims, dtype, wall, kern, cold, extra=None):
+def _entry(name, op, dims, dtype, wall, kern, cold):
     from kore_amd import roofline as R
 
     rf = R.roofline(op, dims, dtype)
     t = kern * 1e-3
-    out = {
+    return {
         "name": name, "op": op, "dims": dims, "dtype": dtype,
         "ms_per_step": round(wall, 5), "kernel_ms": round(kern, 5),
         "cold_ms": round(cold, 5) if cold is not None else None,
@@ -95,52 +106,6 @@ def _entry(name, op, dims, dtype, wall, kern, cold, extra=None):
         "frac_mfma_peak": round(rf.flops / t / rf.peak_flops, 4),
         "frac_hbm_peak": round(rf.bytes / t / rf.peak_bw, 4),
     }
-    if extra:
-        out.update(extra)
-    return out
-
-
-def build_configs(dev):
-    import kore_amd
-    from kore_amd import workloads as W
-
-    cfg = {}
-
-    def fp8(M):
-        xq, wq, xs, ws = W.fp8_inputs(M, 7168, 4096, seed=0, device=dev)
-        return (lambda: kore_amd.gemm_a8w8_blockscale(xq, wq, xs, ws)), ("gemm_fp8", {"M": M, "N": 7168, "K": 4096}, "fp8")
-
-    cfg["fp8_blockscale_2048x7168x4096"] = lambda: fp8(2048)
-
-    def dense(n):
-        a, b = W.dense_inputs(n, n, n, seed=0, device=dev)
-        return (lambda: kore_amd.gemm(a, b)), ("gemm", {"M": n, "N": n, "K": n}, "bf16")
-
-    cfg["bf16_gemm_4096"] = lambda: dense(4096)
-    cfg["bf16_gemm_1024"] = lambda: dense(1024)
-
-    def fused(act):
-        a, b, bias = W.fused_inputs(4096, 4096, 4096, seed=0, device=dev)
-        return (lambda: kore_amd.gemm_fused(a, b, bias, act)), ("gemm", {"M": 4096, "N": 4096, "K": 4096}, "fp16")
-
-    for act in ("gelu", "relu", "silu"):
-        cfg[f"fp16_gemm_bias_{act}_4096"] = (lambda a=act: fused(a))
-
-    def batched():
-        a, b = W.batched_inputs(64, 1024, 1024, 128, seed=0, device=dev)
-        return (lambda: kore_amd.batched_gemm(a, b)), ("batched_gemm", {"B": 64, "M": 1024, "N": 1024, "K": 128}, "bf16")
-
-    cfg["bf16_batched_64x1024x1024x128"] = batched
-    for M in (512, 128, 16):
-        cfg[f"fp8_blockscale_{M}x7168x4096"] = (lambda m=M: fp8(m))
-
-    def moe(T):
-        args = W.moe_inputs(T, 8, 2, 4096, 14336, seed=0, device=dev)
-        return (lambda: kore_amd.fused_moe(*args)), ("fused_moe", {"M": T, "E": 8, "topk": 2, "D": 4096, "I": 14336}, "bf16")
-
-    cfg["moe_decode_T64"] = lambda: moe(64)
-    cfg["moe_prefill_T4096"] = lambda: moe(4096)
-    return cfg
 
 
 def cpu_baseline(seconds_budget: float = 20.0):
@@ -165,7 +130,7 @@ def cpu_baseline(seconds_budget: float = 20.0):
     return {"value": round(2.0 * m * 7168 * 4096 / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
             "sample": f"oracle.quant.matmul_blockscale_ref on rows 0..{m} of the 2048x7168x4096 workload "
-                      f"(fp32 dequant + torch CPU matmul), median of {len(times)} runs, "
+                      f"(fp32 dequant + torch CPU matmul on {threads} threads), median of {len(times)} runs, "
                       f"{t * 1e3:.1f} ms per run"}
 
 
@@ -173,41 +138,42 @@ def main():
     args = _parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU; --gpus {args.gpus} is not supported "
-              "(the GEMM family shards without communication -- see DESIGN.md).", file=sys.stderr)
+              "(the GEMM family shards without communication; the sharding design is documented, "
+              "not measured).", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py: no HIP device visible", file=sys.stderr)
         return 1
     import kore_amd._lib as L
+    from kore_amd.profiling import read_traffic
+    from kore_amd.workloads import bench_workloads
 
     L.load()
     dev = torch.device("cuda:0")
     timer = Timer(args.steps, args.warmup, args.cold_iters)
-    cfgs = build_configs(dev)
-    names = list(cfgs)
+    work = bench_workloads()
+    names = list(work)
     if args.only:
         names = [n for n in names if n in args.only.split(",")]
     results = {}
     for name in names:
-        fn, (op, dims, dtype) = cfgs[name]()
+        fn, op, dims, dtype = work[name](dev)
         wall, kern, cold = timer.run(fn)
         results[name] = _entry(name, op, dims, dtype, wall, kern, cold)
-        print(f"# {name}: {results[name]['tflops']} TFLOP/s, {results[name]['tb_per_s']} TB/s, "
-              f"kernel {kern * 1e3:.1f} us, frac_of_bound {results[name]['frac_of_bound']}",
-              file=sys.stderr, flush=True)
+        r = results[name]
+        print(f"# {name}: {r['tflops']} TFLOP/s, {r['tb_per_s']} TB/s, kernel {kern * 1e3:.1f} us, "
+              f"wall {wall * 1e3:.1f} us, frac_of_bound {r['frac_of_bound']}", file=sys.stderr, flush=True)
         del fn
         torch.cuda.empty_cache()
-    head_name = "fp8_blockscale_2048x7168x4096"
-    head = results.get(head_name) or next(iter(results.values()))
-    peak_unit = "TFLOP/s" if head["bound"] == "mfma" else "GB/s"
+    head = results.get(HEADLINE) or next(iter(results.values()))
+    flops = 2.0 * head["dims"]["M"] * head["dims"]["N"] * head["dims"]["K"] if "K" in head["dims"] else None
     if head["bound"] == "mfma":
-        achieved, peak = head["tflops"], (5000.0 if "fp8" in head["dtype"] else 2500.0)
+        achieved, peak, unit = head["tflops"], (5000.0 if head["dtype"] == "fp8" else 2500.0), "TFLOP/s"
     else:
-        achieved, peak = head["tb_per_s"] * 1000.0, 8000.0
+        achieved, peak, unit = head["tb_per_s"] * 1000.0, 8000.0, "GB/s"
     line = {
         "metric": "TFLOP/s + % MFMA peak, fp8 blockscale GEMM 2048x7168x4096 and bf16 GEMM 4096^3",
-        "value": round(2.0 * 2048 * 7168 * 4096 / (head["ms_per_step"] * 1e-3) / 1e12, 2)
-        if head["name"] == head_name else head["tflops"],
+        "value": round(flops / (head["ms_per_step"] * 1e-3) / 1e12, 2) if flops else head["tflops"],
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -216,19 +182,20 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8_e4m3 (fp32 accumulate, bf16 out)" if "fp8" in head["dtype"] else head["dtype"],
-        "data": "synthetic (seeded N(0,1) inputs, quantised 1x128 / 128x128 to OCP e4m3)",
-        "config": {"workload": head["name"], "M": 2048, "N": 7168, "K": 4096, "parallelism": "single-gpu"},
+        "dtype": head["dtype"],
+        "data": "synthetic (seeded N(0,1) inputs; fp8: quantised 1x128 / 128x128 to OCP e4m3, fp32 scales)",
+        "config": {"workload": head["name"], **head["dims"], "parallelism": "single-gpu"},
         "frac_mfma_peak": head["frac_mfma_peak"],
-        "roofline": {"bound": head["bound"], "achieved": achieved, "peak": peak, "unit": peak_unit,
-                     "frac": round(achieved / peak, 4), "traffic": None,
-                     "kernel": "gemm_fp8_bs_kernel", "kernel_ms": head["kernel_ms"]},
+        "roofline": {"bound": head["bound"], "achieved": achieved, "peak": peak, "unit": unit,
+                     "frac": round(achieved / peak, 4), "traffic": read_traffic(head["name"]),
+                     "kernel": "gemm_fp8_pipe_kernel" if head["dtype"] == "fp8" else None,
+                     "kernel_ms": head["kernel_ms"]},
         "configs": results,
     }
     if "bf16_gemm_4096" in results:
         r = results["bf16_gemm_4096"]
         line["bf16_gemm_4096"] = {"tflops": r["tflops"], "frac_mfma_peak": r["frac_mfma_peak"],
-                                  "kernel_ms": r["kernel_ms"]}
+                                  "kernel_ms": r["kernel_ms"], "ms_per_step": r["ms_per_step"]}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line))

@@ -1,0 +1,229 @@
+"""Workload runner and rocprofv3 summarisers for the GEMM-family kernels.
+
+Run under the profiler (the program itself follows ``--``)::
+
+    rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o run -- \\
+        python3 -m kore_amd.profiling run <workload> [--iters N]
+    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir> -o run -- \\
+        python3 -m kore_amd.profiling run <workload>
+    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir> -o run -- \\
+        python3 -m kore_amd.profiling copy --mib 256
+
+then, anywhere (no GPU needed), turn the CSV output into the text summaries kept
+under ``profiles/``::
+
+    python3 -m kore_amd.profiling stats <dir> --out profiles/<name>.md --cmd "<command>"
+    python3 -m kore_amd.profiling traffic --workload <w> --kernel <substr> \\
+        --fetch <dir> --write <dir> --copy-fetch <dir> --copy-write <dir> --copy-mib 256 \\
+        --out profiles/hbm_traffic.md --cmd "<commands>"
+
+HBM traffic calibration: FETCH_SIZE / WRITE_SIZE count L2-to-fabric traffic in KiB
+per dispatch.  A plain device copy of a known size (``copy``) reads and writes
+exactly that many bytes, so ``known / counted`` is the factor applied to the
+kernel's counts.  ``bench.py`` reads the resulting ``traffic[...]`` lines.
+"""
+
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import os
+import statistics
+import sys
+
+PROFILES = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "profiles")
+TRAFFIC_FILE = os.path.join(PROFILES, "hbm_traffic.md")
+
+
+# --------------------------------------------------------------------------- #
+# GPU side: the programs rocprofv3 runs
+# --------------------------------------------------------------------------- #
+def _run(workload: str, iters: int, warmup: int) -> None:
+    import torch
+
+    from kore_amd import _lib
+    from kore_amd.workloads import bench_workloads
+
+    _lib.load()
+    wl = bench_workloads()
+    if workload not in wl:
+        raise SystemExit(f"unknown workload {workload!r}; choose from {', '.join(wl)}")
+    fn, _, _, _ = wl[workload](torch.device("cuda:0"))
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    for _ in range(iters):
+        fn()
+    torch.cuda.synchronize()
+    print(f"profiling.run {workload}: {warmup} warm-up + {iters} timed calls done", flush=True)
+
+
+def _copy(mib: int, iters: int) -> None:
+    import torch
+
+    n = mib * 1024 * 1024
+    x = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    y = torch.empty_like(x)
+    for _ in range(iters):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(f"profiling.copy: {iters} copies of {mib} MiB done", flush=True)
+
+
+# --------------------------------------------------------------------------- #
+# CPU side: summaries
+# --------------------------------------------------------------------------- #
+def _one(pattern: str) -> str:
+    hits = sorted(glob.glob(pattern, recursive=True))
+    if not hits:
+        raise SystemExit(f"no file matches {pattern}")
+    return hits[0]
+
+
+def _short(name: str) -> str:
+    """Kernel name without the parameter list and anonymous-namespace noise."""
+    n = name.replace("kore::(anonymous namespace)::", "").replace("kore::", "")
+    if n.startswith("void "):
+        n = n[5:]
+    depth, out = 0, []
+    for ch in n:
+        if ch == "(" and depth == 0:
+            break
+        depth += ch == "<"
+        depth -= ch == ">"
+        out.append(ch)
+    return "".join(out).strip()
+
+
+def kernel_stats(directory: str) -> list[dict]:
+    path = _one(os.path.join(directory, "**", "*kernel_stats.csv"))
+    with open(path) as f:
+        return list(csv.DictReader(f))
+
+
+def counter_values(directory: str, counter: str, kernel_substr: str) -> list[float]:
+    """Per-dispatch values of one counter for the kernels whose name contains
+    ``kernel_substr`` (dimension instances summed)."""
+    path = _one(os.path.join(directory, "**", "*counter_collection.csv"))
+    per = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] != counter or kernel_substr.lower() not in r["Kernel_Name"].lower():
+                continue
+            per[r["Dispatch_Id"]] = per.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"])
+    if not per:
+        raise SystemExit(f"{counter} for {kernel_substr!r} not found in {path}")
+    return [per[k] for k in sorted(per, key=int)]
+
+
+def write_stats(directory: str, out: str, cmd: str, title: str) -> None:
+    rows = kernel_stats(directory)
+    lines = [f"# {title}", "", "Command (from the repository root, on one MI355X):", "", "```", cmd, "```", "",
+             "| kernel | calls | average (us) | min (us) | max (us) | share |", "|---|---|---|---|---|---|"]
+    other_calls, other_ns, other_share = 0, 0.0, 0.0
+    for r in rows:
+        if "kore" not in r["Name"]:  # torch kernels that generate the inputs, copies
+            other_calls += int(r["Calls"])
+            other_ns += float(r["TotalDurationNs"])
+            other_share += float(r["Percentage"])
+            continue
+        lines.append(f"| `{_short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                     f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.1f}% |")
+    if other_calls:
+        lines.append(f"| other (input generation, copies; {other_calls} calls) | {other_calls} | "
+                     f"{other_ns / other_calls / 1e3:.1f} | | | {other_share:.1f}% |")
+    os.makedirs(os.path.dirname(os.path.abspath(out)), exist_ok=True)
+    with open(out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print(f"wrote {out}")
+
+
+def write_traffic(a) -> None:
+    fetch = statistics.median(counter_values(a.fetch, "FETCH_SIZE", a.kernel))
+    write = statistics.median(counter_values(a.write, "WRITE_SIZE", a.kernel))
+    known_kib = a.copy_mib * 1024.0
+    cf = statistics.median(counter_values(a.copy_fetch, "FETCH_SIZE", a.copy_kernel))
+    cw = statistics.median(counter_values(a.copy_write, "WRITE_SIZE", a.copy_kernel))
+    f_fetch, f_write = known_kib / cf, known_kib / cw
+    traffic = (fetch * f_fetch + write * f_write) * 1024.0
+    entry = (f"traffic[{a.workload}] = {traffic:.0f}  # bytes per launch of {a.kernel}: "
+             f"FETCH_SIZE {fetch:.0f} KiB x {f_fetch:.4f} + WRITE_SIZE {write:.0f} KiB x {f_write:.4f}")
+    body = []
+    if os.path.exists(a.out):
+        # keep every other workload's section
+        skip = False
+        with open(a.out) as f:
+            for ln in f:
+                ln = ln.rstrip("\n")
+                if ln.startswith("## "):
+                    skip = ln == f"## {a.workload}"
+                if not skip:
+                    body.append(ln)
+        while body and not body[-1]:
+            body.pop()
+    if not body:
+        body = ["# HBM traffic per launch (rocprofv3 FETCH_SIZE / WRITE_SIZE)", "",
+                "FETCH_SIZE and WRITE_SIZE count L2-to-fabric traffic in KiB per dispatch.  Each is",
+                "scaled by known/counted for a plain device copy of a known size (same counters,",
+                "same session), so the figures are bytes that left or entered the L2s.", ""]
+    body += ["", f"## {a.workload}", "", "Commands:", "", "```", a.cmd, "```", "",
+             f"copy calibration: {a.copy_mib} MiB copy counted FETCH {cf:.0f} KiB, WRITE {cw:.0f} KiB "
+             f"(known {known_kib:.0f} KiB)", "", entry]
+    with open(a.out, "w") as f:
+        f.write("\n".join(body) + "\n")
+    print(entry)
+
+
+def read_traffic(workload: str, path: str = TRAFFIC_FILE):
+    """Bytes per launch recorded for ``workload`` in the traffic summary, or None."""
+    try:
+        with open(path) as f:
+            for ln in f:
+                if ln.startswith(f"traffic[{workload}]"):
+                    return float(ln.split("=", 1)[1].split("#", 1)[0])
+    except OSError:
+        return None
+    return None
+
+
+def main(argv=None) -> int:
+    p = argparse.ArgumentParser(prog="python -m kore_amd.profiling")
+    sub = p.add_subparsers(dest="action", required=True)
+    r = sub.add_parser("run")
+    r.add_argument("workload")
+    r.add_argument("--iters", type=int, default=20)
+    r.add_argument("--warmup", type=int, default=3)
+    c = sub.add_parser("copy")
+    c.add_argument("--mib", type=int, default=256)
+    c.add_argument("--iters", type=int, default=5)
+    s = sub.add_parser("stats")
+    s.add_argument("dir")
+    s.add_argument("--out", required=True)
+    s.add_argument("--cmd", required=True)
+    s.add_argument("--title", default="rocprofv3 kernel-trace summary")
+    t = sub.add_parser("traffic")
+    t.add_argument("--workload", required=True)
+    t.add_argument("--kernel", required=True)
+    t.add_argument("--fetch", required=True)
+    t.add_argument("--write", required=True)
+    t.add_argument("--copy-fetch", required=True)
+    t.add_argument("--copy-write", required=True)
+    t.add_argument("--copy-mib", type=int, default=256)
+    t.add_argument("--copy-kernel", default="copy")
+    t.add_argument("--out", default=TRAFFIC_FILE)
+    t.add_argument("--cmd", required=True)
+    a = p.parse_args(argv)
+    if a.action == "run":
+        _run(a.workload, a.iters, a.warmup)
+    elif a.action == "copy":
+        _copy(a.mib, a.iters)
+    elif a.action == "stats":
+        write_stats(a.dir, a.out, a.cmd, a.title)
+    else:
+        write_traffic(a)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -105,3 +105,58 @@ def moe_inputs(T: int, E: int, topk: int, D: int, I: int, seed: int = 0, device=
         logits = logits + router_bias.to(device)
     tw, ti = route(logits, topk)
     return hidden, w1, w2, tw, ti
+
+
+# --------------------------------------------------------------------------- #
+# Benchmark workloads: one entry per BASELINE configuration (inputs drawn on the
+# device so they are resident in HBM before timing starts).
+# --------------------------------------------------------------------------- #
+def bench_workloads():
+    """Ordered ``name -> builder(device)``; a builder returns ``(fn, op, dims, dtype)``
+    where ``fn()`` runs one step of the operator and ``(op, dims, dtype)`` key the
+    roofline model (``kore_amd.roofline``)."""
+    import kore_amd  # deferred: the package imports this module
+
+    def fp8(M):
+        def build(dev):
+            xq, wq, xs, ws = fp8_inputs(M, 7168, 4096, seed=0, device=dev)
+            return (lambda: kore_amd.gemm_a8w8_blockscale(xq, wq, xs, ws)), "gemm_fp8", \
+                {"M": M, "N": 7168, "K": 4096}, "fp8"
+        return build
+
+    def dense(n):
+        def build(dev):
+            a, b = dense_inputs(n, n, n, seed=0, device=dev)
+            return (lambda: kore_amd.gemm(a, b)), "gemm", {"M": n, "N": n, "K": n}, "bf16"
+        return build
+
+    def fused(act):
+        def build(dev):
+            a, b, bias = fused_inputs(4096, 4096, 4096, seed=0, device=dev)
+            return (lambda: kore_amd.gemm_fused(a, b, bias, act)), "gemm", \
+                {"M": 4096, "N": 4096, "K": 4096}, "fp16"
+        return build
+
+    def batched(dev):
+        a, b = batched_inputs(64, 1024, 1024, 128, seed=0, device=dev)
+        return (lambda: kore_amd.batched_gemm(a, b)), "batched_gemm", \
+            {"B": 64, "M": 1024, "N": 1024, "K": 128}, "bf16"
+
+    def moe(T):
+        def build(dev):
+            args = moe_inputs(T, 8, 2, 4096, 14336, seed=0, device=dev)
+            return (lambda: kore_amd.fused_moe(*args)), "fused_moe", \
+                {"M": T, "E": 8, "topk": 2, "D": 4096, "I": 14336}, "bf16"
+        return build
+
+    w = {"fp8_blockscale_2048x7168x4096": fp8(2048),
+         "bf16_gemm_4096": dense(4096),
+         "bf16_gemm_1024": dense(1024)}
+    for act in ("gelu", "relu", "silu"):
+        w[f"fp16_gemm_bias_{act}_4096"] = fused(act)
+    w["bf16_batched_64x1024x1024x128"] = batched
+    for M in (512, 128, 16):
+        w[f"fp8_blockscale_{M}x7168x4096"] = fp8(M)
+    w["moe_decode_T64"] = moe(64)
+    w["moe_prefill_T4096"] = moe(4096)
+    return w

@@ -1,0 +1,76 @@
+"""CPU tests of the rocprofv3 summarisers (synthetic CSVs in rocprofv3's layout) and
+of the benchmark workload registry."""
+
+from __future__ import annotations
+
+import csv
+import math
+from argparse import Namespace
+from pathlib import Path
+
+from kore_amd import profiling as P
+from kore_amd import roofline as R
+from kore_amd.workloads import bench_workloads
+
+
+def _counters(d: Path, rows):
+    d.mkdir(parents=True)
+    with open(d / "run_counter_collection.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
+        w.writeheader()
+        for r in rows:
+            w.writerow(dict(zip(["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"], r)))
+
+
+def test_traffic_calibration_and_roundtrip(tmp_path):
+    kern = "void kore::(anonymous namespace)::gemm_fp8_pipe_kernel<X>(P)"
+    # two dimension instances per dispatch are summed; the median over dispatches is used
+    _counters(tmp_path / "f", [(1, kern, "FETCH_SIZE", 100), (1, kern, "FETCH_SIZE", 100),
+                               (2, kern, "FETCH_SIZE", 150), (2, kern, "FETCH_SIZE", 150),
+                               (3, "other", "FETCH_SIZE", 9999)])
+    _counters(tmp_path / "w", [(1, kern, "WRITE_SIZE", 50), (2, kern, "WRITE_SIZE", 50)])
+    _counters(tmp_path / "cf", [(7, "__amd_rocclr_copyBuffer", "FETCH_SIZE", 512)])
+    _counters(tmp_path / "cw", [(7, "__amd_rocclr_copyBuffer", "WRITE_SIZE", 1024)])
+    assert P.counter_values(str(tmp_path / "f"), "FETCH_SIZE", "gemm_fp8_pipe") == [200.0, 300.0]
+    out = tmp_path / "traffic.md"
+    a = Namespace(workload="w1", kernel="gemm_fp8_pipe", fetch=str(tmp_path / "f"), write=str(tmp_path / "w"),
+                  copy_fetch=str(tmp_path / "cf"), copy_write=str(tmp_path / "cw"), copy_mib=1,
+                  copy_kernel="copy", out=str(out), cmd="cmd")
+    P.write_traffic(a)
+    # fetch: median 250 KiB x (1024/512); write: 50 KiB x (1024/1024)
+    want = (250 * 2.0 + 50 * 1.0) * 1024
+    assert math.isclose(P.read_traffic("w1", str(out)), want)
+    # a second workload keeps the first; rewriting the first replaces its section
+    a.workload = "w2"
+    P.write_traffic(a)
+    a.workload = "w1"
+    P.write_traffic(a)
+    text = out.read_text()
+    assert text.count("## w1") == 1 and text.count("## w2") == 1
+    assert P.read_traffic("w2", str(out)) == P.read_traffic("w1", str(out))
+    assert P.read_traffic("missing", str(out)) is None
+    assert P.read_traffic("w1", str(tmp_path / "nope.md")) is None
+
+
+def test_short_kernel_names():
+    assert P._short("void kore::(anonymous namespace)::gemm_buf_kernel<kore::BF16, 256, 256>(kore::P)") == \
+        "gemm_buf_kernel<BF16, 256, 256>"
+    assert P._short("kore::(anonymous namespace)::moe_align_kernel(int const*, int)") == "moe_align_kernel"
+
+
+def test_bench_workloads_cover_every_config():
+    w = bench_workloads()
+    assert list(w)[0] == "fp8_blockscale_2048x7168x4096"
+    want = {"bf16_gemm_4096", "bf16_gemm_1024", "fp16_gemm_bias_gelu_4096", "fp16_gemm_bias_relu_4096",
+            "fp16_gemm_bias_silu_4096", "bf16_batched_64x1024x1024x128", "fp8_blockscale_512x7168x4096",
+            "fp8_blockscale_128x7168x4096", "fp8_blockscale_16x7168x4096", "moe_decode_T64", "moe_prefill_T4096"}
+    assert want <= set(w)
+
+
+def test_headline_roofline_figures():
+    """The headline's algorithmic work: 2*2048*7168*4096 FLOPs over (MK + NK) fp8 bytes
+    plus 2MN bf16 output bytes; MFMA-bound at 5 PF."""
+    r = R.roofline("gemm_fp8", {"M": 2048, "N": 7168, "K": 4096}, "fp8")
+    assert r.flops == 2.0 * 2048 * 7168 * 4096
+    assert r.bytes == 2048 * 4096 + 7168 * 4096 + 2 * 2048 * 7168
+    assert r.bound == "mfma"
