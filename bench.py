@@ -55,7 +55,7 @@ class Timer:
         self.steps, self.warmup, self.cold_iters = steps, warmup, cold_iters
         self._flush = None
 
-    def run(self, fn, min_warm_s: float = 0.2):
+    def run(self, fn, min_warm_s: float = 0.5):
         # W warm-up steps, and at least min_warm_s of them so the GPU clocks have
         # ramped before the first timed configuration
         t_w = time.perf_counter()

@@ -117,10 +117,11 @@ int kore_moe_align(const int32_t* topk_ids, int64_t T, int64_t topk, int64_t E,
  *   out[t] = sum_k tw[t,k] * W2[e] @ (silu(W1g[e] @ x_t) * W1u[e] @ x_t),  e = ti[t,k]
  *   hidden [T,D] row stride ldh; w1 [E,2I,D] contiguous (gate rows then up rows);
  *   w2 [E,D,I] contiguous; tw [T,topk] fp32; ti [T,topk] int32; out [T,D] contiguous.
- *   The gated activation h is kept in bf16 between the two grouped GEMMs and the
+ *   The gated activation h travels between the two grouped GEMMs as two bf16 planes
+ *   (hi = bf16(h), lo = bf16(h - hi); the down projection multiplies both), and the
  *   top-k combine is a fixed-order (deterministic) sum.  `workspace` must hold
- *   kore_fused_moe_workspace_bytes(T, topk, E, D, I) bytes.  Requires D % 64 == 0
- *   and I % 64 == 0.
+ *   kore_fused_moe_workspace_bytes(T, topk, E, D, I) bytes.  Requires D % 128 == 0
+ *   and I % 128 == 0 (KORE_EUNSUPPORTED otherwise).
  * Replaces: fused_moe(hidden_states, w1, w2, topk_weight, topk_ids)
  *           kore/tasks/fused_moe_silu_bf16/seed_triton.py:69-86
  */
