@@ -180,10 +180,13 @@ __global__ void __launch_bounds__(kEngineThreads)
 // with scalar selects, not branches: a branch would split the tile loop into blocks
 // and let the compiler sink the promotion FMAs away from the MFMAs they overlap.
 //
-// The 16-byte chunks of a 128-byte row are XOR-swizzled with key(r) = ((r >> 1) & 7)
-// ^ ((r >> 4) & 1), r = row % 32: the 16 rows read by a 16-lane group (64 banks) and
-// the 8 rows of equal r % 4 in a 32-lane group (128 banks) all hit distinct 16-byte
-// bank groups, and the key does not depend on which 32-row block a fragment is in.
+// The 16-byte chunks of a 128-byte row are XOR-swizzled with key(r) = (r ^ (r >> 3)) & 7,
+// r = row % 32: a fragment read (lane l: row l % 32) then hits 8 distinct 16-byte bank
+// groups in every 8-lane pass over 32 banks and 16 distinct ones in every 16-lane pass
+// over 64 banks, and the key does not depend on which 32-row block a fragment is in.
+// (The earlier key ((r >> 1) & 7) ^ ((r >> 4) & 1) gave rows 2j and 2j+1 the same chunk,
+// a 2-way conflict per 8-lane pass that SQ_LDS_BANK_CONFLICT measured at 30% of the
+// LDS-active cycles.)  Weight scales are read from one address (an LDS broadcast).
 //
 // NW waves in a WGM x WGN grid, each owning (256/WGM) x 64 outputs as MI x 2 tiles of
 // 32x32.  A tile's two MFMAs (K 0..63, 64..127) accumulate into one of two rotating
@@ -238,7 +241,7 @@ __device__ __forceinline__ void buf_lds(__amdgpu_buffer_rsrc_t r, uint32_t voff,
   else __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_dst, 4, (int)voff, (int)soff, 0, 0);
 }
 
-__device__ __forceinline__ int f8_key(int r) { return ((r >> 1) & 7) ^ ((r >> 4) & 1); }
+__device__ __forceinline__ int f8_key(int r) { return (r ^ (r >> 3)) & 7; }
 
 // 32 K-consecutive bytes of one row: two 16-byte chunks at their swizzled positions.
 __device__ __forceinline__ i32x8_t lds_frag32(const uint8_t* row, const int (&off)[2]) {
@@ -414,11 +417,11 @@ __global__ void __launch_bounds__(C::NW * 64)
           const uint8_t* ring = lds + C::RING + ((s >> 2) & 1) * 4096 + (s & 3) * 4;
 #pragma unroll
           for (int q = 0; q < MI; ++q) xsv[q] = *(const float*)(ring + (rowA0 + 32 * q + lr) * 16);
-          wsv = *(const float*)(cur + C::WOFF + wblk_rd * C::WCOPY + lane * 16 + (s & 3) * 4);
+          wsv = *(const float*)(cur + C::WOFF + wblk_rd * C::WCOPY + (s & 3) * 4);
         } else {
 #pragma unroll
           for (int q = 0; q < MI; ++q) xsv[q] = *(const float*)(cur + C::XOFF + (rowA0 + 32 * q + lr) * 4);
-          wsv = *(const float*)(cur + C::WOFF + wblk_rd * C::WCOPY + lane * 4);
+          wsv = *(const float*)(cur + C::WOFF + wblk_rd * C::WCOPY);
         }
       }
       if (j == 0 && i + 1 < MI) {
@@ -489,6 +492,209 @@ int launch_fp8_pipe(Fp8Params p, hipStream_t st) {
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// ------------------------------------------------------------------------------
+// Skinny-M kernel (M <= 128): the product is bound by streaming W once from HBM, and
+// a 256-row tile would leave most CUs idle (N / 128 workgroups).  A workgroup owns
+// BN = 32 columns and every row of M (padded to MT); its NW waves split the K blocks
+// (wave w takes blocks w, w+NW, ...), so the grid is N / 32 workgroups that each
+// stream their 32 rows of W exactly once.
+//
+// Each wave has a private ring of S LDS stages (one K block each: MT rows of X, then
+// 32 rows of W, 128 bytes per row) filled by direct-to-LDS buffer loads in which one
+// wave instruction covers 8 whole 128-byte rows (full cache lines: an MFMA-layout
+// register load would split every line over two instructions, which measured 1.5x
+// slower for the weight stream).  Waves share nothing, so a stage is consumed after
+// the wave's own `s_waitcnt vmcnt` and no barrier is needed.  The block's scales
+// travel in the same DMA stream (4-byte loads, one activation scale per lane and the
+// weight scale), so the only memory waits in the loop are those vmcnt waits.  16-byte
+// chunks are XOR swizzled by key(r) = (r ^ (r >> 3)) & 7 so fragment reads are
+// conflict-free.
+//
+// v_mfma_f32_16x16x128_f8f6f4 with the W fragment first: D[n][m], lane l owns column
+// m = l % 16 (one activation scale) and rows n = 4*(l/16) + i of a 16-column block
+// (one weight-scale block, as 16 divides 128).  Each lane's 32 fragment bytes are the
+// K chunks g and 4 + g (g = l / 16) of the block; only the pairing of the two
+// operands' K slots matters for the product.  A block's MFMA starts from zero and is
+// promoted with one FMA by xs[m,kb] * ws[nb,kb], every scale applied exactly once as
+// in the reference oracle.  The per-wave partials are summed through LDS in wave
+// order (fixed order: bit-reproducible) and written as bf16.
+// ------------------------------------------------------------------------------
+template <int MT, int NW, int S>
+struct SkinnyCfg {
+  static constexpr int MT_ = MT, NW_ = NW, S_ = S;
+  static constexpr int BN = 32, NB = 2, MB = MT / 16;
+  static constexpr int XQ = MT / 8, WQ = BN / 8;          // 8-row DMA loads per block
+  static constexpr int SQ = (MT + 63) / 64;                // 64-row activation-scale loads
+  static constexpr int LPB = XQ + WQ + SQ + 1;             // DMA instructions per block
+  static constexpr int XS_OFF = (MT + BN) * 128;           // xs[m] of the block (fp32)
+  static constexpr int WS_OFF = XS_OFF + SQ * 256;         // ws of the block (64 copies)
+  static constexpr int STAGE = WS_OFF + 256;               // bytes
+  static constexpr int RING = NW * S * STAGE;
+  static constexpr int BNP = BN + 4;                       // padded fp32 row of the reduction
+  static constexpr int RED = NW * MT * BNP * 4;
+  static constexpr int LDS = RING > RED ? RING : RED;
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+  static_assert(S >= 1 && S <= 3 && LPB * (S - 1) <= 63, "vmcnt range");
+};
+
+__device__ __forceinline__ int sk_key(int r) { return (r ^ (r >> 3)) & 7; }
+
+template <typename C>
+__global__ void __launch_bounds__(C::NW_ * 64)
+    gemm_fp8_skinny_kernel(const Fp8Params p) {
+  constexpr int MT = C::MT_, NW = C::NW_, S = C::S_, MB = C::MB, NB = C::NB, BN = C::BN;
+  constexpr int XQ = C::XQ, WQ = C::WQ, SQ = C::SQ, LPB = C::LPB, STAGE = C::STAGE, BNP = C::BNP;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[C::LDS];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int n0 = (int)blockIdx.x * BN;
+  const int nk = p.K / 128;
+  const int cnt = nk > wave ? (nk - wave + NW - 1) / NW : 0;  // K blocks of this wave
+
+  // buffer resources: X rows [0, M), this workgroup's 32 rows of W
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.xq, (uint32_t)((int64_t)(p.M - 1) * p.ldx + p.K));
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.wq + (int64_t)n0 * p.ldw, (uint32_t)((BN - 1) * p.ldw + p.K));
+  // DMA load q covers LDS rows 8q .. 8q+7; lane l fetches row 8q + l/8, logical chunk
+  // (l % 8) ^ key(row) into position l % 8
+  uint32_t xoff[XQ], woff[WQ];
+#pragma unroll
+  for (int q = 0; q < XQ; ++q) {
+    const int row = 8 * q + (lane >> 3);
+    xoff[q] = (uint32_t)((int64_t)min(row, p.M - 1) * p.ldx + 16 * ((lane & 7) ^ sk_key(row)));
+  }
+#pragma unroll
+  for (int q = 0; q < WQ; ++q) {
+    const int row = 8 * q + (lane >> 3);
+    woff[q] = (uint32_t)((int64_t)row * p.ldw + 16 * ((lane & 7) ^ sk_key(row)));
+  }
+  const __amdgpu_buffer_rsrc_t rxs =
+      make_rsrc(p.xs, (uint32_t)(((int64_t)(p.M - 1) * p.xs_m + (int64_t)(nk - 1) * p.xs_k + 1) * 4));
+  const __amdgpu_buffer_rsrc_t rws = make_rsrc(
+      p.ws, (uint32_t)(((int64_t)(p.N / 128 - 1) * p.ws_n + (int64_t)(nk - 1) * p.ws_k + 1) * 4));
+  uint32_t xsoff[SQ];
+#pragma unroll
+  for (int q = 0; q < SQ; ++q) xsoff[q] = (uint32_t)((int64_t)min(64 * q + lane, p.M - 1) * p.xs_m * 4);
+  const uint32_t ws_base = (uint32_t)((int64_t)(n0 / 128) * p.ws_n * 4);
+  uint8_t* ring = lds + wave * (S * STAGE);
+
+  // fragment read offsets inside a stage: row R + r, chunks g and 4 + g
+  const int k0 = sk_key(r);  // key(R + r) = (key(r) ^ (R / 8)) & 7 for R % 16 == 0
+
+  // issue the loads of block j into stage slot s (DMA operands, then scales)
+  auto issue = [&](int s, int j) {
+    const uint32_t ko = (uint32_t)(wave + NW * j) * 128u;
+    uint8_t* st = ring + s * STAGE;
+#pragma unroll
+    for (int q = 0; q < XQ; ++q) buf_lds(rx, xoff[q], ko, st + q * 1024, 16);
+#pragma unroll
+    for (int q = 0; q < WQ; ++q) buf_lds(rw, woff[q], ko, st + MT * 128 + q * 1024, 16);
+    const uint32_t kb = (uint32_t)(wave + NW * j);
+#pragma unroll
+    for (int q = 0; q < SQ; ++q) buf_lds(rxs, xsoff[q], kb * (uint32_t)(p.xs_k * 4), st + C::XS_OFF + q * 256, 4);
+    buf_lds(rws, 0u, ws_base + kb * (uint32_t)(p.ws_k * 4), st + C::WS_OFF, 4);
+  };
+
+  f32x4_t acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+    if (s < cnt) issue(s, s);
+  for (int j0 = 0; j0 < cnt; j0 += S) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int j = j0 + s;
+      if (j < cnt) {
+        // blocks issued after j: min(S - 1, cnt - 1 - j)
+        const int later = min(S - 1, cnt - 1 - j);
+        if (S >= 3 && later >= 2) wait_vmcnt<(S >= 3 ? 2 * LPB : 0)>();
+        else if (S >= 2 && later >= 1) wait_vmcnt<(S >= 2 ? LPB : 0)>();
+        else wait_vmcnt<0>();
+        const uint8_t* st = ring + s * STAGE;
+        i32x8_t xf[MB], wf[NB];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const uint8_t* row = st + (mb * 16 + r) * 128;
+          const int key = (k0 ^ (2 * mb)) & 7;
+          const u32x4_t lo = *(const u32x4_t*)(row + ((g ^ key) << 4));
+          const u32x4_t hi = *(const u32x4_t*)(row + (((4 + g) ^ key) << 4));
+          xf[mb] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const uint8_t* row = st + (MT + nb * 16 + r) * 128;
+          const int key = (k0 ^ (2 * nb)) & 7;
+          const u32x4_t lo = *(const u32x4_t*)(row + ((g ^ key) << 4));
+          const u32x4_t hi = *(const u32x4_t*)(row + (((4 + g) ^ key) << 4));
+          wf[nb] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        }
+        float sc[MB];
+        const float wsv = *(const float*)(st + C::WS_OFF);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) sc[mb] = *(const float*)(st + C::XS_OFF + (mb * 16 + r) * 4) * wsv;
+        // the slot is free once its fragments are in registers
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (j + S < cnt) issue(s, j + S);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            const f32x4_t part = mma16_fp8(wf[nb], xf[mb], f32x4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[mb][nb][i] = fmaf(part[i], sc[mb], acc[mb][nb][i]);
+          }
+      }
+    }
+  }
+
+  // ---- cross-wave reduction: red[wave][m][n] over the (now idle) ring, fixed-order sum ----
+  wait_vmcnt<0>();
+  __syncthreads();
+  float* red = (float*)lds;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      *(f32x4_t*)(red + (wave * MT + mb * 16 + r) * BNP + nb * 16 + 4 * g) = acc[mb][nb];
+  __syncthreads();
+  constexpr int ITEMS = MT * BN / 8;  // 8 consecutive columns per item
+  const bool vec = p.vec_store != 0;
+  for (int it = tid; it < ITEMS; it += NW * 64) {
+    const int m = it / (BN / 8), c8 = (it % (BN / 8)) * 8;
+    if (m >= p.M) continue;
+    float sum[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sum[e] = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const f32x4_t a = *(const f32x4_t*)(red + (w * MT + m) * BNP + c8);
+      const f32x4_t b = *(const f32x4_t*)(red + (w * MT + m) * BNP + c8 + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sum[e] += a[e];
+        sum[e + 4] += b[e];
+      }
+    }
+    using Op = MfmaOp<BF16>;
+    const u32x4_t v{Op::pack2(sum[0], sum[1]), Op::pack2(sum[2], sum[3]), Op::pack2(sum[4], sum[5]),
+                    Op::pack2(sum[6], sum[7])};
+    const int gn = n0 + c8;
+    store_row8(p.y + (int64_t)m * p.ldy + gn, gn, p.N, vec, v);
+  }
+}
+
+template <typename C>
+int launch_fp8_skinny(const Fp8Params& p, hipStream_t st) {
+  const dim3 grid((unsigned)(p.N / C::BN)), block(C::NW_ * 64);
+  hipLaunchKernelGGL((gemm_fp8_skinny_kernel<C>), grid, block, 0, st, p);
+  return check_launch("gemm_fp8_skinny_kernel");
+}
+
 }  // namespace
 }  // namespace kore
 
@@ -530,6 +736,16 @@ extern "C" int kore_gemm_a8w8_blockscale(const void* xq, int64_t ldx, const void
   // the pipelined kernels address each tile through 32-bit buffer offsets
   const bool pipe_ok = 256 * ldx + K < (1ll << 31) && 256 * ldw + K < (1ll << 31) &&
                        (M * xs_m + K / 128 * xs_k) * 4 < (1ll << 31) && (N / 128 * ws_n + K / 128 * ws_k) * 4 < (1ll << 31);
+  // the skinny kernel addresses X and a 32-row slab of W through 32-bit buffer offsets
+  const bool skinny_ok = 128 * ldx + K < (1ll << 31) && 32 * ldw + K < (1ll << 31);
+  if (M <= 128 && skinny_ok) {
+    // weight streaming: every CU reads its own 32 columns of W once
+    hipStream_t st = (hipStream_t)stream;
+    if (M <= 16) return launch_fp8_skinny<SkinnyCfg<16, 8, 3>>(p, st);
+    if (M <= 32) return launch_fp8_skinny<SkinnyCfg<32, 8, 2>>(p, st);
+    if (M <= 64) return launch_fp8_skinny<SkinnyCfg<64, 4, 3>>(p, st);
+    return launch_fp8_skinny<SkinnyCfg<128, 2, 3>>(p, st);
+  }
   if (pipe_ok) {
     // four K steps of scales per 16-byte load when scale rows are contiguous, 16-byte
     // aligned and K/128 is a multiple of 4 (so no load runs past a row)

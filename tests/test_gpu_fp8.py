@@ -97,3 +97,36 @@ def test_fp8_rejects_unaligned(gpu):
     xq, wq, xs, ws = W.fp8_inputs(64, 256, 256, seed=0)
     with pytest.raises(ValueError):
         kore_amd.gemm_a8w8_blockscale(xq[:, :200].to(gpu), wq[:, :200].to(gpu), xs.to(gpu), ws.to(gpu))
+
+
+@pytest.mark.parametrize("M", [1, 7, 16, 17, 33, 64, 100, 128])
+@pytest.mark.parametrize("N,K", [(128, 128), (384, 384), (1024, 1152), (256, 2048)])
+def test_fp8_skinny(gpu, M, N, K):
+    """M <= 128 runs the weight-streaming split-K kernel: ragged M (rows padded to 16,
+    32, 64 or 128), K/128 blocks fewer than, not a multiple of, and a multiple of the
+    8 waves that split them."""
+    xq, wq, xs, ws = W.fp8_inputs(M, N, K, seed=M * 7 + K, scale=0.2)
+    out = _run(gpu, xq, wq, xs, ws)
+    ref = matmul_blockscale_ref(xq, wq, xs, ws)
+    verdict(out, ref, "blockscale", "fp8", f"{M}x{N}x{K}")
+    verdict(out, ref, "blockscale_genv", "fp8", f"{M}x{N}x{K} (1e-2)")
+    assert bit_equal(_run(gpu, xq, wq, xs, ws), out)  # fixed-order cross-wave sum
+
+
+@pytest.mark.parametrize("M", [16, 100])
+def test_fp8_skinny_layouts(gpu, M):
+    """Skinny kernel: column-major scales and padded operand rows match the contiguous
+    layout bit for bit; doubling x_scale doubles Y exactly."""
+    N, K = 384, 1536
+    xq, wq, xs, ws = W.fp8_inputs(M, N, K, seed=11)
+    base = _run(gpu, xq, wq, xs, ws)
+    verdict(base, matmul_blockscale_ref(xq, wq, xs, ws), "blockscale", "fp8", f"{M}x{N}x{K}")
+    xs_t = xs.t().contiguous().t()
+    ws_t = ws.t().contiguous().t()
+    assert bit_equal(_run(gpu, xq, wq, xs_t, ws_t), base)
+    pad = torch.zeros(M, K + 128, dtype=xq.dtype)
+    pad[:, :K] = xq
+    padw = torch.zeros(N, K + 256, dtype=wq.dtype)
+    padw[:, :K] = wq
+    assert bit_equal(_run(gpu, pad[:, :K], padw[:, :K], xs, ws), base)
+    assert bit_equal(_run(gpu, xq, wq, xs * 2, ws), base * 2)
