@@ -372,9 +372,20 @@ int dispatch_typed(const GemmDesc& d, hipStream_t stream) {
     // Buffer-load engine: each operand tile must span < 4 GiB of bytes.
     const bool buf_ok = d.K % 64 == 0 && d.sam * 2 * 256 + d.K * 2 < (1ll << 31) &&
                         d.sbn * 2 * 256 + d.K * 2 < (1ll << 31);
-    if (b_kc && big && buf_ok) return launch_buf<T, 256, 256>(d, stream);
-    if (b_kc) return big ? launch_tile<T, B_KC, 256, 256>(d, stream) : launch_tile<T, B_KC, 128, 128>(d, stream);
-    return big ? launch_tile<T, B_NC, 256, 256>(d, stream) : launch_tile<T, B_NC, 128, 128>(d, stream);
+    // Short K (a few K steps per tile, e.g. the batched K=128 shape) is bound by the
+    // output stores: 128x128 tiles (64 KiB LDS) let two workgroups share a CU, so one
+    // tile's epilogue overlaps the next tile's loads.  Fewer than 128 tiles of 128x128
+    // (1024^3 has 64) leave most CUs idle: 64x64 tiles then.
+    const int64_t mid_tiles = ((d.M + 127) / 128) * ((d.N + 127) / 128) * d.batch;
+    const bool short_k = d.K <= 256;
+    const bool small = mid_tiles < 128;
+    if (b_kc && big && buf_ok && !short_k) return launch_buf<T, 256, 256>(d, stream);
+    if (b_kc) {
+      if (big && !short_k) return launch_tile<T, B_KC, 256, 256>(d, stream);
+      return small ? launch_tile<T, B_KC, 64, 64>(d, stream) : launch_tile<T, B_KC, 128, 128>(d, stream);
+    }
+    if (big && !short_k) return launch_tile<T, B_NC, 256, 256>(d, stream);
+    return small ? launch_tile<T, B_NC, 64, 64>(d, stream) : launch_tile<T, B_NC, 128, 128>(d, stream);
   }
   return launch_generic<T>(d, stream);
 }

@@ -201,9 +201,9 @@ __global__ void __launch_bounds__(kEngineThreads)
 // over the next W tiles (W = NT with three slots: one to two stages of latency; the
 // remaining tiles of the stage with two slots: one stage).
 // ------------------------------------------------------------------------------
-template <int BN_, int NW_, int NSLOT_, bool XS4_>
+template <int BM_, int BN_, int NW_, int NSLOT_, bool XS4_>
 struct F8Cfg {
-  static constexpr int BM = 256, BN = BN_, NW = NW_, NSLOT = NSLOT_;
+  static constexpr int BM = BM_, BN = BN_, NW = NW_, NSLOT = NSLOT_;
   static constexpr bool XS4 = XS4_;
   static constexpr int NB = BN / 128;         // weight-scale blocks per tile
   static constexpr int WGN = BN / 64, WGM = NW / WGN;
@@ -215,8 +215,9 @@ struct F8Cfg {
   static_assert(MI >= 2, "the barrier tile follows the last read of the current slot");
   static constexpr int AQ = (BM / 8) / NW, BQ = (BN / 8) / NW;  // 8-row loads per wave
   static_assert(AQ * NW * 8 == BM && BQ * NW * 8 == BN, "row loads cover the tile");
-  // scale loads per wave: 4 waves each load 64 xs rows and the ws copies; 8 waves:
-  // waves 0-3 xs, waves 4-7 ws (block (w-4) % NB)
+  // scale loads per wave: 4 waves each load 64 xs rows (rows past the tile are
+  // clamped and never read) and the ws copies; 8 waves: waves 0-3 xs, waves 4-7 ws
+  // (block (w-4) % NB)
   static constexpr int SQ = NW == 4 ? 2 : 1;
   static_assert(NW == 8 || NB == 1, "4-wave tiles have one weight-scale block");
   static constexpr int LPS = AQ + BQ + SQ;
@@ -753,12 +754,20 @@ extern "C" int kore_gemm_a8w8_blockscale(const void* xq, int64_t ldx, const void
                      (K / 128) % 4 == 0;
     hipStream_t st = (hipStream_t)stream;
     // 256x256 tiles halve LDS and L2 traffic per MFMA but need enough of them to
-    // occupy the 256 CUs; otherwise 256x128 tiles (three LDS slots)
+    // occupy the 256 CUs; then 256x128 tiles (three LDS slots); with fewer than that,
+    // 128x128 tiles on 4 waves (four slots) double the tile count again
     const int64_t tiles256 = (M + 255) / 256 * (N / 256);
+    const int64_t tiles256x128 = (M + 255) / 256 * (N / 128);
     if (N % 256 == 0 && tiles256 >= 192) {
-      return xs4 ? launch_fp8_pipe<F8Cfg<256, 8, 2, true>>(p, st) : launch_fp8_pipe<F8Cfg<256, 8, 2, false>>(p, st);
+      return xs4 ? launch_fp8_pipe<F8Cfg<256, 256, 8, 2, true>>(p, st)
+                 : launch_fp8_pipe<F8Cfg<256, 256, 8, 2, false>>(p, st);
     }
-    return xs4 ? launch_fp8_pipe<F8Cfg<128, 8, 3, true>>(p, st) : launch_fp8_pipe<F8Cfg<128, 8, 3, false>>(p, st);
+    if (tiles256x128 >= 192) {
+      return xs4 ? launch_fp8_pipe<F8Cfg<256, 128, 8, 3, true>>(p, st)
+                 : launch_fp8_pipe<F8Cfg<256, 128, 8, 3, false>>(p, st);
+    }
+    return xs4 ? launch_fp8_pipe<F8Cfg<128, 128, 4, 4, true>>(p, st)
+               : launch_fp8_pipe<F8Cfg<128, 128, 4, 4, false>>(p, st);
   }
   hipLaunchKernelGGL((gemm_fp8_bs_kernel<BM, BN>), dim3((unsigned)blocks), dim3(kEngineThreads), 0,
                      (hipStream_t)stream, p);

@@ -18,7 +18,9 @@
 //  4. moe_combine_kernel: out[t] = bf16(sum_k Yw[t*topk + k]) in fixed k order over
 //     the slots whose id is in [0, E): no atomics, bit-reproducible.
 // Grids are sized for the worst case (every expert adds < 1 block of padding) and
-// blocks past the real end exit after reading offsets[E].
+// blocks past the real end exit after reading offsets[E].  With few slots per expert
+// (decode) blocks are 32 rows and both GEMMs stream weights on a deep direct-to-LDS
+// ring (moe_decode_kernel), the down projection split in two along K.
 #include "../../include/kore_amd.h"
 #include "kore_common.hpp"
 #include "tile_engine.hpp"
@@ -133,6 +135,7 @@ struct MoeGemmParams {
   int64_t w_rstride;      // elements between rows of w[e]
   int max_mblocks, ntiles;
   int abm;                // rows per aligned block of the sorted slot list
+  int ksplit;             // K splits (down decode): split k writes Yw + k*S*D
 };
 
 enum { MOE_GATEUP = 0, MOE_DOWN = 1 };
@@ -325,12 +328,79 @@ __global__ void __launch_bounds__(256)
   moe_epilogue<MODE, MI, NI, E::WROWS, E::WCOLS>(acc, lds, p, pos0, n0, wm, wn, wave, lane);
 }
 
+// Decode path (32-row blocks): weight streaming on the skinny ring engine.  Grid =
+// ksplit x ntiles x max_mblocks; a workgroup multiplies one 32-slot block by BN rows
+// of its expert's weights over K / ksplit, so w1/w2 are streamed once per block with
+// NSLOT-1 stages in flight per CU.  The down projection splits K so its grid (32
+// column tiles per block) covers the CUs; split k writes its own Yw slab, summed in
+// fixed order by the combine.
+template <int MODE, int BN, int NSLOT>
+__global__ void __launch_bounds__(256)
+    moe_decode_kernel(const MoeGemmParams p) {
+  constexpr int AP = (MODE == MOE_DOWN) ? 2 : 1;
+  using E = SkinnyRingEngine<BF16, BN, AP, NSLOT>;
+  constexpr int NI = E::NI;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int mb = bid % p.max_mblocks, rest = bid / p.max_mblocks;
+  const int nt = rest % p.ntiles, ks = rest / p.ntiles;
+  const int total = p.offsets[p.E];
+  if (mb * E::BM >= total) return;  // uniform: the whole workgroup leaves
+  const int e = p.block_expert[(mb * E::BM) / p.abm];
+  const int pos0 = mb * E::BM;
+
+  E eng;
+  int n0;
+  const int ar = E::a_row(wave, lane);
+  if constexpr (MODE == MOE_GATEUP) {
+    eng.ra = make_rsrc(p.x, (uint32_t)((int64_t)p.T * p.ldx * 2));
+    const int sl = p.sorted[pos0 + ar];
+    const int64_t row = (sl < p.S) ? sl / p.topk : 0;  // padding rows read token 0; never stored
+    eng.a_voff = (uint32_t)((row * p.ldx + 8 * E::chunk(ar, lane)) * 2);
+    n0 = nt * (BN / 2);
+    const int I = p.Nout;
+    const uint16_t* W = p.w + (int64_t)e * p.w_estride;
+    eng.rb = make_rsrc(W, (uint32_t)((int64_t)2 * I * p.w_rstride * 2));
+#pragma unroll
+    for (int j = 0; j < E::BJ; ++j) {
+      // each wave's WCOLS rows: gate rows of its WCOLS/2 columns, then the up rows
+      const int r = E::b_row(wave, lane, j);
+      const int q = r / E::WCOLS, within = r % E::WCOLS;
+      const int half = within / (E::WCOLS / 2);
+      const int col = n0 + q * (E::WCOLS / 2) + within % (E::WCOLS / 2);
+      eng.b_voff[j] = (uint32_t)(((int64_t)(half * I + col) * p.w_rstride + 8 * E::chunk(r, lane)) * 2);
+    }
+  } else {
+    const uint32_t tile_bytes = (uint32_t)((int64_t)E::BM * p.ldx * 2);
+    eng.ra = make_rsrc(p.x + (int64_t)pos0 * p.ldx, tile_bytes);
+    eng.ra2 = make_rsrc(p.h_lo + (int64_t)pos0 * p.ldx, tile_bytes);
+    eng.a_voff = (uint32_t)(((int64_t)ar * p.ldx + 8 * E::chunk(ar, lane)) * 2);
+    n0 = nt * BN;
+    const uint16_t* W = p.w + (int64_t)e * p.w_estride + (int64_t)n0 * p.w_rstride;
+    eng.rb = make_rsrc(W, (uint32_t)((int64_t)BN * p.w_rstride * 2));
+#pragma unroll
+    for (int j = 0; j < E::BJ; ++j) {
+      const int r = E::b_row(wave, lane, j);
+      eng.b_voff[j] = (uint32_t)(((int64_t)r * p.w_rstride + 8 * E::chunk(r, lane)) * 2);
+    }
+  }
+  const int kper = p.K / p.ksplit;
+  f32x16_t acc[1][NI];
+  E::zero(acc);
+  eng.mainloop(lds, ks * kper, (ks + 1) * kper, acc);
+  MoeGemmParams q = p;
+  q.yw = p.yw + (int64_t)ks * p.S * p.Nout;
+  moe_epilogue<MODE, 1, NI, E::BM, E::WCOLS>(acc, lds, q, pos0, n0, 0, wave, wave, lane);
+}
+
 // ------------------------------------------------------------------------------
 // 4. combine
 // ------------------------------------------------------------------------------
 __global__ void __launch_bounds__(256)
     moe_combine_kernel(const float* __restrict__ yw, const int32_t* __restrict__ ids, uint16_t* __restrict__ out,
-                       int T, int D, int topk, int E) {
+                       int T, int D, int topk, int E, int ksplit) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // one thread per 8 outputs
   const int per_row = D / 8;
   if (idx >= (int64_t)T * per_row) return;
@@ -339,12 +409,14 @@ __global__ void __launch_bounds__(256)
   for (int k = 0; k < topk; ++k) {
     const int e = ids[t * topk + k];
     if (e < 0 || e >= E) continue;
-    const float* src = yw + ((int64_t)t * topk + k) * D + d0;
-    const f32x4_t a = *(const f32x4_t*)src, b = *(const f32x4_t*)(src + 4);
+    for (int sp = 0; sp < ksplit; ++sp) {
+      const float* src = yw + ((int64_t)sp * T * topk + (int64_t)t * topk + k) * D + d0;
+      const f32x4_t a = *(const f32x4_t*)src, b = *(const f32x4_t*)(src + 4);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      s[q] += a[q];
-      s[4 + q] += b[q];
+      for (int q = 0; q < 4; ++q) {
+        s[q] += a[q];
+        s[4 + q] += b[q];
+      }
     }
   }
   using Op = MfmaOp<BF16>;
@@ -364,6 +436,9 @@ inline int64_t align_capacity(int64_t S, int64_t E, int64_t block) {
 
 // Block size of the grouped GEMMs: skinny blocks when experts see few rows.
 inline int moe_block_rows(int64_t S, int64_t E) { return (S <= 32 * E * 2) ? 32 : 256; }
+
+// K splits of the down projection: 2 on the decode path (32-row blocks).
+inline int moe_down_ksplit(int64_t S, int64_t E) { return moe_block_rows(S, E) == 32 ? 2 : 1; }
 
 struct MoeWorkspace {
   int32_t* offsets;
@@ -391,7 +466,7 @@ inline MoeWorkspace carve(void* base, int64_t T, int64_t topk, int64_t E, int64_
   const size_t o_blk = take(sizeof(int32_t) * (cap / BM));
   const size_t o_h = take(sizeof(uint16_t) * cap * I);
   const size_t o_hlo = take(sizeof(uint16_t) * cap * I);
-  const size_t o_yw = take(sizeof(float) * S * D);
+  const size_t o_yw = take(sizeof(float) * S * D * moe_down_ksplit(S, E));
   char* b = (char*)base;
   w.offsets = (int32_t*)(b + o_off);
   w.sorted = (int32_t*)(b + o_sorted);
@@ -413,6 +488,16 @@ int launch_moe_gemm(MoeGemmParams p, int64_t cap, hipStream_t st) {
   return check_launch(MODE == MOE_GATEUP ? "moe_gateup_kernel" : "moe_down_kernel");
 }
 
+
+template <int MODE, int BN, int NSLOT>
+int launch_moe_decode(MoeGemmParams p, int64_t cap, hipStream_t st) {
+  p.ntiles = (MODE == MOE_GATEUP) ? p.Nout / (BN / 2) : p.Nout / BN;
+  p.max_mblocks = (int)(cap / 32);
+  const int64_t blocks = (int64_t)p.max_mblocks * p.ntiles * p.ksplit;
+  if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "fused_moe: grid too large");
+  hipLaunchKernelGGL((moe_decode_kernel<MODE, BN, NSLOT>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+  return check_launch(MODE == MOE_GATEUP ? "moe_gateup_decode_kernel" : "moe_down_decode_kernel");
+}
 
 template <int MODE, int BM, int BN>
 int launch_moe_buf(MoeGemmParams p, int64_t cap, hipStream_t st) {
@@ -490,6 +575,7 @@ extern "C" int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, c
   p.h_lo = ws.h_lo;
   p.yw = ws.yw;
   p.abm = BM;
+  p.ksplit = 1;
   p.E = (int)E;
   p.T = (int)T;
   p.S = (int)S;
@@ -504,7 +590,8 @@ extern "C" int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, c
   p.w_rstride = D;
   // buffer-load engine needs operand byte ranges below 4 GiB and K % 64 == 0
   const bool buf_ok = T * ldh * 2 < (1ll << 32) && 2 * I * D * 2 < (1ll << 32) && D % 64 == 0 && I % 64 == 0;
-  rc = (BM == 32) ? launch_moe_gemm<MOE_GATEUP, 32, 256, 1, 4>(p, cap, st)
+  rc = (BM == 32 && buf_ok) ? launch_moe_decode<MOE_GATEUP, 256, 4>(p, cap, st)
+       : (BM == 32) ? launch_moe_gemm<MOE_GATEUP, 32, 256, 1, 4>(p, cap, st)
        : buf_ok   ? launch_moe_buf<MOE_GATEUP, 256, 256>(p, cap, st)
                   : launch_moe_gemm<MOE_GATEUP, 256, 256, 2, 2>(p, cap, st);
   if (rc) return rc;
@@ -518,13 +605,22 @@ extern "C" int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, c
   p.w_rstride = I;
   // two A planes double the A tile: prefill runs 128-row tiles (halves of a 256-row
   // aligned block) to stay inside the 160 KiB LDS budget.
-  if (BM == 32) rc = launch_moe_gemm<MOE_DOWN, 32, 128, 1, 4>(p, cap, st);
-  else if (buf_ok && D % 256 == 0) rc = launch_moe_buf<MOE_DOWN, 128, 256>(p, cap, st);
-  else if (D % 256 == 0) rc = launch_moe_gemm<MOE_DOWN, 128, 256, 2, 2>(p, cap, st);
-  else rc = launch_moe_gemm<MOE_DOWN, 128, 128, 2, 2>(p, cap, st);
+  const int ksplit = moe_down_ksplit(S, E);
+  if (BM == 32 && buf_ok) {
+    p.ksplit = ksplit;  // I % 128 == 0, so every split is a multiple of 64
+    rc = launch_moe_decode<MOE_DOWN, 128, 6>(p, cap, st);
+  } else if (BM == 32) {
+    rc = launch_moe_gemm<MOE_DOWN, 32, 128, 1, 4>(p, cap, st);
+  } else if (buf_ok && D % 256 == 0) {
+    rc = launch_moe_buf<MOE_DOWN, 128, 256>(p, cap, st);
+  } else if (D % 256 == 0) {
+    rc = launch_moe_gemm<MOE_DOWN, 128, 256, 2, 2>(p, cap, st);
+  } else {
+    rc = launch_moe_gemm<MOE_DOWN, 128, 128, 2, 2>(p, cap, st);
+  }
   if (rc) return rc;
   const int64_t threads = T * (D / 8);
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, ws.yw, topk_ids,
-                     (uint16_t*)out, (int)T, (int)D, (int)topk, (int)E);
+                     (uint16_t*)out, (int)T, (int)D, (int)topk, (int)E, p.ksplit);
   return check_launch("moe_combine_kernel");
 }

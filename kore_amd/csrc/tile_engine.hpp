@@ -248,146 +248,13 @@ __device__ __forceinline__ void store_row8(uint16_t* dst, int gn, int N, bool ve
 namespace kore {
 
 // ---------------------------------------------------------------------------------
-// Direct-to-LDS engine (K-contiguous operands).
-//
-// NW = WM*WN waves (8 -> two waves per SIMD, so one wave's LDS/global waits are
-// covered by the other's MFMAs).  Operand tiles are filled with
-// global_load_lds_dwordx4: one wave instruction writes 64 x 16 bytes = 8 consecutive
-// 128-byte LDS rows, lane l landing at row l/8, chunk l%8.  The XOR swizzle is
-// applied on the source side: lane l fetches logical chunk (l%8) ^ swz8(row), so the
-// LDS image is identical to the register-staged engine's and no staging VGPRs are
-// needed.  Lanes whose chunk lies past K read a zero page instead (no branches).
-// Fragments are double buffered in registers across the four 16-wide K sub-steps.
+// Direct-to-LDS helpers.  `buffer_load_dwordx4 ... lds` writes one wave instruction's
+// 64 x 16 bytes to 1 KiB of consecutive LDS (lane l at byte 16*l), so a 128-byte LDS
+// row gets 8 lanes; the XOR swizzle is applied on the source side (lane l fetches
+// logical chunk (l % 8) ^ swz8(row)), which gives the same LDS image as the
+// register-staged engine.  vmcnt counts these loads like any other vector load.
 // ---------------------------------------------------------------------------------
-__device__ const u32x4_t kZeroPage[4] = {};
-
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-__device__ __forceinline__ void gl_lds16(const void* src, uint16_t* lds_dst) {
-  __builtin_amdgcn_global_load_lds(src, (lds_ptr_t)lds_dst, 16, 0, 0);
-}
-
-__device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-template <typename T, int BM, int BN, int WM, int WN>
-struct DLEngine {
-  static constexpr int NW = WM * WN;
-  static constexpr int NT = 64 * NW;
-  static constexpr int WROWS = BM / WM, WCOLS = BN / WN;
-  static constexpr int MI = WROWS / 32, NI = WCOLS / 32;
-  static_assert(MI >= 1 && NI >= 1 && WROWS % 32 == 0 && WCOLS % 32 == 0, "wave tile is a multiple of 32x32");
-  static constexpr int A_ELEMS = BM * kBK, B_ELEMS = BN * kBK;
-  static constexpr int STAGE = A_ELEMS + B_ELEMS;
-  static constexpr int LDS_ELEMS = 2 * STAGE;
-  static constexpr int AJ = BM / 8 / NW, BJ = BN / 8 / NW;  // wave-loads per wave per stage
-  static_assert(AJ * 8 * NW == BM && BJ * 8 * NW == BN, "8-row wave loads must cover the tile");
-
-  // Row (0..BM) of the tile that lane `lane` of wave `wave` fills in wave-load j, and
-  // the logical 16-byte chunk it fetches for that row.
-  static __device__ __forceinline__ int a_row(int wave, int lane, int j) { return (wave + NW * j) * 8 + (lane >> 3); }
-  static __device__ __forceinline__ int b_row(int wave, int lane, int j) { return (wave + NW * j) * 8 + (lane >> 3); }
-  static __device__ __forceinline__ int chunk(int row, int lane) { return (lane & 7) ^ swz8(row); }
-
-  // Per-lane source of each wave-load: row pointer + 8 * chunk(row, lane) elements.
-  const uint16_t* a_src[AJ];
-  const uint16_t* b_src[BJ];
-  int a_k[AJ], b_k[BJ];  // element offset of the lane's chunk inside a K step (8*chunk)
-
-  __device__ __forceinline__ void issue(uint16_t* lds, int stage, int k0, int K, int wave) {
-    uint16_t* sA = lds + stage * STAGE;
-    uint16_t* sB = sA + A_ELEMS;
-    const bool full = k0 + kBK <= K;
-#pragma unroll
-    for (int j = 0; j < AJ; ++j) {
-      const void* src = full || (k0 + a_k[j] < K) ? (const void*)(a_src[j] + k0) : (const void*)kZeroPage;
-      gl_lds16(src, sA + (wave + NW * j) * 8 * kBK);
-    }
-#pragma unroll
-    for (int j = 0; j < BJ; ++j) {
-      const void* src = full || (k0 + b_k[j] < K) ? (const void*)(b_src[j] + k0) : (const void*)kZeroPage;
-      gl_lds16(src, sB + (wave + NW * j) * 8 * kBK);
-    }
-  }
-
-  static __device__ __forceinline__ void zero(f32x16_t (&acc)[MI][NI]) {
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-      for (int j = 0; j < NI; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-  }
-
-  __device__ __forceinline__ void mainloop(uint16_t* lds, int K, f32x16_t (&acc)[MI][NI]) {
-    using Op = MfmaOp<T>;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / WN, wn = wave % WN;
-    const int lr = lane & 31, hh = lane >> 5;
-    int offA[2][4], offB[2][4];
-#pragma unroll
-    for (int par = 0; par < 2; ++par) {
-      const int qa = (wm * MI + par) & 1, qb = (wn * NI + par) & 1;
-      const int swa = ((lr & 7) ^ (lr >> 3) ^ (4 * qa)) & 7;
-      const int swb = ((lr & 7) ^ (lr >> 3) ^ (4 * qb)) & 7;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        offA[par][ks] = lr * kBK + (((2 * ks + hh) ^ swa) << 3);
-        offB[par][ks] = lr * kBK + (((2 * ks + hh) ^ swb) << 3);
-      }
-    }
-    const int rowA0 = wm * WROWS, rowB0 = wn * WCOLS;
-    const int nk = (K + kBK - 1) / kBK;
-    issue(lds, 0, 0, K, wave);
-    wait_vmem_all();
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-      const int cur = kt & 1;
-      if (kt + 1 < nk) issue(lds, cur ^ 1, (kt + 1) * kBK, K, wave);
-      const uint16_t* sA = lds + cur * STAGE + rowA0 * kBK;
-      const uint16_t* sB = lds + cur * STAGE + A_ELEMS + rowB0 * kBK;
-      u32x4_t af[2][MI], bfr[2][NI];
-#pragma unroll
-      for (int i = 0; i < MI; ++i) af[0][i] = *(const u32x4_t*)(sA + i * 32 * kBK + offA[i & 1][0]);
-#pragma unroll
-      for (int j = 0; j < NI; ++j) bfr[0][j] = *(const u32x4_t*)(sB + j * 32 * kBK + offB[j & 1][0]);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const int c = ks & 1, n = c ^ 1;
-        if (ks < 3) {
-#pragma unroll
-          for (int i = 0; i < MI; ++i) af[n][i] = *(const u32x4_t*)(sA + i * 32 * kBK + offA[i & 1][ks + 1]);
-#pragma unroll
-          for (int j = 0; j < NI; ++j) bfr[n][j] = *(const u32x4_t*)(sB + j * 32 * kBK + offB[j & 1][ks + 1]);
-        }
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-#pragma unroll
-          for (int j = 0; j < NI; ++j) acc[i][j] = Op::mma32(bfr[c][j], af[c][i], acc[i][j]);
-      }
-      wait_vmem_all();
-      __syncthreads();
-    }
-  }
-};
-
-}  // namespace kore
-
-namespace kore {
-
-// ---------------------------------------------------------------------------------
-// Ring engine: direct-to-LDS loads into an NSTAGE-deep ring of 32-wide K stages.
-//
-// Global latency on MI355X under GEMM load is ~1 us, longer than one K step of MFMA
-// work, so stages are issued NSTAGE-1 steps ahead (3 x 32 KiB in flight per CU for a
-// 256x256 tile) and a stage is consumed after `s_waitcnt vmcnt(n)` for the loads
-// issued later plus one barrier.  LDS rows are 64 bytes (32 x 16-bit); chunk c of
-// row r lives at chunk c ^ swz4(r), swz4(r) = ((r >> 1) ^ (r >> 3)) & 3, which keeps
-// the 32 fragment rows read by a half-wave on distinct banks for 32- and 64-bank
-// LDS.  For rows R + lr with R % 32 == 0, swz4(R + lr) == swz4(lr).
-// ---------------------------------------------------------------------------------
-constexpr int kRK = 32;  // K elements per ring stage (64-byte rows)
-
-__device__ __forceinline__ int swz4(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -396,7 +263,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 // Execution barrier without the workgroup release fence of __syncthreads(): that
 // fence waits for *all* outstanding vector-memory operations (vmcnt(0)), which would
-// drain the prefetched ring stages at every K step.  Callers order their own memory:
+// drain prefetched stages at every K step.  Callers order their own memory:
 // direct-to-LDS loads via wait_vmcnt<N>() before the barrier.  The empty asm
 // statements keep the compiler from moving LDS accesses across it.
 __device__ __forceinline__ void exec_barrier() {
@@ -405,408 +272,6 @@ __device__ __forceinline__ void exec_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <typename T, int BM, int BN, int WM, int WN, int NSTAGE>
-struct RingEngine {
-  static constexpr int NW = WM * WN;
-  static constexpr int NT = 64 * NW;
-  static constexpr int WROWS = BM / WM, WCOLS = BN / WN;
-  static constexpr int MI = WROWS / 32, NI = WCOLS / 32;
-  static_assert(MI >= 1 && NI >= 1 && WROWS % 32 == 0 && WCOLS % 32 == 0, "wave tile is a multiple of 32x32");
-  static constexpr int A_ELEMS = BM * kRK, B_ELEMS = BN * kRK;
-  static constexpr int STAGE = A_ELEMS + B_ELEMS;
-  static constexpr int LDS_ELEMS = NSTAGE * STAGE;
-  static constexpr int AJ = BM / 16 / NW, BJ = BN / 16 / NW;  // 16-row wave loads per wave per stage
-  static_assert(AJ * 16 * NW == BM && BJ * 16 * NW == BN, "16-row wave loads must cover the tile");
-  static constexpr int LPS = AJ + BJ;  // load instructions per wave per stage
-  static_assert(NSTAGE >= 2 && NSTAGE <= 4, "2..4 stages");
-
-  static __device__ __forceinline__ int a_row(int wave, int lane, int j) { return (wave + NW * j) * 16 + (lane >> 2); }
-  static __device__ __forceinline__ int b_row(int wave, int lane, int j) { return (wave + NW * j) * 16 + (lane >> 2); }
-  static __device__ __forceinline__ int chunk(int row, int lane) { return (lane & 3) ^ swz4(row); }
-
-  const uint16_t* a_src[AJ];
-  const uint16_t* b_src[BJ];
-  int a_k[AJ], b_k[BJ];
-
-  __device__ __forceinline__ void issue(uint16_t* lds, int slot, int k0, int K, int wave) {
-    uint16_t* sA = lds + slot * STAGE;
-    uint16_t* sB = sA + A_ELEMS;
-    const bool full = k0 + kRK <= K;
-#pragma unroll
-    for (int j = 0; j < AJ; ++j) {
-      const void* src = full || (k0 + a_k[j] < K) ? (const void*)(a_src[j] + k0) : (const void*)kZeroPage;
-      gl_lds16(src, sA + (wave + NW * j) * 16 * kRK);
-    }
-#pragma unroll
-    for (int j = 0; j < BJ; ++j) {
-      const void* src = full || (k0 + b_k[j] < K) ? (const void*)(b_src[j] + k0) : (const void*)kZeroPage;
-      gl_lds16(src, sB + (wave + NW * j) * 16 * kRK);
-    }
-  }
-
-  // Issue load q (0 .. LPS-1) of a stage: A wave-loads first, then B.
-  __device__ __forceinline__ void issue_one(uint16_t* lds, int slot, int k0, int K, int wave, int q) {
-    uint16_t* sA = lds + slot * STAGE;
-    uint16_t* sB = sA + A_ELEMS;
-    const bool full = k0 + kRK <= K;
-    if (q < AJ) {
-      const void* src = full || (k0 + a_k[q] < K) ? (const void*)(a_src[q] + k0) : (const void*)kZeroPage;
-      gl_lds16(src, sA + (wave + NW * q) * 16 * kRK);
-    } else {
-      const int j = q - AJ;
-      const void* src = full || (k0 + b_k[j] < K) ? (const void*)(b_src[j] + k0) : (const void*)kZeroPage;
-      gl_lds16(src, sB + (wave + NW * j) * 16 * kRK);
-    }
-  }
-
-  // Wait until the loads of the stage about to be consumed are done, given that
-  // `later` more stages have been issued after it.
-  static __device__ __forceinline__ void wait_stage(int later) {
-    if (later >= 2) wait_vmcnt<2 * LPS>();
-    else if (later == 1) wait_vmcnt<LPS>();
-    else wait_vmcnt<0>();
-  }
-
-  static __device__ __forceinline__ void zero(f32x16_t (&acc)[MI][NI]) {
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-      for (int j = 0; j < NI; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-  }
-
-  __device__ __forceinline__ void mainloop(uint16_t* lds, int K, f32x16_t (&acc)[MI][NI]) {
-    using Op = MfmaOp<T>;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / WN, wn = wave % WN;
-    const int lr = lane & 31, hh = lane >> 5;
-    const int sw = swz4(lr);
-    const int off0 = lr * kRK + (((0 + hh) ^ sw) << 3);
-    const int off1 = lr * kRK + (((2 + hh) ^ sw) << 3);
-    const int rowA0 = wm * WROWS, rowB0 = wn * WCOLS;
-    const int nk = (K + kRK - 1) / kRK;
-#pragma unroll
-    for (int s = 0; s < NSTAGE - 1; ++s)
-      if (s < nk) issue(lds, s, s * kRK, K, wave);
-    for (int kt = 0; kt < nk; ++kt) {
-      wait_stage(min(NSTAGE - 2, nk - 1 - kt));
-      exec_barrier();
-      const int slot = kt % NSTAGE;
-      const uint16_t* sA = lds + slot * STAGE + rowA0 * kRK;
-      const uint16_t* sB = lds + slot * STAGE + A_ELEMS + rowB0 * kRK;
-      u32x4_t af[2][MI], bfr[2][NI];
-#pragma unroll
-      for (int i = 0; i < MI; ++i) af[0][i] = *(const u32x4_t*)(sA + i * 32 * kRK + off0);
-#pragma unroll
-      for (int j = 0; j < NI; ++j) bfr[0][j] = *(const u32x4_t*)(sB + j * 32 * kRK + off0);
-#pragma unroll
-      for (int i = 0; i < MI; ++i) af[1][i] = *(const u32x4_t*)(sA + i * 32 * kRK + off1);
-#pragma unroll
-      for (int j = 0; j < NI; ++j) bfr[1][j] = *(const u32x4_t*)(sB + j * 32 * kRK + off1);
-      // The next stage's direct loads are spread through the MFMA stream (one load per
-      // MFMA group) so the per-CU request queue never fills: a full queue stalls the
-      // issuing wave and would serialise memory and compute.
-      const bool more = kt + NSTAGE - 1 < nk;
-      const int nslot = (kt + NSTAGE - 1) % NSTAGE, nk0 = (kt + NSTAGE - 1) * kRK;
-      constexpr int NMMA = 2 * MI * NI;
-      constexpr int GROUP = (NMMA + LPS - 1) / LPS;
-#pragma unroll
-      for (int m = 0; m < NMMA; ++m) {
-        if (m % GROUP == 0 && m / GROUP < LPS) {
-          __builtin_amdgcn_sched_barrier(0);
-          if (more) issue_one(lds, nslot, nk0, K, wave, m / GROUP);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        const int ks = m / (MI * NI), i = (m / NI) % MI, j = m % NI;
-        acc[i][j] = Op::mma32(bfr[ks][j], af[ks][i], acc[i][j]);
-      }
-    }
-    __syncthreads();  // every wave is done with the ring before the caller reuses LDS
-  }
-};
-
-}  // namespace kore
-
-namespace kore {
-
-// ---------------------------------------------------------------------------------
-// Pipelined ring engine: 4 waves (one per SIMD, 128x128 wave tiles, accumulators
-// in AGPRs), NSTAGE-deep ring of 32-wide K stages filled by direct-to-LDS loads.
-//
-// A stage is two 16-wide K sub-steps.  Fragments of sub-step t+1 are read from LDS
-// while the MFMAs of sub-step t run, including across the stage boundary: the ring
-// barrier sits between the two halves of a stage (after the wave's own LDS reads
-// have returned), so the first fragments of stage s+1 are read under the second
-// half of stage s's MFMAs.  The next-but-two stage's direct loads are spread through
-// both halves (one per four MFMAs).  Slot reuse: stage s+NSTAGE-1 overwrites the
-// slot of stage s-1, whose last reads completed before the mid barrier of s-1.
-// ---------------------------------------------------------------------------------
-template <typename T, int BM, int BN, int NSTAGE>
-struct PipeEngine {
-  static constexpr int WM = 2, WN = 2, NW = 4;
-  static constexpr int WROWS = BM / WM, WCOLS = BN / WN;
-  static constexpr int MI = WROWS / 32, NI = WCOLS / 32;
-  static_assert(WROWS % 32 == 0 && WCOLS % 32 == 0 && MI >= 1 && NI >= 1, "wave tile");
-  static constexpr int A_ELEMS = BM * kRK, B_ELEMS = BN * kRK;
-  static constexpr int STAGE = A_ELEMS + B_ELEMS;
-  static constexpr int LDS_ELEMS = NSTAGE * STAGE;
-  static constexpr int AJ = BM / 16 / NW, BJ = BN / 16 / NW;
-  static_assert(AJ * 16 * NW == BM && BJ * 16 * NW == BN, "16-row wave loads must cover the tile");
-  static constexpr int LPS = AJ + BJ;
-  static constexpr int HALF = LPS / 2;  // loads issued in the first half of a stage
-  static_assert(NSTAGE == 4, "ring of 4 stages");
-
-  static __device__ __forceinline__ int a_row(int wave, int lane, int j) { return (wave + NW * j) * 16 + (lane >> 2); }
-  static __device__ __forceinline__ int b_row(int wave, int lane, int j) { return (wave + NW * j) * 16 + (lane >> 2); }
-  static __device__ __forceinline__ int chunk(int row, int lane) { return (lane & 3) ^ swz4(row); }
-
-  const uint16_t* a_src[AJ];
-  const uint16_t* b_src[BJ];
-  int a_k[AJ], b_k[BJ];
-
-  __device__ __forceinline__ void issue_one(uint16_t* lds, int slot, int k0, int K, int wave, int q) {
-    uint16_t* sA = lds + slot * STAGE;
-    uint16_t* sB = sA + A_ELEMS;
-    const bool full = k0 + kRK <= K;
-    if (q < AJ) {
-      const void* src = full || (k0 + a_k[q] < K) ? (const void*)(a_src[q] + k0) : (const void*)kZeroPage;
-      gl_lds16(src, sA + (wave + NW * q) * 16 * kRK);
-    } else {
-      const int j = q - AJ;
-      const void* src = full || (k0 + b_k[j] < K) ? (const void*)(b_src[j] + k0) : (const void*)kZeroPage;
-      gl_lds16(src, sB + (wave + NW * j) * 16 * kRK);
-    }
-  }
-
-  static __device__ __forceinline__ void zero(f32x16_t (&acc)[MI][NI]) {
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-      for (int j = 0; j < NI; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-  }
-
-  // Wait for the loads of a stage given how many load instructions were issued after it.
-  static __device__ __forceinline__ void wait_after(int n) {
-    if (n >= LPS + HALF) wait_vmcnt<LPS + HALF>();
-    else if (n >= LPS) wait_vmcnt<LPS>();
-    else if (n >= HALF) wait_vmcnt<HALF>();
-    else wait_vmcnt<0>();
-  }
-
-  __device__ __forceinline__ void read_frags(const uint16_t* lds, int slot, int off, int rowA0, int rowB0,
-                                             u32x4_t (&af)[MI], u32x4_t (&bf)[NI]) const {
-    const uint16_t* sA = lds + slot * STAGE + rowA0 * kRK;
-    const uint16_t* sB = lds + slot * STAGE + A_ELEMS + rowB0 * kRK;
-#pragma unroll
-    for (int i = 0; i < MI; ++i) af[i] = *(const u32x4_t*)(sA + i * 32 * kRK + off);
-#pragma unroll
-    for (int j = 0; j < NI; ++j) bf[j] = *(const u32x4_t*)(sB + j * 32 * kRK + off);
-  }
-
-  __device__ __forceinline__ void mainloop(uint16_t* lds, int K, f32x16_t (&acc)[MI][NI]) {
-    using Op = MfmaOp<T>;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / WN, wn = wave % WN;
-    const int lr = lane & 31, hh = lane >> 5;
-    const int sw = swz4(lr);
-    const int off0 = lr * kRK + (((0 + hh) ^ sw) << 3);
-    const int off1 = lr * kRK + (((2 + hh) ^ sw) << 3);
-    const int rowA0 = wm * WROWS, rowB0 = wn * WCOLS;
-    const int nk = (K + kRK - 1) / kRK;
-    if (nk == 0) return;
-#pragma unroll
-    for (int s = 0; s < NSTAGE - 1; ++s)
-      if (s < nk)
-#pragma unroll
-        for (int q = 0; q < LPS; ++q) issue_one(lds, s, s * kRK, K, wave, q);
-    wait_after((nk > 1 ? LPS : 0) + (nk > 2 ? LPS : 0));
-    exec_barrier();
-    u32x4_t f0a[MI], f0b[NI], f1a[MI], f1b[NI];
-    read_frags(lds, 0, off0, rowA0, rowB0, f0a, f0b);
-    constexpr int NMMA = MI * NI;                  // MFMAs per sub-step
-    constexpr int GRP_LD = (NMMA + HALF - 1) / HALF;  // MFMAs per direct load
-    for (int s = 0; s < nk; ++s) {
-      const int slot = s % NSTAGE;
-      const bool more = s + NSTAGE - 1 < nk;
-      const int nslot = (s + NSTAGE - 1) % NSTAGE, nk0 = (s + NSTAGE - 1) * kRK;
-      // ---- first half: MFMAs of sub-step 0, reads of sub-step 1, HALF direct loads
-      read_frags(lds, slot, off1, rowA0, rowB0, f1a, f1b);
-#pragma unroll
-      for (int m = 0; m < NMMA; ++m) {
-        if (m % GRP_LD == 0 && m / GRP_LD < HALF) {
-          __builtin_amdgcn_sched_barrier(0);
-          if (more) issue_one(lds, nslot, nk0, K, wave, m / GRP_LD);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        const int i = m / NI, j = m % NI;
-        acc[i][j] = Op::mma32(f0b[j], f0a[i], acc[i][j]);
-      }
-      // ---- ring barrier: stage s+1 landed (own loads + everyone past the barrier)
-      const bool next = s + 1 < nk;
-      if (next) {
-        const int after = (s + 2 < nk ? LPS : 0) + (more ? HALF : 0);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        wait_after(after);
-        exec_barrier();
-      }
-      // ---- second half: MFMAs of sub-step 1, reads of stage s+1 sub-step 0, rest of the loads
-      if (next) read_frags(lds, (s + 1) % NSTAGE, off0, rowA0, rowB0, f0a, f0b);
-#pragma unroll
-      for (int m = 0; m < NMMA; ++m) {
-        if (m % GRP_LD == 0 && m / GRP_LD < LPS - HALF) {
-          __builtin_amdgcn_sched_barrier(0);
-          if (more) issue_one(lds, nslot, nk0, K, wave, HALF + m / GRP_LD);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        const int i = m / NI, j = m % NI;
-        acc[i][j] = Op::mma32(f1b[j], f1a[i], acc[i][j]);
-      }
-    }
-    __syncthreads();  // every wave is done with the ring before the caller reuses LDS
-  }
-};
-
-}  // namespace kore
-
-namespace kore {
-
-// ---------------------------------------------------------------------------------
-// Pipe64 engine: 4 waves (one per SIMD, 128x128 wave tiles, AGPR accumulators), two
-// LDS stages of 64-wide K (128-byte rows, chunk c of row r at c ^ swz8(r)), filled
-// by direct-to-LDS loads whose 8 lanes per row cover one whole 128-byte line (one
-// L2 request per line; 64-byte rows would double the request count).
-//
-// Iteration s (stage s in slot s%2, its sub-step-0 fragments already in registers):
-//   issue stage s+1 into slot (s+1)%2, spread over the first two sub-steps' MFMAs;
-//   sub-steps 0..2: MFMAs of sub-step t while the fragments of t+1 are read;
-//   own LDS reads done + own loads landed, then one barrier;
-//   sub-step 3: MFMAs while the first fragments of stage s+1 are read.
-// Slot (s+1)%2 last held stage s-1, whose final reads completed before the barrier
-// of iteration s-1, so one barrier per 64-wide K step suffices.
-// ---------------------------------------------------------------------------------
-template <typename T, int BM, int BN>
-struct Pipe64Engine {
-  static constexpr int WM = 2, WN = 2, NW = 4;
-  static constexpr int WROWS = BM / WM, WCOLS = BN / WN;
-  static constexpr int MI = WROWS / 32, NI = WCOLS / 32;
-  static_assert(WROWS % 32 == 0 && WCOLS % 32 == 0 && MI >= 1 && NI >= 1, "wave tile");
-  static constexpr int A_ELEMS = BM * kBK, B_ELEMS = BN * kBK;
-  static constexpr int STAGE = A_ELEMS + B_ELEMS;
-  static constexpr int LDS_ELEMS = 2 * STAGE;
-  static constexpr int AJ = BM / 8 / NW, BJ = BN / 8 / NW;  // 8-row wave loads per wave per stage
-  static_assert(AJ * 8 * NW == BM && BJ * 8 * NW == BN, "8-row wave loads must cover the tile");
-  static constexpr int LPS = AJ + BJ;
-
-  static __device__ __forceinline__ int a_row(int wave, int lane, int j) { return (wave + NW * j) * 8 + (lane >> 3); }
-  static __device__ __forceinline__ int b_row(int wave, int lane, int j) { return (wave + NW * j) * 8 + (lane >> 3); }
-  static __device__ __forceinline__ int chunk(int row, int lane) { return (lane & 7) ^ swz8(row); }
-
-  const uint16_t* a_src[AJ];
-  const uint16_t* b_src[BJ];
-  int a_k[AJ], b_k[BJ];
-
-  __device__ __forceinline__ void issue_one(uint16_t* lds, int slot, int k0, int K, int wave, int q) {
-    uint16_t* sA = lds + slot * STAGE;
-    uint16_t* sB = sA + A_ELEMS;
-    const bool full = k0 + kBK <= K;
-    if (q < AJ) {
-      const void* src = full || (k0 + a_k[q] < K) ? (const void*)(a_src[q] + k0) : (const void*)kZeroPage;
-      gl_lds16(src, sA + (wave + NW * q) * 8 * kBK);
-    } else {
-      const int j = q - AJ;
-      const void* src = full || (k0 + b_k[j] < K) ? (const void*)(b_src[j] + k0) : (const void*)kZeroPage;
-      gl_lds16(src, sB + (wave + NW * j) * 8 * kBK);
-    }
-  }
-
-  static __device__ __forceinline__ void zero(f32x16_t (&acc)[MI][NI]) {
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-      for (int j = 0; j < NI; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-  }
-
-  __device__ __forceinline__ void mainloop(uint16_t* lds, int K, f32x16_t (&acc)[MI][NI]) {
-    using Op = MfmaOp<T>;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / WN, wn = wave % WN;
-    const int lr = lane & 31, hh = lane >> 5;
-    int offA[2][4], offB[2][4];
-#pragma unroll
-    for (int par = 0; par < 2; ++par) {
-      const int qa = (wm * MI + par) & 1, qb = (wn * NI + par) & 1;
-      const int swa = ((lr & 7) ^ (lr >> 3) ^ (4 * qa)) & 7;
-      const int swb = ((lr & 7) ^ (lr >> 3) ^ (4 * qb)) & 7;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        offA[par][ks] = lr * kBK + (((2 * ks + hh) ^ swa) << 3);
-        offB[par][ks] = lr * kBK + (((2 * ks + hh) ^ swb) << 3);
-      }
-    }
-    const int rowA0 = wm * WROWS, rowB0 = wn * WCOLS;
-    auto read = [&](int slot, int ks, u32x4_t (&af)[MI], u32x4_t (&bf)[NI]) {
-      const uint16_t* sA = lds + slot * STAGE + rowA0 * kBK;
-      const uint16_t* sB = lds + slot * STAGE + A_ELEMS + rowB0 * kBK;
-#pragma unroll
-      for (int i = 0; i < MI; ++i) af[i] = *(const u32x4_t*)(sA + i * 32 * kBK + offA[i & 1][ks]);
-#pragma unroll
-      for (int j = 0; j < NI; ++j) bf[j] = *(const u32x4_t*)(sB + j * 32 * kBK + offB[j & 1][ks]);
-    };
-    const int nk = (K + kBK - 1) / kBK;
-    if (nk == 0) return;
-#pragma unroll
-    for (int q = 0; q < LPS; ++q) issue_one(lds, 0, 0, K, wave, q);
-    wait_vmcnt<0>();
-    exec_barrier();
-    u32x4_t fa[2][MI], fb[2][NI];
-    read(0, 0, fa[0], fb[0]);
-    constexpr int NMMA = MI * NI;
-    constexpr int LD_STEPS = 2;  // sub-steps that carry the next stage's loads
-    constexpr int PER = (LPS + LD_STEPS * NMMA - 1) / (LD_STEPS * NMMA);  // loads per MFMA slot
-    constexpr int EVERY = (LD_STEPS * NMMA) / ((LPS + PER - 1) / PER);     // MFMAs between load slots
-    for (int s = 0; s < nk; ++s) {
-      const int slot = s & 1;
-      const bool more = s + 1 < nk;
-      const int k1 = (s + 1) * kBK;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const int c = ks & 1;
-        if (ks < 3) {
-          read(slot, ks + 1, fa[c ^ 1], fb[c ^ 1]);
-        } else {
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-          wait_vmcnt<0>();
-          exec_barrier();
-          if (more) read(slot ^ 1, 0, fa[c ^ 1], fb[c ^ 1]);
-        }
-#pragma unroll
-        for (int m = 0; m < NMMA; ++m) {
-          if (ks < LD_STEPS) {
-            const int g = ks * NMMA + m;
-            if (g % EVERY == 0) {
-              __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-              for (int u = 0; u < PER; ++u) {
-                const int q = (g / EVERY) * PER + u;
-                if (q < LPS && more) issue_one(lds, slot ^ 1, k1, K, wave, q);
-              }
-              __builtin_amdgcn_sched_barrier(0);
-            }
-          }
-          const int i = m / NI, j = m % NI;
-          acc[i][j] = Op::mma32(fb[c][j], fa[c][i], acc[i][j]);
-        }
-      }
-    }
-    __syncthreads();  // every wave is done with both stages before the caller reuses LDS
-  }
-};
-
 }  // namespace kore
 
 namespace kore {
@@ -814,9 +279,9 @@ namespace kore {
 // ---------------------------------------------------------------------------------
 // Buffer-load pipelined engine (the production dense/grouped GEMM main loop).
 //
-// Same schedule as Pipe64Engine (4 waves, 128x128 wave tiles, two 64-wide K stages,
-// one barrier per K step, next stage's loads spread over the first half of the
-// MFMAs, fragments read one sub-step ahead), but the direct-to-LDS loads are
+// 4 waves (one per SIMD, 128x128 wave tiles, AGPR accumulators), two 64-wide K
+// stages, one barrier per K step; the next stage's loads are spread over the MFMAs
+// and fragments are read one 16-wide sub-step ahead.  The direct-to-LDS loads are
 // buffer_load_dwordx4 ... lds with a buffer resource per operand, a per-lane byte
 // offset fixed at setup (row and swizzled chunk) and the K advance in the scalar
 // offset -- no per-load vector address arithmetic, which otherwise costs more issue
@@ -972,6 +437,110 @@ struct BufPipeEngine {
       }
     }
     wait_vmcnt<0>();  // drain the clamped trailing loads before LDS is reused
+    __syncthreads();
+  }
+};
+
+}  // namespace kore
+
+namespace kore {
+
+// ---------------------------------------------------------------------------------
+// Skinny ring engine (weight streaming, M = 32 rows).
+//
+// For grouped GEMMs with few rows per expert (MoE decode) the time is the weight
+// stream, so what matters is how many bytes each CU keeps in flight.  Four waves sit
+// side by side over N (wave tile 32 x BN/4); an NSLOT-deep ring of 64-wide K stages
+// is filled by direct-to-LDS buffer loads (one wave instruction = 8 whole 128-byte
+// rows), NSLOT-1 stages ahead of the MFMAs.  Per K step: wait for the own loads of
+// the stage, one barrier (every wave's loads landed and every wave finished the
+// previous stage, whose slot is refilled next), issue the stage NSLOT-1 ahead, then
+// 4 sub-steps of MFMAs.  Past the last stage the K offset is clamped (the last
+// stage is re-loaded into a free slot), so every wave issues the same loads and the
+// vmcnt arithmetic is uniform.  AP == 2 multiplies two A planes by the same B
+// fragments (the bf16 high/low split of an fp32 activation).
+// ---------------------------------------------------------------------------------
+template <typename T, int BN, int AP, int NSLOT>
+struct SkinnyRingEngine {
+  static constexpr int NW = 4, BM = 32;
+  static constexpr int WCOLS = BN / NW, NI = WCOLS / 32;
+  static_assert(WCOLS % 32 == 0 && NI >= 1, "wave tile is 32 x (multiple of 32)");
+  static constexpr int A_ELEMS = BM * kBK, B_ELEMS = BN * kBK;
+  static constexpr int B_OFF = AP * A_ELEMS;
+  static constexpr int STAGE = AP * A_ELEMS + B_ELEMS;
+  static constexpr int LDS_ELEMS = NSLOT * STAGE;
+  static constexpr int BJ = BN / 8 / NW;  // 8-row B loads per wave per stage (A: one per plane)
+  static_assert(BJ * 8 * NW == BN, "8-row wave loads must cover the B tile");
+  static constexpr int LPS = AP + BJ;
+  static_assert(NSLOT >= 2 && (NSLOT - 2) * LPS <= 63, "vmcnt range");
+
+  static __device__ __forceinline__ int a_row(int wave, int lane) { return wave * 8 + (lane >> 3); }
+  static __device__ __forceinline__ int b_row(int wave, int lane, int j) { return (wave + NW * j) * 8 + (lane >> 3); }
+  static __device__ __forceinline__ int chunk(int row, int lane) { return (lane & 7) ^ swz8(row); }
+
+  __amdgpu_buffer_rsrc_t ra, ra2, rb;
+  uint32_t a_voff, b_voff[BJ];
+
+  __device__ __forceinline__ void issue(uint16_t* lds, int slot, uint32_t soff, int wave) const {
+    uint16_t* st = lds + slot * STAGE;
+    buf_lds16(ra, a_voff, soff, st + wave * 8 * kBK);
+    if constexpr (AP == 2) buf_lds16(ra2, a_voff, soff, st + A_ELEMS + wave * 8 * kBK);
+#pragma unroll
+    for (int j = 0; j < BJ; ++j) buf_lds16(rb, b_voff[j], soff, st + B_OFF + (wave + NW * j) * 8 * kBK);
+  }
+
+  static __device__ __forceinline__ void zero(f32x16_t (&acc)[1][NI]) {
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[0][j][r] = 0.0f;
+  }
+
+  // Multiply K elements [k_begin, k_end) (multiples of 64; k_end > k_begin).
+  __device__ __forceinline__ void mainloop(uint16_t* lds, int k_begin, int k_end, f32x16_t (&acc)[1][NI]) {
+    using Op = MfmaOp<T>;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lr = lane & 31, hh = lane >> 5;
+    // fragment row R + lr (R % 32 == 0): swz8(R + lr) = (lr & 7) ^ (lr >> 3) ^ (4 * ((R / 32) & 1))
+    int offA[4], offB[2][4];
+    const int swa = ((lr & 7) ^ (lr >> 3)) & 7;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      offA[ks] = lr * kBK + (((2 * ks + hh) ^ swa) << 3);
+#pragma unroll
+      for (int par = 0; par < 2; ++par) {
+        const int qb = (wave * NI + par) & 1;
+        offB[par][ks] = lr * kBK + (((2 * ks + hh) ^ (swa ^ (4 * qb))) << 3);
+      }
+    }
+    const int nk = (k_end - k_begin) / kBK;
+    const uint32_t s0 = (uint32_t)k_begin * 2u, smax = (uint32_t)(k_end - kBK) * 2u;
+    auto soff_of = [&](int stage) { return min(s0 + (uint32_t)stage * (kBK * 2), smax); };
+#pragma unroll
+    for (int s = 0; s < NSLOT - 1; ++s) issue(lds, s, soff_of(s), wave);
+    int slot = 0;
+    for (int s = 0; s < nk; ++s) {
+      wait_vmcnt<(NSLOT - 2) * LPS>();
+      exec_barrier();
+      const int nslot = slot == 0 ? NSLOT - 1 : slot - 1;  // slot of stage s - 1
+      issue(lds, nslot, soff_of(s + NSLOT - 1), wave);
+      const uint16_t* sA = lds + slot * STAGE;
+      const uint16_t* sB = sA + B_OFF + wave * WCOLS * kBK;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        u32x4_t af[AP], bf[NI];
+#pragma unroll
+        for (int pl = 0; pl < AP; ++pl) af[pl] = *(const u32x4_t*)(sA + pl * A_ELEMS + offA[ks]);
+#pragma unroll
+        for (int j = 0; j < NI; ++j) bf[j] = *(const u32x4_t*)(sB + j * 32 * kBK + offB[j & 1][ks]);
+#pragma unroll
+        for (int pl = 0; pl < AP; ++pl)
+#pragma unroll
+          for (int j = 0; j < NI; ++j) acc[0][j] = Op::mma32(bf[j], af[pl], acc[0][j]);
+      }
+      slot = slot + 1 == NSLOT ? 0 : slot + 1;
+    }
+    wait_vmcnt<0>();  // the clamped trailing loads must land before LDS is reused
     __syncthreads();
   }
 };

@@ -40,11 +40,13 @@ def test_fp8_task_shapes(gpu, M, N, K, seed):
     pair_only(out, ref, "fp8", f"{M}x{N}x{K}")
 
 
-@pytest.mark.parametrize("M,N,K", [(4000, 3072, 640), (4000, 3072, 512), (3840, 3072, 1024)])
+@pytest.mark.parametrize("M,N,K", [(4000, 3072, 640), (4000, 3072, 512), (3840, 3072, 1024),
+                                   (1100, 6016, 512), (1100, 6016, 640)])
 def test_fp8_wide_tiles(gpu, M, N, K):
     """Problems with at least 192 tiles of 256x256 run on the 256x256 (two-slot) kernel:
     a partial last M tile (M=4000), per-step scale loads (K/128 = 5) and four-step
-    scale loads (K/128 = 4, 8)."""
+    scale loads (K/128 = 4, 8).  N = 6016 (not a multiple of 256) with 235 tiles of
+    256x128 runs the 256x128 (three-slot) kernel; smaller problems run 128x128 tiles."""
     xq, wq, xs, ws = W.fp8_inputs(M, N, K, seed=M + K, scale=0.2)
     out = _run(gpu, xq, wq, xs, ws)
     ref = matmul_blockscale_ref(xq, wq, xs, ws)
