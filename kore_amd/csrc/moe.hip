@@ -146,29 +146,54 @@ __device__ __forceinline__ void moe_epilogue(f32x16_t (&acc)[MI][NI], uint16_t* 
   using Op = MfmaOp<BF16>;
   if constexpr (MODE == MOE_GATEUP) {
     constexpr int HC = WCOLS / 2;  // h columns per wave
-    constexpr int NH = NI / 2;
     using St = Stager<WROWS, HC>;
     uint16_t* stg_hi = lds + wave * (2 * WROWS * HC);
     uint16_t* stg_lo = stg_hi + WROWS * HC;
+    // h = silu(gate) * up for 4 consecutive h columns, split into bf16 high/low planes
+    auto put_h = [&](int row, int col, const float (&gt)[4], const float (&up)[4]) {
+      float hi[4], lo[4];
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
+      for (int q = 0; q < 4; ++q) {
+        const float h = gt[q] * fast_sigmoid(gt[q]) * up[q];
+        hi[q] = Op::to_f32((uint16_t)(Op::pack2(h, 0.0f) & 0xffffu));
+        lo[q] = h - hi[q];  // exact in fp32
+      }
+      St::put(stg_hi, row, col, u32x2_t{Op::pack2(hi[0], hi[1]), Op::pack2(hi[2], hi[3])});
+      St::put(stg_lo, row, col, u32x2_t{Op::pack2(lo[0], lo[1]), Op::pack2(lo[2], lo[3])});
+    };
+    if constexpr (NI == 1) {
+      // one 32-row block: rows 0-15 are gate rows, 16-31 the matching up rows, so
+      // register 4g+q (g < 2) holds a gate value and register 8+4g+q its up value
 #pragma unroll
-      for (int j = 0; j < NH; ++j)
+      for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          float hi[4], lo[4];
+        for (int g = 0; g < 2; ++g) {
+          float gt[4], up[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const float gt = acc[i][j][4 * g + q], up = acc[i][j + NH][4 * g + q];
-            const float h = gt * fast_sigmoid(gt) * up;
-            hi[q] = Op::to_f32((uint16_t)(Op::pack2(h, 0.0f) & 0xffffu));
-            lo[q] = h - hi[q];  // exact in fp32
+            gt[q] = acc[i][0][4 * g + q];
+            up[q] = acc[i][0][8 + 4 * g + q];
           }
-          St::put(stg_hi, out_row(i, lane), out_col(j, g, lane),
-                  u32x2_t{Op::pack2(hi[0], hi[1]), Op::pack2(hi[2], hi[3])});
-          St::put(stg_lo, out_row(i, lane), out_col(j, g, lane),
-                  u32x2_t{Op::pack2(lo[0], lo[1]), Op::pack2(lo[2], lo[3])});
+          put_h(out_row(i, lane), out_col(0, g, lane), gt, up);
         }
+    } else {
+      // 32-row blocks j < NI/2 are gate rows, block j + NI/2 the matching up rows
+      constexpr int NH = NI / 2;
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NH; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            float gt[4], up[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              gt[q] = acc[i][j][4 * g + q];
+              up[q] = acc[i][j + NH][4 * g + q];
+            }
+            put_h(out_row(i, lane), out_col(j, g, lane), gt, up);
+          }
+    }
     __syncthreads();
     const int rw0 = pos0 + wm * WROWS, cw0 = n0 + wn * HC;
     St::drain(stg_hi, lane, [&](int row, int col, u32x4_t v) {
@@ -590,7 +615,7 @@ extern "C" int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, c
   p.w_rstride = D;
   // buffer-load engine needs operand byte ranges below 4 GiB and K % 64 == 0
   const bool buf_ok = T * ldh * 2 < (1ll << 32) && 2 * I * D * 2 < (1ll << 32) && D % 64 == 0 && I % 64 == 0;
-  rc = (BM == 32 && buf_ok) ? launch_moe_decode<MOE_GATEUP, 256, 4>(p, cap, st)
+  rc = (BM == 32 && buf_ok) ? launch_moe_decode<MOE_GATEUP, 128, 7>(p, cap, st)
        : (BM == 32) ? launch_moe_gemm<MOE_GATEUP, 32, 256, 1, 4>(p, cap, st)
        : buf_ok   ? launch_moe_buf<MOE_GATEUP, 256, 256>(p, cap, st)
                   : launch_moe_gemm<MOE_GATEUP, 256, 256, 2, 2>(p, cap, st);

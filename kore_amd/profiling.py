@@ -175,6 +175,69 @@ def write_traffic(a) -> None:
     print(entry)
 
 
+PMC_FILE = os.path.join(PROFILES, "pmc_counters.md")
+PMC_COUNTERS = ("MfmaUtil", "LdsBankConflict", "LdsUtil", "VALUBusy")
+
+
+def _replace_section(path: str, header: list[str], key: str, section: list[str]) -> None:
+    """Rewrite ``path`` keeping every ``## <other>`` section and replacing ``## key``."""
+    body = []
+    if os.path.exists(path):
+        skip = False
+        with open(path) as f:
+            for ln in f:
+                ln = ln.rstrip("\n")
+                if ln.startswith("## "):
+                    skip = ln == f"## {key}"
+                if not skip:
+                    body.append(ln)
+        while body and not body[-1]:
+            body.pop()
+    if not body:
+        body = list(header)
+    body += ["", f"## {key}", ""] + section
+    with open(path, "w") as f:
+        f.write("\n".join(body) + "\n")
+
+
+def write_pmc(a) -> None:
+    """Per-kernel medians of the derived counters of one ``--pmc`` run."""
+    path = _one(os.path.join(a.dir, "**", "*counter_collection.csv"))
+    vals: dict[str, dict[str, dict[str, float]]] = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if "kore" not in r["Kernel_Name"]:
+                continue
+            k = _short(r["Kernel_Name"])
+            vals.setdefault(k, {}).setdefault(r["Counter_Name"], {})
+            d = vals[k][r["Counter_Name"]]
+            d[r["Dispatch_Id"]] = d.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"])
+    if not vals:
+        raise SystemExit(f"no kore kernels in {path}")
+    names = [c for c in PMC_COUNTERS if any(c in v for v in vals.values())]
+    unit = {"MfmaUtil": "MFMA busy (% of SIMD-cycles)", "LdsBankConflict": "LDS bank conflicts (cycles per access cycle)",
+            "LdsUtil": "LDS active (% of CU-cycles)", "VALUBusy": "VALU busy (% of CU-cycles)"}
+    section = ["Command (from the repository root, on one MI355X):", "", "```", a.cmd, "```", "",
+               "| kernel | " + " | ".join(unit.get(n, n) for n in names) + " |",
+               "|---|" + "---|" * len(names)]
+    for k, cs in vals.items():
+        cells = []
+        for n in names:
+            v = statistics.median(cs[n].values()) if n in cs else float("nan")
+            cells.append(f"{v:.3f}" if n == "LdsBankConflict" else f"{v:.1f}")
+        section.append(f"| `{k}` | " + " | ".join(cells) + " |")
+    if a.note:
+        section += ["", a.note]
+    header = ["# rocprofv3 derived counters per kernel", "",
+              "MfmaUtil = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs); LdsBankConflict =",
+              "SQ_LDS_BANK_CONFLICT / (SQ_LDS_IDX_ACTIVE - SQ_LDS_BANK_CONFLICT); LdsUtil and VALUBusy are",
+              "SQ_LDS_IDX_ACTIVE and SQ_ACTIVE_INST_VALU over GRBM_GUI_ACTIVE x CUs (rocprofv3's own",
+              "definitions).  Medians over the profiled dispatches of each kernel.  Busy fractions count",
+              "every CU of the GPU, so a grid that occupies 224 of the 256 CUs reads at most 87.5%."]
+    _replace_section(a.out, header, a.workload, section)
+    print("\n".join(section[-len(vals):]))
+
+
 def read_traffic(workload: str, path: str = TRAFFIC_FILE):
     """Bytes per launch recorded for ``workload`` in the traffic summary, or None."""
     try:
@@ -213,6 +276,12 @@ def main(argv=None) -> int:
     t.add_argument("--copy-kernel", default="copy")
     t.add_argument("--out", default=TRAFFIC_FILE)
     t.add_argument("--cmd", required=True)
+    m = sub.add_parser("pmc")
+    m.add_argument("dir")
+    m.add_argument("--workload", required=True)
+    m.add_argument("--out", default=PMC_FILE)
+    m.add_argument("--cmd", required=True)
+    m.add_argument("--note", default="")
     a = p.parse_args(argv)
     if a.action == "run":
         _run(a.workload, a.iters, a.warmup)
@@ -220,6 +289,8 @@ def main(argv=None) -> int:
         _copy(a.mib, a.iters)
     elif a.action == "stats":
         write_stats(a.dir, a.out, a.cmd, a.title)
+    elif a.action == "pmc":
+        write_pmc(a)
     else:
         write_traffic(a)
     return 0

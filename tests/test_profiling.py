@@ -74,3 +74,18 @@ def test_headline_roofline_figures():
     assert r.flops == 2.0 * 2048 * 7168 * 4096
     assert r.bytes == 2048 * 4096 + 7168 * 4096 + 2 * 2048 * 7168
     assert r.bound == "mfma"
+
+
+def test_pmc_summary_sections(tmp_path):
+    kern = "void kore::(anonymous namespace)::gemm_fp8_pipe_kernel<X>(P)"
+    _counters(tmp_path / "p", [(1, kern, "MfmaUtil", 40.0), (2, kern, "MfmaUtil", 44.0), (3, kern, "MfmaUtil", 50.0),
+                               (1, kern, "LdsBankConflict", 0.25), (2, kern, "LdsBankConflict", 0.25),
+                               (3, kern, "LdsBankConflict", 0.25), (4, "other", "MfmaUtil", 99.0)])
+    out = tmp_path / "pmc.md"
+    P.write_pmc(Namespace(dir=str(tmp_path / "p"), workload="w1", out=str(out), cmd="cmd1", note=""))
+    P.write_pmc(Namespace(dir=str(tmp_path / "p"), workload="w2", out=str(out), cmd="cmd2", note="n"))
+    P.write_pmc(Namespace(dir=str(tmp_path / "p"), workload="w1", out=str(out), cmd="cmd3", note=""))
+    text = out.read_text()
+    assert text.count("## w1") == 1 and text.count("## w2") == 1 and "cmd3" in text and "cmd1" not in text
+    row = [ln for ln in text.splitlines() if ln.startswith("| `gemm_fp8_pipe_kernel")][0]
+    assert "| 44.0 |" in row and "0.250" in row  # medians; the non-kore kernel is ignored
