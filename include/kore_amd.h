@@ -41,6 +41,10 @@ extern "C" {
 #define KORE_ACT_TANH 4
 #define KORE_ACT_SIGMOID 5
 
+/* 8-bit operand types of kore_gemm_a8w8 */
+#define KORE_Q_FP8 0   /* OCP e4m3 (torch.float8_e4m3fn) */
+#define KORE_Q_INT8 1  /* symmetric int8 */
+
 /* Last error message of the calling host thread ("" when none). */
 const char* kore_last_error(void);
 
@@ -93,6 +97,28 @@ int kore_gemm_a8w8_blockscale(const void* xq, int64_t ldx, const void* wq, int64
                               const float* ws, int64_t ws_n, int64_t ws_k,
                               void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                               void* stream);
+
+/*
+ * 8-bit a8w8 GEMM with per-row activation and per-column weight scales:
+ *   Y[M,N] (bf16) = (xq[m,:] . wq[n,:]) * xs[m] * ws[n]
+ *   qtype KORE_Q_FP8 (OCP e4m3) or KORE_Q_INT8 for both operands; xq [M,K] with
+ *   element strides (ldx_m, ldx_k); wq [N,K] with (ldw_n, ldw_k); xs [M] and ws [N]
+ *   fp32 with element strides xs_stride / ws_stride (x_scale [M,1], w_scale [1,N] or
+ *   [N,1] views); Y row stride ldy.  Per-tensor scales are equal entries.  Any K and
+ *   any strides (K % 128 == 0, N % 128 == 0, K-contiguous 16-byte aligned rows take the
+ *   MFMA kernels; everything else a generic kernel); int8 sums are exact in int32.
+ * Replaces: gemm(xq, wq, x_scale, w_scale)
+ *           kore/tasks/gemm_fp8_a8w8/seed_triton.py (per-tensor),
+ *           kore/tasks/gemm_fp8_a8w8_pertoken/seed_triton.py,
+ *           kore/tasks/gemm_fp8_a8w8_pertensor/seed_triton.py,
+ *           kore/tasks/gemm_int8_a8w8/seed_triton.py;
+ *           gemm_a8w8(xq, wq, x_scale, w_scale) kore/tasks/vendor_ops.py:697-760
+ *           (genv_gemm_a8w8_fp8 / _int8); oracle kore/tasks/_quant_common.py:236-242.
+ */
+int kore_gemm_a8w8(int qtype, const void* xq, int64_t ldx_m, int64_t ldx_k,
+                   const void* wq, int64_t ldw_n, int64_t ldw_k,
+                   const float* xs, int64_t xs_stride, const float* ws, int64_t ws_stride,
+                   void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream);
 
 /*
  * MoE dispatch sort/align.  Slots are s = t*topk + k over topk_ids [T, topk] int32

@@ -2,7 +2,7 @@
 
 Operators (all on HIP device tensors, launched on torch's current stream):
 dense bf16/fp16 GEMM with fused bias + activation epilogues, batched GEMM, OCP-e4m3
-fp8 a8w8 block-scaled GEMM, and the fused top-k MoE SiLU grouped GEMM.  The kernels
+fp8 a8w8 block-scaled GEMM, fp8/int8 a8w8 GEMM with row/column scales, and the fused top-k MoE SiLU grouped GEMM.  The kernels
 live in ``libkore_amd.so`` (built by ``python -m kore_amd.build``); see
 ``include/kore_amd.h`` for its C ABI.
 """
@@ -13,6 +13,7 @@ from .ops import (  # noqa: F401
     batched_gemm,
     fused_moe,
     gemm,
+    gemm_a8w8,
     gemm_a8w8_blockscale,
     gemm_fused,
     moe_align,
@@ -23,5 +24,5 @@ from . import ops as _ops
 for _name in _ops.GEMM_FUSION_OPS:
     globals()[_name] = getattr(_ops, _name)
 
-__all__ = ["gemm", "gemm_fused", "batched_gemm", "gemm_a8w8_blockscale", "fused_moe", "moe_gated_silu", "moe_align",
+__all__ = ["gemm", "gemm_fused", "batched_gemm", "gemm_a8w8_blockscale", "gemm_a8w8", "fused_moe", "moe_gated_silu", "moe_align",
            *_ops.GEMM_FUSION_OPS]

@@ -27,6 +27,8 @@ SIGNATURES = {
                                  _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
     "kore_gemm_a8w8_blockscale": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _vp, _i64,
                                          _i64, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "kore_gemm_a8w8": (_i32, [_i32, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64,
+                              _i64, _i64, _i64, _vp]),
     "kore_moe_align_capacity": (_i64, [_i64, _i64, _i64, _i64]),
     "kore_moe_align": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
     "kore_fused_moe_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64]),

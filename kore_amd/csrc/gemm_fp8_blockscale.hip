@@ -16,6 +16,8 @@
 #include "kore_common.hpp"
 #include "tile_engine.hpp"
 
+#include <type_traits>
+
 namespace kore {
 namespace {
 
@@ -201,10 +203,16 @@ __global__ void __launch_bounds__(kEngineThreads)
 // over the next W tiles (W = NT with three slots: one to two stages of latency; the
 // remaining tiles of the stage with two slots: one stage).
 // ------------------------------------------------------------------------------
-template <int BM_, int BN_, int NW_, int NSLOT_, bool XS4_>
+// Scale modes of the 8-bit kernels: DeepSeek block scales promoted once per 128-wide
+// K block (fp8), or one activation scale per row and one weight scale per column,
+// applied once to the finished accumulator in the epilogue (fp8 or int8 operands).
+enum { Q_BLOCK_FP8 = 0, Q_ROW_FP8 = 1, Q_ROW_I8 = 2 };
+
+template <int BM_, int BN_, int NW_, int NSLOT_, bool XS4_, int MODE_ = Q_BLOCK_FP8>
 struct F8Cfg {
-  static constexpr int BM = BM_, BN = BN_, NW = NW_, NSLOT = NSLOT_;
-  static constexpr bool XS4 = XS4_;
+  static constexpr int BM = BM_, BN = BN_, NW = NW_, NSLOT = NSLOT_, MODE = MODE_;
+  static constexpr bool ROW = MODE != Q_BLOCK_FP8;
+  static constexpr bool XS4 = XS4_ && !ROW;
   static constexpr int NB = BN / 128;         // weight-scale blocks per tile
   static constexpr int WGN = BN / 64, WGM = NW / WGN;
   static_assert(WGM * WGN == NW && WGM >= 1, "wave grid");
@@ -218,8 +226,8 @@ struct F8Cfg {
   // scale loads per wave: 4 waves each load 64 xs rows (rows past the tile are
   // clamped and never read) and the ws copies; 8 waves: waves 0-3 xs, waves 4-7 ws
   // (block (w-4) % NB)
-  static constexpr int SQ = NW == 4 ? 2 : 1;
-  static_assert(NW == 8 || NB == 1, "4-wave tiles have one weight-scale block");
+  static constexpr int SQ = ROW ? 0 : (NW == 4 ? 2 : 1);
+  static_assert(ROW || NW == 8 || NB == 1, "4-wave tiles have one weight-scale block");
   static constexpr int LPS = AQ + BQ + SQ;
   static constexpr int W = NSLOT >= 3 ? NT : NT - TB;  // load window in tiles
   static constexpr int PER = (LPS + W - 1) / W;
@@ -227,8 +235,8 @@ struct F8Cfg {
   // LDS layout of a slot
   static constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
   static constexpr int XOFF = A_BYTES + B_BYTES;          // xs (per-step mode only)
-  static constexpr int WOFF = XOFF + (XS4 ? 0 : 1024);
-  static constexpr int WCOPY = XS4 ? 1024 : 256;           // bytes of one ws block's copies
+  static constexpr int WOFF = XOFF + (XS4 || ROW ? 0 : 1024);
+  static constexpr int WCOPY = ROW ? 0 : (XS4 ? 1024 : 256);  // bytes of one ws block's copies
   static constexpr int SLOT = WOFF + NB * WCOPY;
   static constexpr int RING = NSLOT * SLOT;                // XS4 activation-scale ring
   static constexpr int LDS = RING + (XS4 ? 2 * 4096 : 0);
@@ -258,7 +266,8 @@ __global__ void __launch_bounds__(C::NW * 64)
     gemm_fp8_pipe_kernel(const Fp8Params p) {
   constexpr int NW = C::NW, MI = C::MI, NI = C::NI, NT = C::NT, TB = C::TB;
   constexpr int AQ = C::AQ, BQ = C::BQ, LPS = C::LPS, PER = C::PER, NSLOT = C::NSLOT;
-  constexpr bool XS4 = C::XS4;
+  constexpr bool XS4 = C::XS4, ROW = C::ROW, I8 = C::MODE == Q_ROW_I8;
+  using AccT = std::conditional_t<I8, i32x16_t, f32x16_t>;
 
   __shared__ __attribute__((aligned(1024))) uint8_t lds[C::LDS];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -316,7 +325,7 @@ __global__ void __launch_bounds__(C::NW * 64)
     } else if (q < AQ + BQ) {
       buf_lds(rb, b_voff, (uint32_t)kb * 128u + (uint32_t)(q - AQ) * b_rstep,
               base + C::A_BYTES + (wave + NW * (q - AQ)) * 1024, 16);
-    } else {
+    } else if constexpr (!ROW) {
       // scale load (wave-uniform selects): activation scales, or weight-scale copies
       const bool xload = (NW == 4 ? q == AQ + BQ : wave < 4) && (!XS4 || (kb & 3) == 0);
       if constexpr (XS4) {
@@ -342,13 +351,24 @@ __global__ void __launch_bounds__(C::NW * 64)
     for (int e = 0; e < 2; ++e) off[h][e] = lr * 128 + (((4 * h + 2 * hh + e) ^ key) << 4);
   const int rowA0 = wm * C::WROWS, rowB0 = wn * 64;
 
-  f32x16_t acc[MI][NI];
+  AccT acc[MI][NI];
 #pragma unroll
   for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < NI; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+  // row-scale modes: one K half of a 32x32 tile straight into its accumulator
+  auto row_mma = [&](AccT& c, const i32x8_t& b, const i32x8_t& a) {
+    if constexpr (I8) {
+      c = mma32_i8(u32x4_t{(uint32_t)b[0], (uint32_t)b[1], (uint32_t)b[2], (uint32_t)b[3]},
+                   u32x4_t{(uint32_t)a[0], (uint32_t)a[1], (uint32_t)a[2], (uint32_t)a[3]}, c);
+      c = mma32_i8(u32x4_t{(uint32_t)b[4], (uint32_t)b[5], (uint32_t)b[6], (uint32_t)b[7]},
+                   u32x4_t{(uint32_t)a[4], (uint32_t)a[5], (uint32_t)a[6], (uint32_t)a[7]}, c);
+    } else if constexpr (ROW) {
+      c = mma32_fp8(b, a, c);
+    }
+  };
   f32x16_t part[2];
 #pragma unroll
   for (int r = 0; r < 16; ++r) part[1][r] = 0.0f;
@@ -393,27 +413,32 @@ __global__ void __launch_bounds__(C::NW * 64)
         exec_barrier();
       }
       __builtin_amdgcn_sched_barrier(0);
-      part[j] = mma32_fp8(bf[j][0], af[i & 1][0], zero);
-      __builtin_amdgcn_sched_barrier(0);
-      if (t == 1) {
+      if constexpr (ROW) {
+        row_mma(acc[i][j], bf[j][0], af[i & 1][0]);
+      } else {
+        part[j] = mma32_fp8(bf[j][0], af[i & 1][0], zero);
+        __builtin_amdgcn_sched_barrier(0);
+        if (t == 1) {
 #pragma unroll
-        for (int q = 0; q < MI; ++q) sc[q] = xsv[q] * wsv;
-      }
-      {
-        // promote the previous tile (t == 0: the last tile of the previous stage,
-        // whose scale sc[MI-1] is still live; zeros before the first stage)
-        const int pt = (t + NT - 1) % NT;
-        const float f = sc[pt / NI];
+          for (int q = 0; q < MI; ++q) sc[q] = xsv[q] * wsv;
+        }
+        {
+          // promote the previous tile (t == 0: the last tile of the previous stage,
+          // whose scale sc[MI-1] is still live; zeros before the first stage)
+          const int pt = (t + NT - 1) % NT;
+          const float f = sc[pt / NI];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[pt / NI][pt % NI][r] = fmaf(part[j ^ 1][r], f, acc[pt / NI][pt % NI][r]);
+          for (int r = 0; r < 16; ++r) acc[pt / NI][pt % NI][r] = fmaf(part[j ^ 1][r], f, acc[pt / NI][pt % NI][r]);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
-      part[j] = mma32_fp8(bf[j][1], af[i & 1][1], part[j]);
+      if constexpr (ROW) row_mma(acc[i][j], bf[j][1], af[i & 1][1]);
+      else part[j] = mma32_fp8(bf[j][1], af[i & 1][1], part[j]);
       __builtin_amdgcn_sched_barrier(0);
       // LDS reads: scales of this stage; A block i+1 (both K halves) at the first
       // tile of block i, two MFMA pairs before its first use; after the barrier A
       // block 0 of the next stage; B of the next stage right after its last use.
-      if (t == 0) {
+      if (!ROW && t == 0) {
         if constexpr (XS4) {
           const uint8_t* ring = lds + C::RING + ((s >> 2) & 1) * 4096 + (s & 3) * 4;
 #pragma unroll
@@ -453,25 +478,44 @@ __global__ void __launch_bounds__(C::NW * 64)
     __builtin_amdgcn_sched_barrier(0);
     slot = slot1;
   }
-  // promote the last tile of the last stage
+  if constexpr (!ROW) {
+    // promote the last tile of the last stage
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[MI - 1][NI - 1][r] = fmaf(part[1][r], sc[MI - 1], acc[MI - 1][NI - 1][r]);
+    for (int r = 0; r < 16; ++r) acc[MI - 1][NI - 1][r] = fmaf(part[1][r], sc[MI - 1], acc[MI - 1][NI - 1][r]);
+  }
   wait_vmcnt<0>();  // the clamped trailing loads must land before LDS is reused
   __syncthreads();
 
-  // ---- epilogue: bf16 pack, stage per wave, 16-byte row stores ----
+  // ---- epilogue: (row modes: x scale of the row times w scale of the column), bf16
+  // pack, stage per wave, 16-byte row stores ----
   using St = Stager<C::WROWS, 64>;
   using Op = MfmaOp<BF16>;
   uint16_t* stg = (uint16_t*)lds + wave * (C::WROWS * 64);
+  float xrow[MI];
 #pragma unroll
   for (int i = 0; i < MI; ++i)
+    xrow[i] = ROW ? p.xs[(int64_t)min(m0 + rowA0 + 32 * i + lr, p.M - 1) * p.xs_m] : 1.0f;
 #pragma unroll
-    for (int j = 0; j < NI; ++j)
+  for (int j = 0; j < NI; ++j)
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-        St::put(stg, out_row(i, lane), out_col(j, g, lane),
-                u32x2_t{Op::pack2(acc[i][j][4 * g], acc[i][j][4 * g + 1]),
-                        Op::pack2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3])});
+    for (int g = 0; g < 4; ++g) {
+      float wcol[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+      if constexpr (ROW) {
+        const int64_t n = n0 + rowB0 + out_col(j, g, lane);  // n + 3 < N: N % BN == 0
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wcol[e] = p.ws[(n + e) * p.ws_n];
+      }
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = (float)acc[i][j][4 * g + e];
+          if constexpr (ROW) v[e] = v[e] * xrow[i] * wcol[e];
+        }
+        St::put(stg, out_row(i, lane), out_col(j, g, lane), u32x2_t{Op::pack2(v[0], v[1]), Op::pack2(v[2], v[3])});
+      }
+    }
   __syncthreads();
   const int mw0 = m0 + rowA0, nw0 = n0 + rowB0;
   const bool vec = p.vec_store != 0;
@@ -520,16 +564,17 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // in the reference oracle.  The per-wave partials are summed through LDS in wave
 // order (fixed order: bit-reproducible) and written as bf16.
 // ------------------------------------------------------------------------------
-template <int MT, int NW, int S>
+template <int MT, int NW, int S, int MODE = Q_BLOCK_FP8>
 struct SkinnyCfg {
-  static constexpr int MT_ = MT, NW_ = NW, S_ = S;
+  static constexpr int MT_ = MT, NW_ = NW, S_ = S, MODE_ = MODE;
+  static constexpr bool ROW = MODE != Q_BLOCK_FP8;          // scales in the epilogue only
   static constexpr int BN = 32, NB = 2, MB = MT / 16;
   static constexpr int XQ = MT / 8, WQ = BN / 8;          // 8-row DMA loads per block
-  static constexpr int SQ = (MT + 63) / 64;                // 64-row activation-scale loads
-  static constexpr int LPB = XQ + WQ + SQ + 1;             // DMA instructions per block
+  static constexpr int SQ = ROW ? 0 : (MT + 63) / 64;      // 64-row activation-scale loads
+  static constexpr int LPB = XQ + WQ + (ROW ? 0 : SQ + 1); // DMA instructions per block
   static constexpr int XS_OFF = (MT + BN) * 128;           // xs[m] of the block (fp32)
   static constexpr int WS_OFF = XS_OFF + SQ * 256;         // ws of the block (64 copies)
-  static constexpr int STAGE = WS_OFF + 256;               // bytes
+  static constexpr int STAGE = WS_OFF + (ROW ? 0 : 256);   // bytes
   static constexpr int RING = NW * S * STAGE;
   static constexpr int BNP = BN + 4;                       // padded fp32 row of the reduction
   static constexpr int RED = NW * MT * BNP * 4;
@@ -545,6 +590,8 @@ __global__ void __launch_bounds__(C::NW_ * 64)
     gemm_fp8_skinny_kernel(const Fp8Params p) {
   constexpr int MT = C::MT_, NW = C::NW_, S = C::S_, MB = C::MB, NB = C::NB, BN = C::BN;
   constexpr int XQ = C::XQ, WQ = C::WQ, SQ = C::SQ, LPB = C::LPB, STAGE = C::STAGE, BNP = C::BNP;
+  constexpr bool ROW = C::ROW, I8 = C::MODE_ == Q_ROW_I8;
+  using AccT = std::conditional_t<I8, i32x4_t, f32x4_t>;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[C::LDS];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -574,7 +621,7 @@ __global__ void __launch_bounds__(C::NW_ * 64)
       make_rsrc(p.xs, (uint32_t)(((int64_t)(p.M - 1) * p.xs_m + (int64_t)(nk - 1) * p.xs_k + 1) * 4));
   const __amdgpu_buffer_rsrc_t rws = make_rsrc(
       p.ws, (uint32_t)(((int64_t)(p.N / 128 - 1) * p.ws_n + (int64_t)(nk - 1) * p.ws_k + 1) * 4));
-  uint32_t xsoff[SQ];
+  uint32_t xsoff[SQ > 0 ? SQ : 1];
 #pragma unroll
   for (int q = 0; q < SQ; ++q) xsoff[q] = (uint32_t)((int64_t)min(64 * q + lane, p.M - 1) * p.xs_m * 4);
   const uint32_t ws_base = (uint32_t)((int64_t)(n0 / 128) * p.ws_n * 4);
@@ -591,17 +638,19 @@ __global__ void __launch_bounds__(C::NW_ * 64)
     for (int q = 0; q < XQ; ++q) buf_lds(rx, xoff[q], ko, st + q * 1024, 16);
 #pragma unroll
     for (int q = 0; q < WQ; ++q) buf_lds(rw, woff[q], ko, st + MT * 128 + q * 1024, 16);
-    const uint32_t kb = (uint32_t)(wave + NW * j);
+    if constexpr (!ROW) {
+      const uint32_t kb = (uint32_t)(wave + NW * j);
 #pragma unroll
-    for (int q = 0; q < SQ; ++q) buf_lds(rxs, xsoff[q], kb * (uint32_t)(p.xs_k * 4), st + C::XS_OFF + q * 256, 4);
-    buf_lds(rws, 0u, ws_base + kb * (uint32_t)(p.ws_k * 4), st + C::WS_OFF, 4);
+      for (int q = 0; q < SQ; ++q) buf_lds(rxs, xsoff[q], kb * (uint32_t)(p.xs_k * 4), st + C::XS_OFF + q * 256, 4);
+      buf_lds(rws, 0u, ws_base + kb * (uint32_t)(p.ws_k * 4), st + C::WS_OFF, 4);
+    }
   };
 
-  f32x4_t acc[MB][NB];
+  AccT acc[MB][NB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = AccT{0, 0, 0, 0};
 
 #pragma unroll
   for (int s = 0; s < S; ++s)
@@ -635,9 +684,11 @@ __global__ void __launch_bounds__(C::NW_ * 64)
           wf[nb] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
         }
         float sc[MB];
-        const float wsv = *(const float*)(st + C::WS_OFF);
+        if constexpr (!ROW) {
+          const float wsv = *(const float*)(st + C::WS_OFF);
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) sc[mb] = *(const float*)(st + C::XS_OFF + (mb * 16 + r) * 4) * wsv;
+          for (int mb = 0; mb < MB; ++mb) sc[mb] = *(const float*)(st + C::XS_OFF + (mb * 16 + r) * 4) * wsv;
+        }
         // the slot is free once its fragments are in registers
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         if (j + S < cnt) issue(s, j + S);
@@ -645,9 +696,22 @@ __global__ void __launch_bounds__(C::NW_ * 64)
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
-            const f32x4_t part = mma16_fp8(wf[nb], xf[mb], f32x4_t{0.f, 0.f, 0.f, 0.f});
+            if constexpr (I8) {
+              // int8 16x16x64: the 16-byte chunks g and 4 + g are two K slices
+              const i32x8_t w = wf[nb], x = xf[mb];
+              acc[mb][nb] = mma16_i8(u32x4_t{(uint32_t)w[0], (uint32_t)w[1], (uint32_t)w[2], (uint32_t)w[3]},
+                                     u32x4_t{(uint32_t)x[0], (uint32_t)x[1], (uint32_t)x[2], (uint32_t)x[3]},
+                                     acc[mb][nb]);
+              acc[mb][nb] = mma16_i8(u32x4_t{(uint32_t)w[4], (uint32_t)w[5], (uint32_t)w[6], (uint32_t)w[7]},
+                                     u32x4_t{(uint32_t)x[4], (uint32_t)x[5], (uint32_t)x[6], (uint32_t)x[7]},
+                                     acc[mb][nb]);
+            } else if constexpr (ROW) {
+              acc[mb][nb] = mma16_fp8(wf[nb], xf[mb], acc[mb][nb]);
+            } else {
+              const f32x4_t part = mma16_fp8(wf[nb], xf[mb], f32x4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[mb][nb][i] = fmaf(part[i], sc[mb], acc[mb][nb][i]);
+              for (int i = 0; i < 4; ++i) acc[mb][nb][i] = fmaf(part[i], sc[mb], acc[mb][nb][i]);
+            }
           }
       }
     }
@@ -661,7 +725,8 @@ __global__ void __launch_bounds__(C::NW_ * 64)
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
-      *(f32x4_t*)(red + (wave * MT + mb * 16 + r) * BNP + nb * 16 + 4 * g) = acc[mb][nb];
+      *(f32x4_t*)(red + (wave * MT + mb * 16 + r) * BNP + nb * 16 + 4 * g) =
+          f32x4_t{(float)acc[mb][nb][0], (float)acc[mb][nb][1], (float)acc[mb][nb][2], (float)acc[mb][nb][3]};
   __syncthreads();
   constexpr int ITEMS = MT * BN / 8;  // 8 consecutive columns per item
   const bool vec = p.vec_store != 0;
@@ -681,10 +746,15 @@ __global__ void __launch_bounds__(C::NW_ * 64)
         sum[e + 4] += b[e];
       }
     }
+    const int gn = n0 + c8;
+    if constexpr (ROW) {
+      const float xv = p.xs[(int64_t)m * p.xs_m];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sum[e] = sum[e] * xv * p.ws[(int64_t)(gn + e) * p.ws_n];
+    }
     using Op = MfmaOp<BF16>;
     const u32x4_t v{Op::pack2(sum[0], sum[1]), Op::pack2(sum[2], sum[3]), Op::pack2(sum[4], sum[5]),
                     Op::pack2(sum[6], sum[7])};
-    const int gn = n0 + c8;
     store_row8(p.y + (int64_t)m * p.ldy + gn, gn, p.N, vec, v);
   }
 }
@@ -772,4 +842,155 @@ extern "C" int kore_gemm_a8w8_blockscale(const void* xq, int64_t ldx, const void
   hipLaunchKernelGGL((gemm_fp8_bs_kernel<BM, BN>), dim3((unsigned)blocks), dim3(kEngineThreads), 0,
                      (hipStream_t)stream, p);
   return check_launch("gemm_fp8_bs_kernel");
+}
+
+// ==============================================================================
+// a8w8 GEMM with per-row activation and per-column weight scales (fp8 e4m3 or
+// int8): Y[M,N] = bf16((sum_k xq[m,k] * wq[n,k]) * xs[m] * ws[n]).  The tiled and
+// skinny kernels above run it in their row-scale modes (the K loop accumulates in
+// the MFMA registers, scales are applied once in the epilogue); anything they cannot
+// take (a K not a multiple of 128, strided or unaligned rows) runs a generic kernel.
+// ==============================================================================
+namespace kore {
+namespace {
+
+// OCP e4m3 byte -> fp32 from the format: sign bit 7, exponent bits 6..3 (bias 7),
+// mantissa bits 2..0; exponent 0 is subnormal (m * 2^-9); 0x7f / 0xff are NaN.
+__device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
+  const uint32_t e = (c >> 3) & 0xfu, m = c & 7u;
+  const float mag = e == 0 ? (float)m * 0x1p-9f : __builtin_bit_cast(float, ((e + 120u) << 23) | (m << 20));
+  const float v = (e == 0xfu && m == 7u) ? __builtin_nanf("") : mag;
+  return (c & 0x80u) ? -v : v;
+}
+
+struct A8GenericParams {
+  const uint8_t* xq;
+  const uint8_t* wq;
+  const float* xs;
+  const float* ws;
+  uint16_t* y;
+  int M, N, K;
+  int64_t ldx_m, ldx_k, ldw_n, ldw_k, xs_st, ws_st, ldy;
+};
+
+// 64x64 output tile per workgroup (4x4 per thread), 32-wide K steps staged through
+// LDS with bounds checks on every element.  int8 accumulates exactly in int32.
+template <bool I8>
+__global__ void __launch_bounds__(256) gemm_a8w8_generic_kernel(const A8GenericParams p) {
+  using V = std::conditional_t<I8, int, float>;
+  __shared__ V As[64][33];
+  __shared__ V Bs[64][33];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int m0 = (int)blockIdx.y * 64, n0 = (int)blockIdx.x * 64;
+  V acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0;
+  auto decode = [](uint8_t c) -> V {
+    if constexpr (I8) return (int)(int8_t)c;
+    else return e4m3_to_f32(c);
+  };
+  for (int k0 = 0; k0 < p.K; k0 += 32) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int idx = tid + 256 * q, r = idx >> 5, kk = idx & 31, k = k0 + kk;
+      const int m = m0 + r, n = n0 + r;
+      As[r][kk] = (m < p.M && k < p.K) ? decode(p.xq[(int64_t)m * p.ldx_m + (int64_t)k * p.ldx_k]) : (V)0;
+      Bs[r][kk] = (n < p.N && k < p.K) ? decode(p.wq[(int64_t)n * p.ldw_n + (int64_t)k * p.ldw_k]) : (V)0;
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int kk = 0; kk < 32; ++kk) {
+      V a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = As[ty * 4 + i][kk];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = Bs[tx * 4 + j][kk];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * b[j];
+    }
+    __syncthreads();
+  }
+  using Op = MfmaOp<BF16>;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + ty * 4 + i;
+    if (m >= p.M) continue;
+    const float xv = p.xs[(int64_t)m * p.xs_st];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + tx * 4 + j;
+      if (n < p.N) {
+        const float v = (float)acc[i][j] * xv * p.ws[(int64_t)n * p.ws_st];
+        p.y[(int64_t)m * p.ldy + n] = (uint16_t)(Op::pack2(v, 0.0f) & 0xffffu);
+      }
+    }
+  }
+}
+
+template <int MODE>
+int launch_a8w8(const Fp8Params& p0, bool skinny, hipStream_t st) {
+  Fp8Params p = p0;
+  if (skinny) {
+    if (p.M <= 16) return launch_fp8_skinny<SkinnyCfg<16, 8, 3, MODE>>(p, st);
+    if (p.M <= 32) return launch_fp8_skinny<SkinnyCfg<32, 8, 2, MODE>>(p, st);
+    if (p.M <= 64) return launch_fp8_skinny<SkinnyCfg<64, 4, 3, MODE>>(p, st);
+    return launch_fp8_skinny<SkinnyCfg<128, 4, 2, MODE>>(p, st);
+  }
+  const int64_t tiles256 = (int64_t)(p.M + 255) / 256 * (p.N / 256);
+  const int64_t tiles256x128 = (int64_t)(p.M + 255) / 256 * (p.N / 128);
+  if (p.N % 256 == 0 && tiles256 >= 192) return launch_fp8_pipe<F8Cfg<256, 256, 8, 2, false, MODE>>(p, st);
+  if (tiles256x128 >= 192) return launch_fp8_pipe<F8Cfg<256, 128, 8, 3, false, MODE>>(p, st);
+  return launch_fp8_pipe<F8Cfg<128, 128, 4, 4, false, MODE>>(p, st);
+}
+
+}  // namespace
+}  // namespace kore
+
+extern "C" int kore_gemm_a8w8(int qtype, const void* xq, int64_t ldx_m, int64_t ldx_k, const void* wq, int64_t ldw_n,
+                              int64_t ldw_k, const float* xs, int64_t xs_stride, const float* ws, int64_t ws_stride,
+                              void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream) {
+  using namespace kore;
+  if (!xq || !wq || !xs || !ws || !y) return set_error(KORE_EINVAL, "gemm_a8w8: null pointer");
+  if (qtype != KORE_Q_FP8 && qtype != KORE_Q_INT8) return set_error(KORE_EINVAL, "gemm_a8w8: unknown qtype %d", qtype);
+  if (M <= 0 || N <= 0 || K <= 0) return set_error(KORE_EINVAL, "gemm_a8w8: M, N, K must be >= 1");
+  if (ldy < N) return set_error(KORE_EINVAL, "gemm_a8w8: ldy (%lld) < N (%lld)", (long long)ldy, (long long)N);
+  if (M >= (1ll << 31) || N >= (1ll << 31) || K >= (1ll << 31))
+    return set_error(KORE_EUNSUPPORTED, "gemm_a8w8: dimension >= 2^31");
+  hipStream_t st = (hipStream_t)stream;
+  const bool fast = ldx_k == 1 && ldw_k == 1 && K % 128 == 0 && N % 128 == 0 && ldx_m % 16 == 0 &&
+                    ldw_n % 16 == 0 && aligned16(xq) && aligned16(wq) && 256 * ldx_m + K < (1ll << 31) &&
+                    256 * ldw_n + K < (1ll << 31) && ldx_m >= K && ldw_n >= K;
+  if (fast) {
+    Fp8Params p;
+    p.xq = (const uint8_t*)xq;
+    p.wq = (const uint8_t*)wq;
+    p.xs = xs;
+    p.ws = ws;
+    p.y = (uint16_t*)y;
+    p.M = (int)M;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.ldx = ldx_m;
+    p.ldw = ldw_n;
+    p.ldy = ldy;
+    p.xs_m = xs_stride;
+    p.xs_k = 0;
+    p.ws_n = ws_stride;
+    p.ws_k = 0;
+    p.tiles_m = p.tiles_n = 0;
+    p.vec_store = (ldy % 8 == 0) && aligned16(y);
+    const bool skinny = M <= 128;
+    return qtype == KORE_Q_FP8 ? launch_a8w8<Q_ROW_FP8>(p, skinny, st) : launch_a8w8<Q_ROW_I8>(p, skinny, st);
+  }
+  A8GenericParams g{(const uint8_t*)xq, (const uint8_t*)wq, xs, ws, (uint16_t*)y, (int)M, (int)N, (int)K,
+                    ldx_m, ldx_k, ldw_n, ldw_k, xs_stride, ws_stride, ldy};
+  const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
+  if (grid.y > 65535) return set_error(KORE_EUNSUPPORTED, "gemm_a8w8: M too large for the generic kernel");
+  if (qtype == KORE_Q_FP8) hipLaunchKernelGGL(gemm_a8w8_generic_kernel<false>, grid, dim3(256), 0, st, g);
+  else hipLaunchKernelGGL(gemm_a8w8_generic_kernel<true>, grid, dim3(256), 0, st, g);
+  return check_launch("gemm_a8w8_generic_kernel");
 }

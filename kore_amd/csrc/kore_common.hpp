@@ -9,6 +9,9 @@
 //     (l % 32), K offset 32*(l/32); same output layout.
 //   v_mfma_f32_16x16x32_bf16: lane l holds 8 K values of row (l % 16) at K offset
 //     8*(l/16); output register i is D[4*(l/16) + i][l % 16].
+//   v_mfma_f32_16x16x128_f8f6f4, v_mfma_i32_{32x32x32,16x16x64}_i8: row (l % 32) or
+//     (l % 16) per lane, output layouts as above (pinned by the GPU parity tests
+//     of the kernels that use them).
 // Only the pairing of A and B K-slots matters for a product, and both operands are
 // always staged with the same K mapping.
 #pragma once
@@ -24,6 +27,7 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef int i32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -76,6 +80,17 @@ __device__ __forceinline__ f32x16_t mma32_fp8(i32x8_t a, i32x8_t b, f32x16_t c) 
 }
 __device__ __forceinline__ f32x4_t mma16_fp8(i32x8_t a, i32x8_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// int8 MFMAs (int32 accumulate): 16 K-bytes per lane, the same row-per-lane layout and
+// output layout as the 16-bit shapes of the same M x N.
+__device__ __forceinline__ i32x16_t mma32_i8(u32x4_t a, u32x4_t b, i32x16_t c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4_t, a), __builtin_bit_cast(i32x4_t, b), c, 0,
+                                               0, 0);
+}
+__device__ __forceinline__ i32x4_t mma16_i8(u32x4_t a, u32x4_t b, i32x4_t c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4_t, a), __builtin_bit_cast(i32x4_t, b), c, 0,
+                                               0, 0);
 }
 
 // Epilogue activations (fp32), KORE act codes, built on the hardware exp2 and

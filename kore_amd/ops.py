@@ -16,6 +16,8 @@ Entry points and the reference callables they replace:
 ``batched_gemm(a, b)``     ``kore/tasks/vendor_ops.py:914-920``
 ``gemm_a8w8_blockscale``   ``kore/tasks/gemm_fp8_a8w8_blockscale/seed_triton.py:49-60``
 (task entry name ``gemm``)
+``gemm_a8w8``              ``kore/tasks/gemm_{fp8_a8w8,fp8_a8w8_pertoken,fp8_a8w8_pertensor,
+                           int8_a8w8}/seed_triton.py``; ``kore/tasks/vendor_ops.py:697-760``
 ``fused_moe(...)``         ``kore/tasks/fused_moe_silu_bf16/seed_triton.py:69-86``
 ``moe_align(ids, E, blk)`` sort/align stage (``kore/tasks/breadth/moe_ext.py:617-621``)
 =========================  =======================================================
@@ -183,6 +185,53 @@ def gemm_a8w8_blockscale(xq: torch.Tensor, wq: torch.Tensor, x_scale: torch.Tens
                                        x_scale.data_ptr(), x_scale.stride(0), x_scale.stride(1),
                                        w_scale.data_ptr(), w_scale.stride(0), w_scale.stride(1),
                                        y.data_ptr(), y.stride(0), M, N, K, _stream(xq))
+    _lib.check(rc)
+    return y
+
+
+# --------------------------------------------------------------------------- #
+# a8w8 GEMM with per-row / per-column scales (fp8 e4m3 or int8)
+# --------------------------------------------------------------------------- #
+Q_CODE = {FP8_DTYPE: 0, torch.int8: 1}
+
+
+def _scale_vector(s: torch.Tensor, n: int, what: str) -> tuple[torch.Tensor, int]:
+    """A [n,1] / [1,n] / [n] fp32 scale as (tensor, element stride along n)."""
+    if s.dtype != torch.float32:
+        raise ValueError(f"{what} must be fp32 (got {s.dtype})")
+    if s.numel() != n or not (s.dim() == 1 or (s.dim() == 2 and 1 in s.shape)):
+        raise ValueError(f"{what} must hold {n} values as [{n},1], [1,{n}] or [{n}] (got {tuple(s.shape)})")
+    along_dim0 = s.dim() == 1 or s.shape[0] == n
+    return s, s.stride(0) if along_dim0 else s.stride(1)
+
+
+def gemm_a8w8(xq: torch.Tensor, wq: torch.Tensor, x_scale: torch.Tensor,
+              w_scale: torch.Tensor) -> torch.Tensor:
+    """8-bit a8w8 GEMM -> bf16 [M,N]: ``(xq * x_scale) @ (wq * w_scale)^T``.
+
+    xq[M,K], wq[N,K] both ``float8_e4m3fn`` or both ``int8`` (any strides),
+    x_scale [M,1] (per token; per tensor = equal entries), w_scale [1,N] / [N,1] / [N]
+    (per output channel), fp32.  Each scale is applied once to the fp32 (int8: exact
+    int32) accumulator.
+    """
+    _require_cuda(xq, wq, x_scale, w_scale)
+    if xq.dtype not in Q_CODE or wq.dtype != xq.dtype:
+        raise ValueError(f"xq/wq must both be float8_e4m3fn or both int8 (got {xq.dtype}, {wq.dtype})")
+    if xq.dim() != 2 or wq.dim() != 2 or xq.shape[1] != wq.shape[1]:
+        raise ValueError(f"expected xq[M,K], wq[N,K] (got {tuple(xq.shape)}, {tuple(wq.shape)})")
+    M, K = xq.shape
+    N = wq.shape[0]
+    xs, xs_st = _scale_vector(x_scale, M, "x_scale")
+    ws, ws_st = _scale_vector(w_scale, N, "w_scale")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=xq.device)
+    if M == 0 or N == 0:
+        return y
+    if K == 0:
+        return y.zero_()
+    lib = _lib.load()
+    rc = lib.kore_gemm_a8w8(Q_CODE[xq.dtype], xq.data_ptr(), xq.stride(0), xq.stride(1), wq.data_ptr(),
+                            wq.stride(0), wq.stride(1), xs.data_ptr(), xs_st, ws.data_ptr(), ws_st,
+                            y.data_ptr(), y.stride(0), M, N, K, _stream(xq))
     _lib.check(rc)
     return y
 

@@ -1,12 +1,12 @@
 """Roofline model for the GEMM family on MI355X.
 
 FLOP and byte counts follow the reference's scorer (``kore/analysis/rooflines.py:153-282``):
-GEMM ``F = 2MNK``, ``Q = (MK + KN + MN)*e``; fp8 GEMM ``Q = (MK + KN)*1 + MN*2``;
+GEMM ``F = 2MNK``, ``Q = (MK + KN + MN)*e``; fp8 / int8 GEMM ``Q = (MK + KN)*1 + MN*2``;
 batched/grouped GEMM multiply both by B; fused MoE ``F = M*topk*6*D*I``,
 ``Q = (E*3*D*I + 2*M*D)*e``.  ``T_min = max(F/peak_flops, Q/peak_bw)``.
 
 Peaks are MI355X's published dense figures (no sparsity): bf16/fp16 2.5 PFLOP/s,
-fp8 5.0 PFLOP/s, HBM3E 8.0 TB/s.  ``KORE_PEAK_BF16`` / ``KORE_PEAK_FP8`` /
+fp8 5.0 PFLOP/s, int8 5.0 POP/s, HBM3E 8.0 TB/s.  ``KORE_PEAK_BF16`` / ``KORE_PEAK_FP8`` /
 ``KORE_PEAK_HBM_BW`` override them as in the reference (``rooflines.py:84-97``).
 """
 
@@ -50,7 +50,7 @@ def flops_bytes(operation: str, dims: dict[str, int], dtype: str) -> tuple[float
     """Algorithmic (FLOPs, HBM bytes) of one call, per the reference's formulas."""
     op = operation.lower()
     e = dtype_bytes(dtype)
-    fp8 = "fp8" in dtype.lower()
+    fp8 = "fp8" in dtype.lower() or "int8" in dtype.lower()  # 8-bit operands, bf16 output
     if "batched_gemm" in op or "grouped_gemm" in op or op == "bmm":
         B = dims.get("B", dims.get("batch", 1))
         M, N, K = dims["M"], dims["N"], dims["K"]
@@ -82,7 +82,8 @@ def roofline(operation: str, dims: dict[str, int], dtype: str) -> Roofline:
     peaks = resolve_peaks()
     f, q = flops_bytes(operation, dims, dtype)
     d = dtype.lower()
-    pf = peaks["fp8_flops_per_s"] if "fp8" in d else peaks["bf16_flops_per_s"]
+    pf = peaks["fp8_flops_per_s"] if "fp8" in d else peaks["int8_flops_per_s"] if "int8" in d else \
+        peaks["bf16_flops_per_s"]
     pb = peaks["hbm_bytes_per_s"]
     tc, tm = f / pf, q / pb
     return Roofline(f, q, tc, tm, max(tc, tm), "mfma" if tc >= tm else "hbm", pf, pb)

@@ -81,6 +81,45 @@ def fp8_inputs(M: int, N: int, K: int, seed: int = 0, device="cpu", scale: float
     return xq, wq, xs, ws
 
 
+def _q8_rowwise(x: torch.Tensor, kind: str):
+    """Per-row symmetric quantisation (fp8 e4m3 max 448 / int8 max 127); scale [R,1]."""
+    qmax = 448.0 if kind == "fp8" else 127.0
+    s = (x.float().abs().amax(dim=-1, keepdim=True).clamp(min=1e-12) / qmax).to(torch.float32)
+    if kind == "fp8":
+        return (x.float() / s).clamp(-qmax, qmax).to(FP8), s
+    return (x.float() / s).round().clamp(-qmax, qmax).to(torch.int8), s
+
+
+def a8w8_inputs(M: int, N: int, K: int, kind: str = "fp8", mode: str = "pertoken", seed: int = 0,
+                device="cpu", transpose_a: bool = False):
+    """(xq[M,K], wq[N,K], x_scale[M,1], w_scale[1,N]) of the a8w8 tasks: X, W ~ N(0,1);
+    ``pertoken`` quantises X per row and W per output channel, ``pertensor`` uses one
+    scale per tensor broadcast to those shapes.  ``transpose_a`` returns xq as a
+    non-contiguous [M,K] view of a [K,M] buffer (the per-token task's TA case)."""
+    g = _gen(device, seed)
+    X = torch.randn((K, M) if transpose_a else (M, K), generator=g, device=device)
+    W = torch.randn((N, K), generator=g, device=device)
+    if mode == "pertensor":
+        qmax = 448.0 if kind == "fp8" else 127.0
+        sx = (X.abs().max().clamp(min=1e-12) / qmax).to(torch.float32)
+        sw = (W.abs().max().clamp(min=1e-12) / qmax).to(torch.float32)
+        xq = (X / sx).clamp(-qmax, qmax)
+        wq = (W / sw).clamp(-qmax, qmax)
+        xq = xq.to(FP8) if kind == "fp8" else xq.round().to(torch.int8)
+        wq = wq.to(FP8) if kind == "fp8" else wq.round().to(torch.int8)
+        if transpose_a:
+            xq = xq.t()
+        return xq, wq, sx.reshape(1, 1).repeat(M, 1).contiguous(), sw.reshape(1, 1).repeat(1, N).contiguous()
+    if transpose_a:
+        xq_t, xs_t = _q8_rowwise(X.t().contiguous(), kind)
+        xq = xq_t.t().contiguous().t()  # [M,K] view of a [K,M] buffer
+        xs = xs_t
+    else:
+        xq, xs = _q8_rowwise(X, kind)
+    wq, ws = _q8_rowwise(W, kind)
+    return xq, wq, xs, ws.reshape(1, N).contiguous()
+
+
 def route(logits: torch.Tensor, topk: int, renorm: bool = True):
     probs = torch.softmax(logits.float(), dim=-1)
     tw, ti = torch.topk(probs, topk, dim=-1)
@@ -157,6 +196,17 @@ def bench_workloads():
     w["bf16_batched_64x1024x1024x128"] = batched
     for M in (512, 128, 16):
         w[f"fp8_blockscale_{M}x7168x4096"] = fp8(M)
+    def a8w8(M, N, K, kind):
+        def build(dev):
+            xq, wq, xs, ws = a8w8_inputs(M, N, K, kind, "pertoken", seed=0, device=dev)
+            return (lambda: kore_amd.gemm_a8w8(xq, wq, xs, ws)), "gemm_a8w8", \
+                {"M": M, "N": N, "K": K}, kind
+        return build
+
+    # a8w8 with per-token / per-channel scales (task primaries + decode)
+    w["fp8_a8w8_pertoken_4096"] = a8w8(4096, 4096, 4096, "fp8")
+    w["int8_a8w8_4096"] = a8w8(4096, 4096, 4096, "int8")
+    w["fp8_a8w8_pertoken_16x4096x4096"] = a8w8(16, 4096, 4096, "fp8")
     w["moe_decode_T64"] = moe(64)
     w["moe_prefill_T4096"] = moe(4096)
     return w

@@ -88,3 +88,63 @@ def matmul_blockscale_ref(xq, wq, xs, ws) -> torch.Tensor:
     wd = (wq.view(N // BLK, BLK, K // BLK, BLK).float()
           * ws.float()[:, None, :, None]).view(N, K)
     return (xd @ wd.t()).to(torch.bfloat16)
+
+
+# --------------------------------------------------------------------------- #
+# a8w8 GEMM with per-row activation and per-column weight scales (fp8 / int8)
+# --------------------------------------------------------------------------- #
+INT8_MAX = 127.0     # kore/tasks/_quant_common.py INT8_MAX (symmetric int8)
+
+
+def quant_per_tensor_fp8(x: torch.Tensor):
+    """Per-tensor fp8: x -> (xq e4m3, scalar fp32 scale); ``amax`` floored at 1e-12.
+
+    Follows ``kore/tasks/_quant_common.py:77-83`` (``quant_per_tensor_fp8``).
+    """
+    amax = x.float().abs().max().clamp(min=1e-12)
+    s = (amax / FP8_MAX).to(torch.float32)
+    xq = (x.float() / s).clamp(-FP8_MAX, FP8_MAX).to(FP8_DTYPE)
+    return xq, s.reshape(())
+
+
+def quant_rowwise_fp8(x: torch.Tensor):
+    """Per-row fp8: x[R,K] -> (xq[R,K] e4m3, scale[R,1] fp32); ``x ~= xq * scale``.
+
+    Follows ``kore/tasks/_quant_common.py:86-93`` (``quant_rowwise_fp8``).
+    """
+    amax = x.float().abs().amax(dim=-1, keepdim=True).clamp(min=1e-12)
+    s = (amax / FP8_MAX).to(torch.float32)
+    return (x.float() / s).clamp(-FP8_MAX, FP8_MAX).to(FP8_DTYPE), s
+
+
+def quant_rowwise_int8(x: torch.Tensor):
+    """Per-row symmetric int8: x[R,K] -> (xq[R,K] int8, scale[R,1] fp32).
+
+    ``q = clamp(round(x / s), +-127)`` with round-half-even, ``s = max(amax, 1e-12)/127``;
+    follows ``kore/tasks/_quant_common.py:96-101`` (``quant_rowwise_int8``).
+    """
+    amax = x.float().abs().amax(dim=-1, keepdim=True).clamp(min=1e-12)
+    s = (amax / INT8_MAX).to(torch.float32)
+    return (x.float() / s).round().clamp(-INT8_MAX, INT8_MAX).to(torch.int8), s
+
+
+def quant_per_tensor_int8(x: torch.Tensor):
+    """Per-tensor symmetric int8 (``kore/tasks/vendor_ops.py:163-177``, int8 branch)."""
+    amax = x.float().abs().max().clamp(min=1e-12)
+    s = (amax / INT8_MAX).to(torch.float32)
+    return (x.float() / s).round().clamp(-INT8_MAX, INT8_MAX).to(torch.int8), s.reshape(())
+
+
+def matmul_a8w8_ref(xq, wq, x_scale, w_scale) -> torch.Tensor:
+    """8-bit (fp8 / int8) a8w8 GEMM oracle -> bf16 [M,N].
+
+    ``(xq * x_scale[M,1]) @ (wq * w_scale.reshape(-1,1))^T`` in fp32, one cast; covers
+    per-tensor (equal scales), per-token / per-channel and int8.  Follows
+    ``kore/tasks/_quant_common.py:236-242`` (``matmul_a8w8_fp32``).  Pinned in
+    ``tests/test_oracle_quant.py`` by the reference test's explicit dequant
+    (``tests/test_vendor_ops.py:38-65``), exact int64 arithmetic for int8 on small K,
+    and power-of-two scale invariance.
+    """
+    a = xq.float() * x_scale.float().reshape(-1, 1)
+    w = wq.float() * w_scale.float().reshape(-1, 1)
+    return (a @ w.t()).to(torch.bfloat16)

@@ -188,6 +188,11 @@ EXPECTED_ENTRIES = {
     "moe_batched_gemm_bf16": ("batched_gemm", 2), "gemm_fp8_a8w8_blockscale": ("gemm", 4),
     "genv_gemm_a8w8_blockscale_fp8": ("gemm_a8w8_blockscale", 4),
     "fused_moe_silu_bf16": ("fused_moe", 5),
+    # a8w8 with per-row/per-column scales: gemm_fp8_a8w8/driver.py:40 takes ``gemm_fp8``;
+    # the _quant_common tasks take ENTRY = "gemm"; vendor_ops.py:742 ``gemm_a8w8``
+    "gemm_fp8_a8w8": ("gemm_fp8", 4), "gemm_fp8_a8w8_pertoken": ("gemm", 4),
+    "gemm_fp8_a8w8_pertensor": ("gemm", 4), "gemm_int8_a8w8": ("gemm", 4),
+    "genv_gemm_a8w8_fp8": ("gemm_a8w8", 4), "genv_gemm_a8w8_int8": ("gemm_a8w8", 4),
 }
 
 

@@ -141,3 +141,74 @@ def test_workload_quantisers_match_oracle_bit_exact():
     b1, t1 = W.quant_128x128(w)
     b2, t2 = quant_128x128_fp8(w)
     assert torch.equal(b1.view(torch.uint8), b2.view(torch.uint8)) and torch.equal(t1, t2)
+
+
+# ---------------------------------------------------------------------------
+# a8w8 (per-row / per-column scales, fp8 and int8)
+# ---------------------------------------------------------------------------
+from oracle.quant import (  # noqa: E402
+    matmul_a8w8_ref, quant_per_tensor_fp8, quant_per_tensor_int8, quant_rowwise_fp8, quant_rowwise_int8,
+)
+
+
+def test_int8_quantiser_rounding_and_clamp():
+    """Symmetric int8: s = amax/127, q = clamp(round-half-even(x/s), +-127)."""
+    x = torch.tensor([[127.0, 0.5, 1.5, -2.5, 63.5, -127.0]])
+    q, s = quant_rowwise_int8(x)
+    assert s.shape == (1, 1) and float(s) == 1.0
+    assert q.tolist() == [[127, 0, 2, -2, 64, -127]]
+    z, sz = quant_rowwise_int8(torch.zeros(2, 4))
+    assert torch.all(z == 0) and torch.all(sz == 1e-12 / 127.0)
+    qt, st = quant_per_tensor_int8(torch.tensor([[1.0, -254.0]]))
+    assert float(st) == 2.0 and qt.tolist() == [[0, -127]]
+
+
+def test_rowwise_fp8_quantiser_roundtrip():
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(16, 96, generator=g) * 3
+    q, s = quant_rowwise_fp8(x)
+    assert q.dtype == torch.float8_e4m3fn and s.shape == (16, 1)
+    assert torch.allclose(s[:, 0], x.abs().amax(-1) / 448.0)
+    assert torch.all(q.float().abs().amax(-1) == 448.0)  # each row's amax maps to 448
+    # relative error of an e4m3 normal is at most half an ulp (2^-4)
+    rel = ((q.float() * s - x).abs() / x.abs().clamp(min=1e-3 * float(s.max())))
+    assert float(rel.max()) <= 2.0 ** -4 + 1e-6
+    qt, st = quant_per_tensor_fp8(x)
+    assert st.shape == () and float(qt.float().abs().max()) == 448.0
+
+
+@pytest.mark.parametrize("kind", ["fp8", "int8"])
+def test_a8w8_oracle_matches_explicit_dequant(kind):
+    """The reference's own checks (tests/test_vendor_ops.py:38-65): the oracle equals the
+    explicit dequantised matmul at M=8, N=16, K=32."""
+    g = torch.Generator().manual_seed(0)
+    a, w = torch.randn(8, 32, generator=g), torch.randn(16, 32, generator=g)
+    quant = quant_rowwise_fp8 if kind == "fp8" else quant_rowwise_int8
+    xq, xs = quant(a)
+    wq, wsc = quant(w)
+    ws = wsc.reshape(1, 16)
+    out = matmul_a8w8_ref(xq, wq, xs, ws)
+    assert out.shape == (8, 16) and out.dtype == torch.bfloat16
+    exp = (xq.float() * xs.float()) @ (wq.float() * ws.float().reshape(-1, 1)).t()
+    assert torch.allclose(out.float(), exp, atol=1e-2, rtol=1e-2)
+    # the weight scale belongs to output columns: applying it per row must differ
+    wrong = ((xq.float() * ws.float().reshape(1, -1)[:, :8].reshape(-1, 1)) @ (wq.float() * xs.float()[:1]).t())
+    assert not torch.allclose(out.float(), wrong, atol=1e-2, rtol=1e-2)
+
+
+def test_a8w8_int8_exact_and_scale_invariance():
+    """int8 products and sums up to K=64 are exact integers in fp32: with unit scales the
+    oracle is the int64 matmul rounded once to bf16; doubling x_scale doubles Y exactly."""
+    g = torch.Generator().manual_seed(5)
+    xq = torch.randint(-127, 128, (12, 64), generator=g, dtype=torch.int8)
+    wq = torch.randint(-127, 128, (20, 64), generator=g, dtype=torch.int8)
+    one_x, one_w = torch.ones(12, 1), torch.ones(1, 20)
+    exact = (xq.long() @ wq.long().t()).double().float().to(torch.bfloat16)
+    assert torch.equal(matmul_a8w8_ref(xq, wq, one_x, one_w), exact)
+    xs = torch.rand(12, 1, generator=g) + 0.5
+    ws = torch.rand(1, 20, generator=g) + 0.5
+    y1 = matmul_a8w8_ref(xq, wq, xs, ws)
+    assert torch.equal(matmul_a8w8_ref(xq, wq, xs * 2, ws), (y1.float() * 2).to(torch.bfloat16))
+    # w_scale given as [N,1] or [N] is the same operand
+    assert torch.equal(matmul_a8w8_ref(xq, wq, xs, ws.reshape(20, 1)), y1)
+    assert torch.equal(matmul_a8w8_ref(xq, wq, xs, ws.reshape(20)), y1)
