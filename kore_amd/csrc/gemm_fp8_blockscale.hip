@@ -540,12 +540,13 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // ------------------------------------------------------------------------------
 // Skinny-M kernel (M <= 128): the product is bound by streaming W once from HBM, and
 // a 256-row tile would leave most CUs idle (N / 128 workgroups).  A workgroup owns
-// BN = 32 columns and every row of M (padded to MT); its NW waves split the K blocks
-// (wave w takes blocks w, w+NW, ...), so the grid is N / 32 workgroups that each
-// stream their 32 rows of W exactly once.
+// BN = 16*NB columns (32, or 16 when N / 32 workgroups would not cover the CUs) and
+// every row of M (padded to MT); its NW waves split the K blocks (wave w takes blocks
+// w, w+NW, ...), so the grid is N / BN workgroups that each stream their BN rows of W
+// exactly once.
 //
 // Each wave has a private ring of S LDS stages (one K block each: MT rows of X, then
-// 32 rows of W, 128 bytes per row) filled by direct-to-LDS buffer loads in which one
+// BN rows of W, 128 bytes per row) filled by direct-to-LDS buffer loads in which one
 // wave instruction covers 8 whole 128-byte rows (full cache lines: an MFMA-layout
 // register load would split every line over two instructions, which measured 1.5x
 // slower for the weight stream).  Waves share nothing, so a stage is consumed after
@@ -564,11 +565,11 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // in the reference oracle.  The per-wave partials are summed through LDS in wave
 // order (fixed order: bit-reproducible) and written as bf16.
 // ------------------------------------------------------------------------------
-template <int MT, int NW, int S, int MODE = Q_BLOCK_FP8>
+template <int MT, int NW, int S, int MODE = Q_BLOCK_FP8, int NB_ = 2>
 struct SkinnyCfg {
   static constexpr int MT_ = MT, NW_ = NW, S_ = S, MODE_ = MODE;
   static constexpr bool ROW = MODE != Q_BLOCK_FP8;          // scales in the epilogue only
-  static constexpr int BN = 32, NB = 2, MB = MT / 16;
+  static constexpr int NB = NB_, BN = 16 * NB, MB = MT / 16;  // 16-column blocks per workgroup
   static constexpr int XQ = MT / 8, WQ = BN / 8;          // 8-row DMA loads per block
   static constexpr int SQ = ROW ? 0 : (MT + 63) / 64;      // 64-row activation-scale loads
   static constexpr int LPB = XQ + WQ + (ROW ? 0 : SQ + 1); // DMA instructions per block
@@ -601,7 +602,7 @@ __global__ void __launch_bounds__(C::NW_ * 64)
   const int nk = p.K / 128;
   const int cnt = nk > wave ? (nk - wave + NW - 1) / NW : 0;  // K blocks of this wave
 
-  // buffer resources: X rows [0, M), this workgroup's 32 rows of W
+  // buffer resources: X rows [0, M), this workgroup's BN rows of W
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.xq, (uint32_t)((int64_t)(p.M - 1) * p.ldx + p.K));
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.wq + (int64_t)n0 * p.ldw, (uint32_t)((BN - 1) * p.ldw + p.K));
   // DMA load q covers LDS rows 8q .. 8q+7; lane l fetches row 8q + l/8, logical chunk
@@ -935,6 +936,13 @@ template <int MODE>
 int launch_a8w8(const Fp8Params& p0, bool skinny, hipStream_t st) {
   Fp8Params p = p0;
   if (skinny) {
+    // 16-column workgroups when 32-column ones would leave CUs idle (N < 8192)
+    if (p.N / 32 < 256) {
+      if (p.M <= 16) return launch_fp8_skinny<SkinnyCfg<16, 8, 3, MODE, 1>>(p, st);
+      if (p.M <= 32) return launch_fp8_skinny<SkinnyCfg<32, 8, 3, MODE, 1>>(p, st);
+      if (p.M <= 64) return launch_fp8_skinny<SkinnyCfg<64, 8, 2, MODE, 1>>(p, st);
+      return launch_fp8_skinny<SkinnyCfg<128, 4, 2, MODE, 1>>(p, st);
+    }
     if (p.M <= 16) return launch_fp8_skinny<SkinnyCfg<16, 8, 3, MODE>>(p, st);
     if (p.M <= 32) return launch_fp8_skinny<SkinnyCfg<32, 8, 2, MODE>>(p, st);
     if (p.M <= 64) return launch_fp8_skinny<SkinnyCfg<64, 4, 3, MODE>>(p, st);

@@ -74,10 +74,12 @@ def test_genv_gemm_a8w8_task(gpu, kind, M, N, K):
 
 @pytest.mark.parametrize("kind", ["fp8", "int8"])
 @pytest.mark.parametrize("M,N,K", [(1, 128, 128), (33, 256, 640), (100, 384, 1152), (128, 512, 256),
-                                   (129, 256, 384), (300, 384, 640), (200, 300, 256), (96, 128, 100)])
+                                   (20, 8192, 256), (100, 8192, 384), (129, 256, 384), (300, 384, 640),
+                                   (200, 300, 256), (96, 128, 100)])
 def test_a8w8_paths(gpu, kind, M, N, K):
-    """Every kernel path: skinny (M <= 128), tiled (M > 128, 128x128 / 256x128 tiles),
-    generic (N % 128 != 0, K % 128 != 0); ragged M throughout."""
+    """Every kernel path: skinny (M <= 128; 16-column workgroups below N = 8192,
+    32-column ones from it), tiled (M > 128, 128x128 / 256x128 tiles), generic
+    (N % 128 != 0, K % 128 != 0); ragged M throughout."""
     _check(gpu, kind, "pertoken", M, N, K, seed=M + K)
 
 
