@@ -23,7 +23,7 @@ if ROOT not in sys.path:
 from kore_amd import workloads as W  # noqa: E402
 from oracle.gemm import batched_gemm_ref, gemm_fusion_ref, matmul_ref  # noqa: E402
 from oracle.moe import moe_align_ref, moe_ref, trace32_bias  # noqa: E402
-from oracle.quant import matmul_blockscale_ref  # noqa: E402
+from oracle.quant import matmul_a8w8_ref, matmul_blockscale_ref  # noqa: E402
 
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden.pt")
 
@@ -41,6 +41,10 @@ def build() -> dict:
     xq, wq, xs, ws = W.fp8_inputs(40, 256, 384, seed=14)
     g["fp8_blockscale"] = {"xq": xq.view(torch.uint8), "wq": wq.view(torch.uint8), "xs": xs, "ws": ws,
                            "out": matmul_blockscale_ref(xq, wq, xs, ws)}
+    for kind, seed in (("fp8", 16), ("int8", 17)):
+        xq, wq, xs, ws = W.a8w8_inputs(24, 256, 384, kind, "pertoken", seed=seed)
+        u8 = (lambda t: t.view(torch.uint8)) if kind == "fp8" else (lambda t: t)
+        g[f"a8w8_{kind}"] = {"xq": u8(xq), "wq": u8(wq), "xs": xs, "ws": ws, "out": matmul_a8w8_ref(xq, wq, xs, ws)}
     hidden, w1, w2, tw, ti = W.moe_inputs(24, 4, 2, 128, 128, seed=15, wscale=0.05, router_bias=trace32_bias(4))
     g["fused_moe"] = {"hidden": hidden, "w1": w1, "w2": w2, "tw": tw, "ti": ti,
                       "out": moe_ref(hidden, w1, w2, tw, ti)}

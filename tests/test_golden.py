@@ -15,7 +15,7 @@ import torch
 from kore_amd import workloads as W
 from oracle.gemm import batched_gemm_ref, gemm_fusion_ref, matmul_ref
 from oracle.moe import moe_align_ref, moe_ref, trace32_bias
-from oracle.quant import matmul_blockscale_ref
+from oracle.quant import matmul_a8w8_ref, matmul_blockscale_ref
 from tests.fourprong import verdict
 
 GOLDEN = torch.load(Path(__file__).parent / "golden" / "golden.pt", weights_only=True)
@@ -36,6 +36,8 @@ def test_golden_inputs_are_the_seeded_draws():
     assert _eq(xq.view(torch.uint8), GOLDEN["fp8_blockscale"]["xq"]) and _eq(ws, GOLDEN["fp8_blockscale"]["ws"])
     hidden, w1, w2, tw, ti = W.moe_inputs(24, 4, 2, 128, 128, seed=15, wscale=0.05, router_bias=trace32_bias(4))
     assert _eq(ti, GOLDEN["fused_moe"]["ti"]) and _eq(w2, GOLDEN["fused_moe"]["w2"])
+    xq, wq, xs, ws = W.a8w8_inputs(24, 256, 384, "int8", "pertoken", seed=17)
+    assert _eq(xq, GOLDEN["a8w8_int8"]["xq"]) and _eq(ws, GOLDEN["a8w8_int8"]["ws"])
 
 
 def test_oracle_reproduces_golden_outputs():
@@ -50,6 +52,10 @@ def test_oracle_reproduces_golden_outputs():
     assert _eq(matmul_blockscale_ref(g["xq"].view(FP8), g["wq"].view(FP8), g["xs"], g["ws"]), g["out"])
     g = GOLDEN["fused_moe"]
     assert _eq(moe_ref(g["hidden"], g["w1"], g["w2"], g["tw"], g["ti"]), g["out"])
+    g = GOLDEN["a8w8_fp8"]
+    assert _eq(matmul_a8w8_ref(g["xq"].view(FP8), g["wq"].view(FP8), g["xs"], g["ws"]), g["out"])
+    g = GOLDEN["a8w8_int8"]
+    assert _eq(matmul_a8w8_ref(g["xq"], g["wq"], g["xs"], g["ws"]), g["out"])
     g = GOLDEN["moe_align"]
     off, srt, blk = moe_align_ref(g["ti"], int(g["E"]), int(g["block"]))
     assert np.array_equal(off, g["offsets"].numpy()) and np.array_equal(srt, g["sorted"].numpy())
@@ -73,6 +79,12 @@ def test_hip_matches_golden(gpu):
     g = GOLDEN["fp8_blockscale"]
     out = kore_amd.gemm_a8w8_blockscale(d(g["xq"]).view(FP8), d(g["wq"]).view(FP8), d(g["xs"]), d(g["ws"]))
     verdict(out, g["out"], "blockscale", "fp8", "golden fp8_blockscale")
+    g = GOLDEN["a8w8_fp8"]
+    out = kore_amd.gemm_a8w8(d(g["xq"]).view(FP8), d(g["wq"]).view(FP8), d(g["xs"]), d(g["ws"]))
+    verdict(out, g["out"], "a8w8", "fp8", "golden a8w8_fp8")
+    g = GOLDEN["a8w8_int8"]
+    out = kore_amd.gemm_a8w8(d(g["xq"]), d(g["wq"]), d(g["xs"]), d(g["ws"]))
+    verdict(out, g["out"], "a8w8", "int8", "golden a8w8_int8")
     g = GOLDEN["fused_moe"]
     out = kore_amd.fused_moe(d(g["hidden"]), d(g["w1"]), d(g["w2"]), d(g["tw"]), d(g["ti"]))
     verdict(out, g["out"], "fused_moe", "bf16", "golden fused_moe")
