@@ -158,6 +158,41 @@ int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, const void* 
                    int64_t T, int64_t D, int64_t I, int64_t E, int64_t topk,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Top-1 grouped (segmented) expert GEMM (bf16):
+ *   out[m, :] = x[m, :] @ w[expert_ids[m]]^T,  fp32 accumulate, bf16 out in token order
+ *   x [M,K] row stride ldx; w [E,N,K] contiguous; expert_ids [M] int32 (ids outside
+ *   [0,E) leave their row unwritten); out [M,N] row stride ldo.  Tokens are sorted
+ *   and block-aligned per expert on the device (the sort/align kernel above), then one
+ *   grouped MFMA launch covers every expert.  `workspace` must hold
+ *   kore_moe_grouped_gemm_workspace_bytes(M, E) bytes.  Requires N % 128 == 0 and
+ *   K % 8 == 0 (KORE_EUNSUPPORTED otherwise).
+ * Replaces: grouped_gemm(hidden, w, expert_ids)
+ *           kore/tasks/moe_grouped_gemm_bf16/seed_triton.py (ENTRY reference.py:25;
+ *           oracle _moe_common.py:203-226); moe_grouped_gemm(hidden, w, expert_ids)
+ *           kore/tasks/breadth/moe_ext.py:625-636 (genb_moe_grouped_gemm_bf16).
+ */
+size_t kore_moe_grouped_gemm_workspace_bytes(int64_t M, int64_t E);
+int kore_moe_grouped_gemm(const void* x, int64_t ldx, const void* w, const int32_t* expert_ids,
+                          void* out, int64_t ldo, int64_t M, int64_t N, int64_t K, int64_t E,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Token permute / unpermute as row copies of any element type:
+ *   gather:  dst[i, :] = src[idx[i], :] for i < n (idx outside [0, src_rows): zero row)
+ *   scatter: dst[idx[i], :] = src[i, :] for i < n (idx outside [0, dst_rows): skipped)
+ *   Strides and the row length are in bytes.  idx [n] int32, device.
+ * Replaces: moe_permute(hidden, sort_idx) kore/tasks/moe_permute_bf16/seed_triton.py
+ *           (oracle reference.py:56-59) and kore/tasks/breadth/moe_ext.py:546-556;
+ *           moe_unpermute(permuted, sort_idx) kore/tasks/breadth/moe_ext.py:558-571.
+ */
+int kore_gather_rows(const void* src, int64_t ld_src_bytes, int64_t src_rows,
+                     const int32_t* idx, int64_t n, int64_t row_bytes,
+                     void* dst, int64_t ld_dst_bytes, void* stream);
+int kore_scatter_rows(const void* src, int64_t ld_src_bytes, const int32_t* idx, int64_t n,
+                      void* dst, int64_t dst_rows, int64_t row_bytes, int64_t ld_dst_bytes,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

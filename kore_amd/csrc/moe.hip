@@ -136,9 +136,13 @@ struct MoeGemmParams {
   int max_mblocks, ntiles;
   int abm;                // rows per aligned block of the sorted slot list
   int ksplit;             // K splits (down decode): split k writes Yw + k*S*D
+  uint16_t* out;          // plain grouped GEMM: bf16 output rows, scattered by token
+  int64_t ldo;
 };
 
-enum { MOE_GATEUP = 0, MOE_DOWN = 1 };
+// GATEUP / DOWN: the two projections of the fused MoE.  PLAIN: a top-1 grouped GEMM
+// out[t] = x[t] @ w[e]^T (gathered rows in, bf16 rows scattered back by token).
+enum { MOE_GATEUP = 0, MOE_DOWN = 1, MOE_PLAIN = 2 };
 
 template <int MODE, int MI, int NI, int WROWS, int WCOLS>
 __device__ __forceinline__ void moe_epilogue(f32x16_t (&acc)[MI][NI], uint16_t* lds, const MoeGemmParams& p, int pos0,
@@ -202,6 +206,21 @@ __device__ __forceinline__ void moe_epilogue(f32x16_t (&acc)[MI][NI], uint16_t* 
     St::drain(stg_lo, lane, [&](int row, int col, u32x4_t v) {
       *(u32x4_t*)(p.h_lo + (int64_t)(rw0 + row) * p.Nout + cw0 + col) = v;
     });
+  } else if constexpr (MODE == MOE_PLAIN) {
+    // rows of this lane -> token (top-1: slot == token); bf16 8-byte stores of 4 columns
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int s = p.sorted[pos0 + wm * WROWS + out_row(i, lane)];
+      if (s >= p.S) continue;
+      uint16_t* dst = p.out + (int64_t)s * p.ldo + n0 + wn * WCOLS;
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *(u32x2_t*)(dst + out_col(j, g, lane)) =
+              u32x2_t{Op::pack2(acc[i][j][4 * g], acc[i][j][4 * g + 1]),
+                      Op::pack2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3])};
+    }
   } else {
     // rows of this lane: pos0 + wm*WROWS + i*32 + lane%32 -> slot; fp32 16-byte stores
 #pragma unroll
@@ -246,7 +265,7 @@ __global__ void __launch_bounds__(kEngineThreads)
   for (int j = 0; j < E::LA; ++j) {
     const int r = E::a_row_of(tid, j);
     int64_t row;
-    if constexpr (MODE == MOE_GATEUP) {
+    if constexpr (MODE != MOE_DOWN) {
       const int s = p.sorted[pos0 + r];
       row = (s < p.S) ? s / p.topk : 0;  // padding rows read token 0; never stored
     } else {
@@ -306,8 +325,8 @@ __global__ void __launch_bounds__(256)
   const int pos0 = mb * BM;
 
   E eng;
-  int n0;
-  if constexpr (MODE == MOE_GATEUP) {
+  // A: gathered token rows (gate_up, plain) or the H planes of this block (down)
+  if constexpr (MODE != MOE_DOWN) {
     eng.ra = make_rsrc(p.x, (uint32_t)((int64_t)p.T * p.ldx * 2));
 #pragma unroll
     for (int j = 0; j < E::AJ; ++j) {
@@ -316,6 +335,19 @@ __global__ void __launch_bounds__(256)
       const int64_t row = (sl < p.S) ? sl / p.topk : 0;  // padding rows read token 0; never stored
       eng.a_voff[j] = (uint32_t)((row * p.ldx + 8 * E::chunk(r, lane)) * 2);
     }
+  } else {
+    const int64_t tile_bytes = (int64_t)BM * p.ldx * 2;
+    eng.ra = make_rsrc(p.x + (int64_t)pos0 * p.ldx, (uint32_t)tile_bytes);
+    eng.ra2 = make_rsrc(p.h_lo + (int64_t)pos0 * p.ldx, (uint32_t)tile_bytes);
+#pragma unroll
+    for (int j = 0; j < E::AJ; ++j) {
+      const int r = E::a_row(wave, lane, j);
+      eng.a_voff[j] = (uint32_t)(((int64_t)r * p.ldx + 8 * E::chunk(r, lane)) * 2);
+    }
+  }
+  // B: interleaved gate/up rows of w1[e] (gate_up) or consecutive rows of w[e]
+  int n0;
+  if constexpr (MODE == MOE_GATEUP) {
     n0 = nt * (BN / 2);
     const int I = p.Nout;
     const uint16_t* W = p.w + (int64_t)e * p.w_estride;
@@ -329,14 +361,6 @@ __global__ void __launch_bounds__(256)
       eng.b_voff[j] = (uint32_t)(((int64_t)(half * I + col) * p.w_rstride + 8 * E::chunk(r, lane)) * 2);
     }
   } else {
-    const int64_t tile_bytes = (int64_t)BM * p.ldx * 2;
-    eng.ra = make_rsrc(p.x + (int64_t)pos0 * p.ldx, (uint32_t)tile_bytes);
-    eng.ra2 = make_rsrc(p.h_lo + (int64_t)pos0 * p.ldx, (uint32_t)tile_bytes);
-#pragma unroll
-    for (int j = 0; j < E::AJ; ++j) {
-      const int r = E::a_row(wave, lane, j);
-      eng.a_voff[j] = (uint32_t)(((int64_t)r * p.ldx + 8 * E::chunk(r, lane)) * 2);
-    }
     n0 = nt * BN;
     const uint16_t* W = p.w + (int64_t)e * p.w_estride + (int64_t)n0 * p.w_rstride;
     eng.rb = make_rsrc(W, (uint32_t)((int64_t)BN * p.w_rstride * 2));
@@ -377,13 +401,22 @@ __global__ void __launch_bounds__(256)
   const int pos0 = mb * E::BM;
 
   E eng;
-  int n0;
   const int ar = E::a_row(wave, lane);
-  if constexpr (MODE == MOE_GATEUP) {
+  // A: gathered token rows (gate_up, plain) or the H planes of this block (down)
+  if constexpr (MODE != MOE_DOWN) {
     eng.ra = make_rsrc(p.x, (uint32_t)((int64_t)p.T * p.ldx * 2));
     const int sl = p.sorted[pos0 + ar];
     const int64_t row = (sl < p.S) ? sl / p.topk : 0;  // padding rows read token 0; never stored
     eng.a_voff = (uint32_t)((row * p.ldx + 8 * E::chunk(ar, lane)) * 2);
+  } else {
+    const uint32_t tile_bytes = (uint32_t)((int64_t)E::BM * p.ldx * 2);
+    eng.ra = make_rsrc(p.x + (int64_t)pos0 * p.ldx, tile_bytes);
+    eng.ra2 = make_rsrc(p.h_lo + (int64_t)pos0 * p.ldx, tile_bytes);
+    eng.a_voff = (uint32_t)(((int64_t)ar * p.ldx + 8 * E::chunk(ar, lane)) * 2);
+  }
+  // B: interleaved gate/up rows of w1[e] (gate_up) or consecutive rows of w[e]
+  int n0;
+  if constexpr (MODE == MOE_GATEUP) {
     n0 = nt * (BN / 2);
     const int I = p.Nout;
     const uint16_t* W = p.w + (int64_t)e * p.w_estride;
@@ -398,10 +431,6 @@ __global__ void __launch_bounds__(256)
       eng.b_voff[j] = (uint32_t)(((int64_t)(half * I + col) * p.w_rstride + 8 * E::chunk(r, lane)) * 2);
     }
   } else {
-    const uint32_t tile_bytes = (uint32_t)((int64_t)E::BM * p.ldx * 2);
-    eng.ra = make_rsrc(p.x + (int64_t)pos0 * p.ldx, tile_bytes);
-    eng.ra2 = make_rsrc(p.h_lo + (int64_t)pos0 * p.ldx, tile_bytes);
-    eng.a_voff = (uint32_t)(((int64_t)ar * p.ldx + 8 * E::chunk(ar, lane)) * 2);
     n0 = nt * BN;
     const uint16_t* W = p.w + (int64_t)e * p.w_estride + (int64_t)n0 * p.w_rstride;
     eng.rb = make_rsrc(W, (uint32_t)((int64_t)BN * p.w_rstride * 2));
@@ -648,4 +677,155 @@ extern "C" int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, c
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, ws.yw, topk_ids,
                      (uint16_t*)out, (int)T, (int)D, (int)topk, (int)E, p.ksplit);
   return check_launch("moe_combine_kernel");
+}
+
+// ==============================================================================
+// Top-1 grouped (segmented) expert GEMM and the token permute (row gather).
+// ==============================================================================
+namespace kore {
+namespace {
+
+struct GroupedWorkspace {
+  int32_t* offsets;
+  int32_t* sorted;
+  int32_t* block_expert;
+  size_t bytes;
+};
+
+inline GroupedWorkspace carve_grouped(void* base, int64_t M, int64_t E) {
+  const int BM = moe_block_rows(M, E);
+  const int64_t cap = align_capacity(M, E, BM);
+  GroupedWorkspace w{};
+  size_t off = 0;
+  auto take = [&](size_t n) {
+    const size_t o = off;
+    off = (size_t)align_up((int64_t)(off + n), 256);
+    return o;
+  };
+  const size_t o_off = take(sizeof(int32_t) * (E + 1));
+  const size_t o_sorted = take(sizeof(int32_t) * cap);
+  const size_t o_blk = take(sizeof(int32_t) * (cap / BM));
+  char* b = (char*)base;
+  w.offsets = (int32_t*)(b + o_off);
+  w.sorted = (int32_t*)(b + o_sorted);
+  w.block_expert = (int32_t*)(b + o_blk);
+  w.bytes = off;
+  return w;
+}
+
+// Gather dst[i] = src[idx[i]] (an index outside [0, rows) writes a zero row) or, with
+// SCATTER, dst[idx[i]] = src[i] (an index outside [0, rows) is skipped); 16-byte
+// copies when every row start is 16-byte aligned.
+template <bool SCATTER>
+__global__ void __launch_bounds__(256)
+    gather_rows_kernel(const uint8_t* __restrict__ src, int64_t ld_src, const int32_t* __restrict__ idx,
+                       int64_t row_bytes, uint8_t* __restrict__ dst, int64_t ld_dst, int rows, int vec16) {
+  const int i = (int)blockIdx.x;
+  const int r = idx[i];
+  const bool ok = r >= 0 && r < rows;
+  if (SCATTER && !ok) return;
+  const uint8_t* s = src + (SCATTER ? (int64_t)i : (int64_t)(ok ? r : 0)) * ld_src;
+  uint8_t* d = dst + (SCATTER ? (int64_t)r : (int64_t)i) * ld_dst;
+  if (vec16) {
+    for (int64_t c = threadIdx.x; c < row_bytes / 16; c += 256)
+      *(u32x4_t*)(d + 16 * c) = ok ? __builtin_nontemporal_load((const u32x4_t*)(s + 16 * c)) : u32x4_t{0u, 0u, 0u, 0u};
+  } else {
+    for (int64_t c = threadIdx.x; c < row_bytes; c += 256) d[c] = ok ? s[c] : (uint8_t)0;
+  }
+}
+
+}  // namespace
+}  // namespace kore
+
+extern "C" size_t kore_moe_grouped_gemm_workspace_bytes(int64_t M, int64_t E) {
+  if (M <= 0 || E <= 0) return 0;
+  return kore::carve_grouped(nullptr, M, E).bytes;
+}
+
+extern "C" int kore_moe_grouped_gemm(const void* x, int64_t ldx, const void* w, const int32_t* expert_ids, void* out,
+                                     int64_t ldo, int64_t M, int64_t N, int64_t K, int64_t E, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  using namespace kore;
+  if (!x || !w || !expert_ids || !out || !workspace) return set_error(KORE_EINVAL, "moe_grouped_gemm: null pointer");
+  if (M <= 0 || N <= 0 || K <= 0 || E <= 0) return set_error(KORE_EINVAL, "moe_grouped_gemm: sizes must be >= 1");
+  if (E > kAlignMaxE) return set_error(KORE_EUNSUPPORTED, "moe_grouped_gemm: E > %d", kAlignMaxE);
+  if (N % 128 != 0 || K % 8 != 0)
+    return set_error(KORE_EUNSUPPORTED, "moe_grouped_gemm: needs N %% 128 == 0 and K %% 8 == 0 (N=%lld K=%lld)",
+                     (long long)N, (long long)K);
+  if (ldx < K || ldx % 8 != 0 || ldo < N || ldo % 8 != 0 || ((uintptr_t)x & 15u) || ((uintptr_t)w & 15u) ||
+      ((uintptr_t)out & 15u))
+    return set_error(KORE_EINVAL, "moe_grouped_gemm: rows must be 16-byte aligned (ldx, ldo %% 8 == 0)");
+  if (M >= (1ll << 30) || N * K >= (1ll << 40)) return set_error(KORE_EUNSUPPORTED, "moe_grouped_gemm: too large");
+  const GroupedWorkspace ws = carve_grouped(workspace, M, E);
+  if (workspace_bytes < ws.bytes)
+    return set_error(KORE_EWORKSPACE, "moe_grouped_gemm: workspace %zu bytes < required %zu", workspace_bytes, ws.bytes);
+  hipStream_t st = (hipStream_t)stream;
+  const int BM = moe_block_rows(M, E);
+  const int64_t cap = align_capacity(M, E, BM);
+  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, st, expert_ids, (int)M, (int)E, BM,
+                     ws.offsets, ws.sorted, ws.block_expert, (int)cap);
+  int rc = check_launch("moe_align_kernel");
+  if (rc) return rc;
+  MoeGemmParams p{};
+  p.x = (const uint16_t*)x;
+  p.ldx = ldx;
+  p.w = (const uint16_t*)w;
+  p.offsets = ws.offsets;
+  p.sorted = ws.sorted;
+  p.block_expert = ws.block_expert;
+  p.E = (int)E;
+  p.S = (int)M;
+  p.T = (int)M;
+  p.topk = 1;
+  p.K = (int)K;
+  p.Nout = (int)N;
+  p.w_estride = N * K;
+  p.w_rstride = K;
+  p.abm = BM;
+  p.ksplit = 1;
+  p.out = (uint16_t*)out;
+  p.ldo = ldo;
+  const bool buf_ok = K % 64 == 0 && M * ldx * 2 < (1ll << 32) && N * K * 2 < (1ll << 32);
+  if (BM == 32) {
+    rc = buf_ok ? launch_moe_decode<MOE_PLAIN, 128, 7>(p, cap, st) : launch_moe_gemm<MOE_PLAIN, 32, 128, 1, 4>(p, cap, st);
+  } else if (buf_ok) {
+    rc = N % 256 == 0 ? launch_moe_buf<MOE_PLAIN, 256, 256>(p, cap, st) : launch_moe_buf<MOE_PLAIN, 256, 128>(p, cap, st);
+  } else {
+    rc = N % 256 == 0 ? launch_moe_gemm<MOE_PLAIN, 256, 256, 2, 2>(p, cap, st)
+                      : launch_moe_gemm<MOE_PLAIN, 256, 128, 2, 2>(p, cap, st);
+  }
+  return rc;
+}
+
+namespace kore {
+namespace {
+int launch_rows(bool scatter, const void* src, int64_t ld_src_bytes, const int32_t* idx, int64_t n, int64_t rows,
+                int64_t row_bytes, void* dst, int64_t ld_dst_bytes, void* stream) {
+  const char* what = scatter ? "scatter_rows" : "gather_rows";
+  if (n == 0 || row_bytes == 0) return KORE_OK;
+  if (!src || !idx || !dst) return set_error(KORE_EINVAL, "%s: null pointer", what);
+  if (n < 0 || row_bytes < 0 || rows <= 0 || ld_src_bytes < row_bytes || ld_dst_bytes < row_bytes)
+    return set_error(KORE_EINVAL, "%s: bad sizes", what);
+  if (n >= (1ll << 31) || rows >= (1ll << 31)) return set_error(KORE_EUNSUPPORTED, "%s: too many rows", what);
+  const int vec = row_bytes % 16 == 0 && ld_src_bytes % 16 == 0 && ld_dst_bytes % 16 == 0 &&
+                  ((uintptr_t)src & 15u) == 0 && ((uintptr_t)dst & 15u) == 0;
+  if (scatter)
+    hipLaunchKernelGGL(gather_rows_kernel<true>, dim3((unsigned)n), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t*)src, ld_src_bytes, idx, row_bytes, (uint8_t*)dst, ld_dst_bytes, (int)rows, vec);
+  else
+    hipLaunchKernelGGL(gather_rows_kernel<false>, dim3((unsigned)n), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t*)src, ld_src_bytes, idx, row_bytes, (uint8_t*)dst, ld_dst_bytes, (int)rows, vec);
+  return check_launch(what);
+}
+}  // namespace
+}  // namespace kore
+
+extern "C" int kore_gather_rows(const void* src, int64_t ld_src_bytes, int64_t src_rows, const int32_t* idx, int64_t n,
+                                int64_t row_bytes, void* dst, int64_t ld_dst_bytes, void* stream) {
+  return kore::launch_rows(false, src, ld_src_bytes, idx, n, src_rows, row_bytes, dst, ld_dst_bytes, stream);
+}
+
+extern "C" int kore_scatter_rows(const void* src, int64_t ld_src_bytes, const int32_t* idx, int64_t n, void* dst,
+                                 int64_t dst_rows, int64_t row_bytes, int64_t ld_dst_bytes, void* stream) {
+  return kore::launch_rows(true, src, ld_src_bytes, idx, n, dst_rows, row_bytes, dst, ld_dst_bytes, stream);
 }

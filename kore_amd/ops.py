@@ -20,6 +20,10 @@ Entry points and the reference callables they replace:
                            int8_a8w8}/seed_triton.py``; ``kore/tasks/vendor_ops.py:697-760``
 ``fused_moe(...)``         ``kore/tasks/fused_moe_silu_bf16/seed_triton.py:69-86``
 ``moe_align(ids, E, blk)`` sort/align stage (``kore/tasks/breadth/moe_ext.py:617-621``)
+``grouped_gemm``           ``kore/tasks/moe_grouped_gemm_bf16/seed_triton.py``; breadth ``moe_grouped_gemm``
+``moe_permute``            ``kore/tasks/moe_permute_bf16/seed_triton.py``; breadth ``moe_permute`` /
+``moe_unpermute``          ``moe_unpermute`` (``kore/tasks/breadth/moe_ext.py:546-571``)
+``moe_align_block_offsets`` breadth ``moe_align_block_offsets`` / ``moe_expert_offsets``
 =========================  =======================================================
 """
 
@@ -301,6 +305,97 @@ def fused_moe(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
                             _stream(x))
     _lib.check(rc)
     return out
+
+
+def grouped_gemm(hidden: torch.Tensor, w: torch.Tensor, expert_ids: torch.Tensor) -> torch.Tensor:
+    """Top-1 grouped expert GEMM -> bf16 [M,N]: ``out[m] = hidden[m] @ w[expert_ids[m]]^T``.
+
+    hidden[M,K] bf16, w[E,N,K] bf16, expert_ids[M] int; output rows in token order.
+    Rows whose id is outside [0, E) are zero.  The kernels need N % 128 == 0 and
+    K % 8 == 0; other shapes are zero-padded here first (a copy of ``w``).
+    """
+    _require_cuda(hidden, w, expert_ids)
+    if hidden.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise NotImplementedError(f"grouped_gemm runs bf16 operands (got {hidden.dtype}, {w.dtype})")
+    if hidden.dim() != 2 or w.dim() != 3 or w.shape[2] != hidden.shape[1]:
+        raise ValueError(f"expected hidden[M,K], w[E,N,K] (got {tuple(hidden.shape)}, {tuple(w.shape)})")
+    M, K = hidden.shape
+    E, N, _ = w.shape
+    if expert_ids.numel() != M:
+        raise ValueError(f"expert_ids must hold {M} ids (got {tuple(expert_ids.shape)})")
+    ids = expert_ids.reshape(M).to(torch.int32).contiguous()
+    if M == 0 or N == 0:
+        return torch.zeros((M, N), dtype=torch.bfloat16, device=hidden.device)
+    Kp, Np = -(-K // 8) * 8, -(-N // 128) * 128
+    if Kp != K or Np != N:
+        xp = torch.zeros((M, Kp), dtype=torch.bfloat16, device=hidden.device)
+        xp[:, :K] = hidden
+        wp = torch.zeros((E, Np, Kp), dtype=torch.bfloat16, device=w.device)
+        wp[:, :N, :K] = w
+        return grouped_gemm(xp, wp, ids)[:, :N].contiguous()
+    x = hidden if hidden.stride(1) == 1 and hidden.stride(0) % 8 == 0 else hidden.contiguous()
+    wc = w.contiguous()
+    out = torch.zeros((M, N), dtype=torch.bfloat16, device=x.device)
+    lib = _lib.load()
+    nbytes = lib.kore_moe_grouped_gemm_workspace_bytes(M, E)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    rc = lib.kore_moe_grouped_gemm(x.data_ptr(), x.stride(0), wc.data_ptr(), ids.data_ptr(), out.data_ptr(),
+                                   out.stride(0), M, N, K, E, ws.data_ptr(), nbytes, _stream(x))
+    _lib.check(rc)
+    return out
+
+
+def _rows(op: str, src: torch.Tensor, idx: torch.Tensor, dst: torch.Tensor, rows: int) -> None:
+    lib = _lib.load()
+    eb = src.element_size()
+    n = idx.numel()
+    if op == "gather":
+        rc = lib.kore_gather_rows(src.data_ptr(), src.stride(0) * eb, rows, idx.data_ptr(), n,
+                                  src.shape[1] * eb, dst.data_ptr(), dst.stride(0) * eb, _stream(src))
+    else:
+        rc = lib.kore_scatter_rows(src.data_ptr(), src.stride(0) * eb, idx.data_ptr(), n, dst.data_ptr(), rows,
+                                   src.shape[1] * eb, dst.stride(0) * eb, _stream(src))
+    _lib.check(rc)
+
+
+def moe_permute(hidden: torch.Tensor, sort_idx: torch.Tensor) -> torch.Tensor:
+    """Expert-sorted token dispatch: ``out[i] = hidden[sort_idx[i]]`` (any dtype)."""
+    _require_cuda(hidden, sort_idx)
+    if hidden.dim() != 2 or sort_idx.dim() != 1:
+        raise ValueError("expected hidden[M,D] and sort_idx[n]")
+    x = hidden if hidden.stride(1) == 1 else hidden.contiguous()
+    idx = sort_idx.to(torch.int32).contiguous()
+    out = torch.empty((idx.numel(), x.shape[1]), dtype=x.dtype, device=x.device)
+    if idx.numel() and x.shape[1]:
+        _rows("gather", x, idx, out, x.shape[0])
+    return out
+
+
+def moe_unpermute(permuted: torch.Tensor, sort_idx: torch.Tensor) -> torch.Tensor:
+    """Inverse of ``moe_permute``: ``out[sort_idx[i]] = permuted[i]`` (rows not named by
+    ``sort_idx`` are zero; ``sort_idx`` is a permutation in the reference tasks)."""
+    _require_cuda(permuted, sort_idx)
+    if permuted.dim() != 2 or sort_idx.dim() != 1 or sort_idx.numel() != permuted.shape[0]:
+        raise ValueError("expected permuted[M,D] and sort_idx[M]")
+    x = permuted if permuted.stride(1) == 1 else permuted.contiguous()
+    idx = sort_idx.to(torch.int32).contiguous()
+    out = torch.zeros_like(x)
+    if idx.numel() and x.shape[1]:
+        _rows("scatter", x, idx, out, x.shape[0])
+    return out
+
+
+def moe_align_block_offsets(expert_ids: torch.Tensor, num_experts: int, block: int) -> torch.Tensor:
+    """``offsets[E+1]`` int32: exclusive cumsum of each expert's token count rounded up to
+    a multiple of ``block`` (``kore/tasks/breadth/moe_ext.py:610-621``)."""
+    ids = expert_ids.reshape(-1, 1).to(torch.int32)
+    return moe_align(ids, int(num_experts), int(block))[0]
+
+
+def moe_expert_offsets(expert_ids: torch.Tensor, num_experts: int) -> torch.Tensor:
+    """``offsets[E+1]`` int32: exclusive cumsum of the per-expert token counts
+    (``kore/tasks/breadth/moe_ext.py:600-608``); the block-1 case of the align offsets."""
+    return moe_align_block_offsets(expert_ids, num_experts, 1)
 
 
 # Alias for drop-in shims: the reference's static scanner rejects any ``<x>.fused_moe(``

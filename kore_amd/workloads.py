@@ -150,6 +150,21 @@ def moe_inputs(T: int, E: int, topk: int, D: int, I: int, seed: int = 0, device=
 # Benchmark workloads: one entry per BASELINE configuration (inputs drawn on the
 # device so they are resident in HBM before timing starts).
 # --------------------------------------------------------------------------- #
+def grouped_inputs(M: int, E: int, N: int, K: int, seed: int = 0, device="cpu",
+                   router_bias: torch.Tensor | None = None):
+    """(hidden[M,K] bf16, w[E,N,K] bf16, expert_ids[M] int32) of the top-1 grouped GEMM
+    task: hidden, w ~ N(0,1)/sqrt(K); ids = argmax of softmax(N(0,1) logits + bias)."""
+    g = _gen(device, seed)
+    sc = 1.0 / K ** 0.5
+    hidden = (torch.randn((M, K), generator=g, device=device) * sc).to(torch.bfloat16)
+    w = (torch.randn((E, N, K), generator=g, device=device) * sc).to(torch.bfloat16)
+    logits = torch.randn((M, E), generator=g, device=device)
+    if router_bias is not None:
+        logits = logits + router_bias.to(device)
+    _, ti = route(logits, 1, renorm=False)
+    return hidden, w, ti[:, 0].contiguous()
+
+
 def bench_workloads():
     """Ordered ``name -> builder(device)``; a builder returns ``(fn, op, dims, dtype)``
     where ``fn()`` runs one step of the operator and ``(op, dims, dtype)`` key the

@@ -134,3 +134,47 @@ def moe_align_ref(topk_ids, E: int, block: int):
         block_expert[offsets[e] // block: offsets[e + 1] // block] = e
     return (offsets.astype(np.int32), sorted_slots.astype(np.int32),
             block_expert.astype(np.int32))
+
+
+def grouped_gemm_ref(hidden, w, expert_ids) -> torch.Tensor:
+    """Top-1 grouped expert GEMM oracle -> hidden.dtype [M, N] in token order.
+
+    ``out[m] = hidden[m] @ w[expert_ids[m]]^T`` in fp32, one cast; experts with no
+    token are never visited and ids outside ``[0, E)`` leave a zero row.  Follows
+    ``kore/tasks/_moe_common.py:203-226`` (``grouped_gemm_fp32``).  Pinned in
+    ``tests/test_oracle_moe.py`` by per-token matvecs (an independent gather path) and
+    the dense one-hot form.
+    """
+    M, K = hidden.shape
+    E, N, _ = w.shape
+    x, wf = hidden.float(), w.float()
+    out = torch.zeros((M, N), dtype=torch.float32)
+    eids = expert_ids.reshape(-1).long()
+    for e in range(E):
+        idx = (eids == e).nonzero(as_tuple=True)[0]
+        if idx.numel():
+            out[idx] = x[idx] @ wf[e].t()
+    return out.to(hidden.dtype)
+
+
+def permute_ref(hidden, sort_idx) -> torch.Tensor:
+    """``out[i] = hidden[sort_idx[i]]`` (``kore/tasks/moe_permute_bf16/reference.py:56-59``)."""
+    return hidden[sort_idx.long()]
+
+
+def unpermute_ref(permuted, sort_idx) -> torch.Tensor:
+    """``out[sort_idx[i]] = permuted[i]`` (``kore/tasks/breadth/moe_ext.py:567-570``)."""
+    out = torch.zeros_like(permuted)
+    out[sort_idx.long()] = permuted
+    return out
+
+
+def expert_offsets_ref(expert_ids, E: int, block: int = 1) -> torch.Tensor:
+    """``offsets[E+1]`` int32: exclusive cumsum of per-expert counts rounded up to a
+    multiple of ``block`` (``kore/tasks/breadth/moe_ext.py:597-621``, ``offsets`` /
+    ``align_offsets``)."""
+    counts = torch.bincount(expert_ids.reshape(-1).long(), minlength=E)[:E]
+    padded = (counts + block - 1) // block * block
+    off = torch.zeros(E + 1, dtype=torch.int64)
+    off[1:] = torch.cumsum(padded, 0)
+    return off.to(torch.int32)

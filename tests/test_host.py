@@ -193,6 +193,15 @@ EXPECTED_ENTRIES = {
     "gemm_fp8_a8w8": ("gemm_fp8", 4), "gemm_fp8_a8w8_pertoken": ("gemm", 4),
     "gemm_fp8_a8w8_pertensor": ("gemm", 4), "gemm_int8_a8w8": ("gemm", 4),
     "genv_gemm_a8w8_fp8": ("gemm_a8w8", 4), "genv_gemm_a8w8_int8": ("gemm_a8w8", 4),
+    # MoE dispatch stages exposed as tasks (moe_grouped_gemm_bf16/reference.py:25,
+    # moe_permute_bf16/reference.py:25; breadth entries are the op names, moe_ext.py:853)
+    "moe_grouped_gemm_bf16": ("grouped_gemm", 3), "genb_moe_grouped_gemm_bf16": ("moe_grouped_gemm", 3),
+    "moe_permute_bf16": ("moe_permute", 2), "genb_moe_permute_bf16": ("moe_permute", 2),
+    "genb_moe_permute_fp16": ("moe_permute", 2), "genb_moe_unpermute_bf16": ("moe_unpermute", 2),
+    "genb_moe_unpermute_fp16": ("moe_unpermute", 2),
+    "genb_moe_align_block_offsets_bf16": ("moe_align_block_offsets", 3),
+    "genb_moe_align_block_offsets_fp16": ("moe_align_block_offsets", 3),
+    "genb_moe_expert_offsets_bf16": ("moe_expert_offsets", 2), "genb_moe_expert_offsets_fp16": ("moe_expert_offsets", 2),
 }
 
 

@@ -157,3 +157,47 @@ def test_moe_align_ref(T, topk, E, block):
     assert len(np.unique(real)) == len(real)
     counts = np.bincount(ids[(ids >= 0) & (ids < E)], minlength=E)
     assert np.array_equal(off[1:], np.cumsum((counts + block - 1) // block * block))  # moe_ext align_offsets
+
+
+# ---------------------------------------------------------------------------
+# top-1 grouped GEMM, permute / unpermute, expert offsets
+# ---------------------------------------------------------------------------
+from oracle.moe import expert_offsets_ref, grouped_gemm_ref, moe_align_ref, permute_ref, unpermute_ref  # noqa: E402
+
+
+def test_grouped_gemm_oracle_two_paths():
+    """Per-token matvec (gather) path and the dense one-hot path both equal the oracle;
+    a dead expert and an out-of-range id are handled."""
+    g = torch.Generator().manual_seed(4)
+    M, E, N, K = 40, 5, 24, 32
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = torch.randn(E, N, K, generator=g).to(torch.bfloat16)
+    ids = torch.randint(0, E - 1, (M,), generator=g, dtype=torch.int32)  # expert E-1 dead
+    ids[3] = E + 2  # matches no expert: zero row
+    out = grouped_gemm_ref(x, w, ids)
+    per_tok = torch.stack([x[m].double() @ w[ids[m]].double().t() if 0 <= ids[m] < E else torch.zeros(N).double()
+                           for m in range(M)])
+    assert torch.allclose(out.float(), per_tok.float(), atol=1e-2, rtol=1e-2)
+    onehot = torch.zeros(M, E, dtype=torch.float64)
+    valid = (ids >= 0) & (ids < E)
+    onehot[valid.nonzero()[:, 0], ids[valid].long()] = 1.0
+    dense = torch.einsum("me,enk,mk->mn", onehot, w.double(), x.double())
+    assert torch.allclose(out.float(), dense.float(), atol=1e-2, rtol=1e-2)
+    assert torch.all(out[3] == 0)
+
+
+def test_permute_unpermute_roundtrip_and_offsets():
+    g = torch.Generator().manual_seed(5)
+    M, E = 50, 6
+    ids = torch.randint(0, E, (M,), generator=g, dtype=torch.int32)
+    sort_idx = torch.argsort(ids, stable=True).to(torch.int32)
+    h = torch.randn(M, 8, generator=g).to(torch.bfloat16)
+    p = permute_ref(h, sort_idx)
+    assert torch.all(ids[sort_idx.long()][1:] >= ids[sort_idx.long()][:-1])  # expert-sorted
+    assert torch.equal(unpermute_ref(p, sort_idx), h)
+    # offsets (block 1) are the bincount prefix sum; align offsets match the align oracle
+    off = expert_offsets_ref(ids, E)
+    assert off[0] == 0 and off[-1] == M and torch.equal(off[1:] - off[:-1], torch.bincount(ids.long(), minlength=E).int())
+    for block in (1, 4, 64):
+        a_off, _, _ = moe_align_ref(ids.reshape(M, 1).numpy(), E, block)
+        assert np.array_equal(expert_offsets_ref(ids, E, block).numpy(), a_off)
