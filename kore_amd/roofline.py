@@ -5,6 +5,12 @@ GEMM ``F = 2MNK``, ``Q = (MK + KN + MN)*e``; fp8 / int8 GEMM ``Q = (MK + KN)*1 +
 batched/grouped GEMM multiply both by B; fused MoE ``F = M*topk*6*D*I``,
 ``Q = (E*3*D*I + 2*M*D)*e``.  ``T_min = max(F/peak_flops, Q/peak_bw)``.
 
+Two operators are priced here by what they must move, not by the scorer's formula:
+the top-1 expert GEMM ``moe_grouped_gemm`` (the scorer's B=1 grouped form counts one
+``K x N`` weight, but every expert that receives a token has its weight read once:
+``Q = (M*K + E_used*N*K + M*N)*e``) and the row permute ``moe_permute``
+(``F = 0``, ``Q = 2*M*D*e + 4*M``: rows in, rows out, one int32 index per row).
+
 Peaks are MI355X's published dense figures (no sparsity): bf16/fp16 2.5 PFLOP/s,
 fp8 5.0 PFLOP/s, int8 5.0 POP/s, HBM3E 8.0 TB/s.  ``KORE_PEAK_BF16`` / ``KORE_PEAK_FP8`` /
 ``KORE_PEAK_HBM_BW`` override them as in the reference (``rooflines.py:84-97``).
@@ -51,6 +57,13 @@ def flops_bytes(operation: str, dims: dict[str, int], dtype: str) -> tuple[float
     op = operation.lower()
     e = dtype_bytes(dtype)
     fp8 = "fp8" in dtype.lower() or "int8" in dtype.lower()  # 8-bit operands, bf16 output
+    if op == "moe_grouped_gemm":
+        M, N, K = dims["M"], dims["N"], dims["K"]
+        Eu = dims.get("E_used", dims["E"])
+        return 2.0 * M * N * K, float((M * K + Eu * N * K + M * N) * e)
+    if op in ("moe_permute", "moe_unpermute"):
+        M, D = dims["M"], dims["D"]
+        return 0.0, float(2 * M * D * e + 4 * M)
     if "batched_gemm" in op or "grouped_gemm" in op or op == "bmm":
         B = dims.get("B", dims.get("batch", 1))
         M, N, K = dims["M"], dims["N"], dims["K"]

@@ -150,6 +150,24 @@ def moe_inputs(T: int, E: int, topk: int, D: int, I: int, seed: int = 0, device=
 # Benchmark workloads: one entry per BASELINE configuration (inputs drawn on the
 # device so they are resident in HBM before timing starts).
 # --------------------------------------------------------------------------- #
+# Per-expert token-count trace of the reference's MoE tasks (``kore/tasks/
+# _moe_common.py:93-113``): unbalanced, the last expert dead; tiled past 32 experts.
+ROUTER_TRACE = (16053, 105, 1843, 2724, 327, 88, 4102, 51, 9210, 61, 3020, 44, 1502, 990, 233, 77,
+                6740, 120, 410, 58, 2210, 39, 812, 175, 5030, 66, 1360, 92, 3550, 47, 1180, 0)
+
+
+def jagged_bias(E: int) -> torch.Tensor:
+    """Router bias ``log(count)`` over ``ROUTER_TRACE`` (``-inf`` on the dead last
+    expert), added to N(0,1) logits to make the reference's unbalanced routing."""
+    live = [c for c in ROUTER_TRACE if c > 0]
+    counts = list(ROUTER_TRACE[:E]) if E <= len(ROUTER_TRACE) else [live[i % len(live)] for i in range(E)]
+    counts[-1] = 0
+    c = torch.tensor(counts, dtype=torch.float32)
+    bias = torch.log(c + 1e-6)
+    bias[c == 0] = float("-inf")
+    return bias
+
+
 def grouped_inputs(M: int, E: int, N: int, K: int, seed: int = 0, device="cpu",
                    router_bias: torch.Tensor | None = None):
     """(hidden[M,K] bf16, w[E,N,K] bf16, expert_ids[M] int32) of the top-1 grouped GEMM
@@ -218,10 +236,31 @@ def bench_workloads():
                 {"M": M, "N": N, "K": K}, kind
         return build
 
-    # SURVEY 8(f) row 1: a8w8 with per-token / per-channel scales (task primaries + decode)
+    # a8w8 with per-token / per-channel scales (task primaries + decode)
     w["fp8_a8w8_pertoken_4096"] = a8w8(4096, 4096, 4096, "fp8")
     w["int8_a8w8_4096"] = a8w8(4096, 4096, 4096, "int8")
     w["fp8_a8w8_pertoken_16x4096x4096"] = a8w8(16, 4096, 4096, "fp8")
     w["moe_decode_T64"] = moe(64)
     w["moe_prefill_T4096"] = moe(4096)
+
+    def grouped(M, E, N, K):
+        def build(dev):
+            hidden, wt, ids = grouped_inputs(M, E, N, K, seed=0, device=dev, router_bias=jagged_bias(E))
+            used = int(torch.unique(ids).numel())
+            return (lambda: kore_amd.grouped_gemm(hidden, wt, ids)), "moe_grouped_gemm", \
+                {"M": M, "E": E, "N": N, "K": K, "E_used": used}, "bf16"
+        return build
+
+    def permute(M, E, D):
+        def build(dev):
+            g = _gen(dev, 0)
+            hidden = torch.randn((M, D), generator=g, device=dev).to(torch.bfloat16)
+            _, _, ids = grouped_inputs(M, E, 128, 8, seed=1, device=dev, router_bias=jagged_bias(E))
+            sidx = torch.argsort(ids, stable=True).to(torch.int32)
+            return (lambda: kore_amd.moe_permute(hidden, sidx)), "moe_permute", {"M": M, "D": D}, "bf16"
+        return build
+
+    # expert-dispatch stages: top-1 grouped GEMM and the token permute (task primaries)
+    w["moe_grouped_gemm_4096x32x2048x4096"] = grouped(4096, 32, 2048, 4096)
+    w["moe_permute_8192x7168"] = permute(8192, 256, 7168)
     return w

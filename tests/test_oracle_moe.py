@@ -126,6 +126,14 @@ def test_trace32_router_never_picks_dead_expert():
     assert counts[0] > counts[1] * 5      # jagged: expert 0 (16053) dominates expert 1 (105)
 
 
+def test_workload_router_bias_matches_oracle_trace():
+    """The bench workloads' router bias (host side) equals the oracle's trace bias."""
+    from kore_amd import workloads as W
+
+    for E in (1, 4, 8, 31, 32, 33, 64, 256):
+        assert torch.equal(W.jagged_bias(E), trace32_bias(E)), E
+
+
 def _align_bruteforce(ids, E, block):
     T, topk = ids.shape
     S = T * topk
