@@ -178,6 +178,24 @@ int kore_moe_grouped_gemm(const void* x, int64_t ldx, const void* w, const int32
                           void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Top-1 grouped fp8 (OCP e4m3) a8w8 expert GEMM, bf16 out in token order:
+ *   out[m, :] = xs[m] * ws[e, :] * (xq[m, :] . wq[e, :, :]^T),  e = expert_ids[m]
+ *   xq [M,K] fp8 (row stride ldx bytes), wq [E,N,K] fp8 contiguous, xs per token
+ *   (xs[m * xs_stride]), ws [E,N] fp32 contiguous (per expert, per output channel),
+ *   fp32 accumulation, one bf16 rounding; rows with ids outside [0,E) are unwritten.
+ *   Same workspace as kore_moe_grouped_gemm.  Requires N % 128 == 0, K % 128 == 0 and
+ *   16-byte aligned rows (KORE_EUNSUPPORTED / KORE_EINVAL otherwise).
+ * Replaces: grouped_gemm_fp8(xq, wq, x_scale, w_scale, expert_ids)
+ *           kore/tasks/moe_grouped_gemm_fp8/seed_triton.py (ENTRY reference.py:29;
+ *           oracle _moe_common.py:228-249); moe_grouped_gemm_fp8(xq, wq, xs, ws, expert_ids)
+ *           kore/tasks/breadth/moe_ext.py:638-652 (genb_moe_grouped_gemm_fp8_fp8).
+ */
+int kore_moe_grouped_gemm_fp8(const void* xq, int64_t ldx, const void* wq, const float* xs,
+                              int64_t xs_stride, const float* ws, const int32_t* expert_ids,
+                              void* out, int64_t ldo, int64_t M, int64_t N, int64_t K, int64_t E,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Token permute / unpermute as row copies of any element type:
  *   gather:  dst[i, :] = src[idx[i], :] for i < n (idx outside [0, src_rows): zero row)
  *   scatter: dst[idx[i], :] = src[i, :] for i < n (idx outside [0, dst_rows): skipped)

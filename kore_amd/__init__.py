@@ -17,6 +17,7 @@ from .ops import (  # noqa: F401
     gemm_a8w8_blockscale,
     gemm_fused,
     grouped_gemm,
+    grouped_gemm_fp8,
     moe_align,
     moe_align_block_offsets,
     moe_expert_offsets,
@@ -30,5 +31,5 @@ for _name in _ops.GEMM_FUSION_OPS:
     globals()[_name] = getattr(_ops, _name)
 
 __all__ = ["gemm", "gemm_fused", "batched_gemm", "gemm_a8w8_blockscale", "gemm_a8w8", "fused_moe", "moe_gated_silu", "moe_align",
-           "grouped_gemm", "moe_permute", "moe_unpermute", "moe_align_block_offsets", "moe_expert_offsets",
+           "grouped_gemm", "grouped_gemm_fp8", "moe_permute", "moe_unpermute", "moe_align_block_offsets", "moe_expert_offsets",
            *_ops.GEMM_FUSION_OPS]

@@ -32,6 +32,8 @@ SIGNATURES = {
     "kore_moe_align_capacity": (_i64, [_i64, _i64, _i64, _i64]),
     "kore_moe_grouped_gemm_workspace_bytes": (_sz, [_i64, _i64]),
     "kore_moe_grouped_gemm": (_i32, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _sz, _vp]),
+    "kore_moe_grouped_gemm_fp8": (_i32, [_vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                         _vp, _sz, _vp]),
     "kore_gather_rows": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp]),
     "kore_scatter_rows": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "kore_moe_align": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),

@@ -32,6 +32,11 @@ struct Fp8Params {
   int64_t xs_m, xs_k, ws_n, ws_k;
   int tiles_m, tiles_n;
   int vec_store;
+  // grouped (top-1 expert) mode: tile m-block b holds the rows sorted[b*BM ..] of
+  // expert block_expert[b] (-1: unused block); a sorted entry >= M is a padding row
+  const int32_t* sorted;
+  const int32_t* block_expert;
+  int64_t w_estride, ws_estride;
 };
 
 constexpr int kFp8GroupM = 4;
@@ -261,12 +266,16 @@ __device__ __forceinline__ i32x8_t lds_frag32(const uint8_t* row, const int (&of
 
 // FULL_M: every row of the M tile exists, so the A loads of a wave share one per-lane
 // offset and differ by a scalar row offset; otherwise rows are clamped per load.
-template <typename C, bool FULL_M>
+// GROUPED (row-scale modes): the tile's A rows are gathered through p.sorted (padding
+// rows read row 0 and are never stored), B and the weight scales are those of the
+// block's expert, and output rows are scattered back to token order.
+template <typename C, bool FULL_M, bool GROUPED = false>
 __global__ void __launch_bounds__(C::NW * 64)
     gemm_fp8_pipe_kernel(const Fp8Params p) {
   constexpr int NW = C::NW, MI = C::MI, NI = C::NI, NT = C::NT, TB = C::TB;
   constexpr int AQ = C::AQ, BQ = C::BQ, LPS = C::LPS, PER = C::PER, NSLOT = C::NSLOT;
   constexpr bool XS4 = C::XS4, ROW = C::ROW, I8 = C::MODE == Q_ROW_I8;
+  static_assert(!GROUPED || (ROW && !FULL_M), "grouped tiles use row scales and gathered rows");
   using AccT = std::conditional_t<I8, i32x16_t, f32x16_t>;
 
   __shared__ __attribute__((aligned(1024))) uint8_t lds[C::LDS];
@@ -275,20 +284,44 @@ __global__ void __launch_bounds__(C::NW * 64)
   const int wm = wave / C::WGN, wn = wave % C::WGN;
   const int lr = lane & 31, hh = lane >> 5;
 
-  const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-  const int width = kFp8GroupM * p.tiles_n;
-  const int grp = bid / width;
-  const int first_m = grp * kFp8GroupM;
-  const int gsz = min(p.tiles_m - first_m, kFp8GroupM);
-  const int tl = bid - grp * width;
-  const int m0 = (first_m + tl % gsz) * C::BM;
-  const int n0 = (tl / gsz) * C::BN;
-  const int rows_a = min(p.M - m0, C::BM);
+  int m0, n0;
+  if constexpr (GROUPED) {
+    // m-block major: the live blocks are a prefix of the grid, which the round-robin
+    // dispatch spreads evenly over the XCDs (a remap would pack them onto a few)
+    m0 = ((int)blockIdx.x / p.tiles_n) * C::BM;
+    n0 = ((int)blockIdx.x % p.tiles_n) * C::BN;
+  } else {
+    const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int width = kFp8GroupM * p.tiles_n;
+    const int grp = bid / width;
+    const int first_m = grp * kFp8GroupM;
+    const int gsz = min(p.tiles_m - first_m, kFp8GroupM);
+    const int tl = bid - grp * width;
+    m0 = (first_m + tl % gsz) * C::BM;
+    n0 = (tl / gsz) * C::BN;
+  }
+  const int rows_a = GROUPED ? C::BM : min(p.M - m0, C::BM);
   const int nk = p.K / 128;
+  int expert = 0;
+  if constexpr (GROUPED) {
+    expert = p.block_expert[m0 / C::BM];  // uniform: an unused block leaves before any barrier
+    if (expert < 0) return;
+  }
+  // token row of tile row r (grouped: padding rows read token 0)
+  auto grow = [&](int r) -> int {
+    if constexpr (GROUPED) {
+      const int t = p.sorted[m0 + r];
+      return t < p.M ? t : 0;
+    } else {
+      return min(r, rows_a - 1);
+    }
+  };
 
   // ---- buffer resources (tile-based) and per-lane load offsets ----
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.xq + (int64_t)m0 * p.ldx, (uint32_t)(rows_a * p.ldx));
-  const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.wq + (int64_t)n0 * p.ldw, (uint32_t)(C::BN * p.ldw));
+  const __amdgpu_buffer_rsrc_t ra = GROUPED ? make_rsrc(p.xq, (uint32_t)((int64_t)p.M * p.ldx))
+                                            : make_rsrc(p.xq + (int64_t)m0 * p.ldx, (uint32_t)(rows_a * p.ldx));
+  const __amdgpu_buffer_rsrc_t rb =
+      make_rsrc(p.wq + (int64_t)expert * p.w_estride + (int64_t)n0 * p.ldw, (uint32_t)(C::BN * p.ldw));
   const __amdgpu_buffer_rsrc_t rx =
       make_rsrc(p.xs + (int64_t)m0 * p.xs_m, (uint32_t)(((rows_a - 1) * p.xs_m + (nk - 1) * p.xs_k + 1) * 4));
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(
@@ -303,8 +336,7 @@ __global__ void __launch_bounds__(C::NW * 64)
     a_voff[0] = (uint32_t)((lrow + 8 * wave) * p.ldx + 16 * dchunk);
   } else {
 #pragma unroll
-    for (int q = 0; q < AQ; ++q)
-      a_voff[q] = (uint32_t)(min(lrow + 8 * (wave + NW * q), rows_a - 1) * p.ldx + 16 * dchunk);
+    for (int q = 0; q < AQ; ++q) a_voff[q] = (uint32_t)(grow(lrow + 8 * (wave + NW * q)) * p.ldx + 16 * dchunk);
   }
   const uint32_t b_voff = (uint32_t)((lrow + 8 * wave) * p.ldw + 16 * dchunk);
   const uint32_t x_voff = (uint32_t)(min(64 * (wave & 3) + lane, rows_a - 1) * p.xs_m * 4);
@@ -493,8 +525,11 @@ __global__ void __launch_bounds__(C::NW * 64)
   uint16_t* stg = (uint16_t*)lds + wave * (C::WROWS * 64);
   float xrow[MI];
 #pragma unroll
-  for (int i = 0; i < MI; ++i)
-    xrow[i] = ROW ? p.xs[(int64_t)min(m0 + rowA0 + 32 * i + lr, p.M - 1) * p.xs_m] : 1.0f;
+  for (int i = 0; i < MI; ++i) {
+    if constexpr (GROUPED) xrow[i] = p.xs[(int64_t)grow(rowA0 + 32 * i + lr) * p.xs_m];
+    else xrow[i] = ROW ? p.xs[(int64_t)min(m0 + rowA0 + 32 * i + lr, p.M - 1) * p.xs_m] : 1.0f;
+  }
+  const float* wsx = p.ws + (int64_t)expert * p.ws_estride;
 #pragma unroll
   for (int j = 0; j < NI; ++j)
 #pragma unroll
@@ -503,7 +538,7 @@ __global__ void __launch_bounds__(C::NW * 64)
       if constexpr (ROW) {
         const int64_t n = n0 + rowB0 + out_col(j, g, lane);  // n + 3 < N: N % BN == 0
 #pragma unroll
-        for (int e = 0; e < 4; ++e) wcol[e] = p.ws[(n + e) * p.ws_n];
+        for (int e = 0; e < 4; ++e) wcol[e] = wsx[(n + e) * p.ws_n];
       }
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
@@ -520,7 +555,8 @@ __global__ void __launch_bounds__(C::NW * 64)
   const int mw0 = m0 + rowA0, nw0 = n0 + rowB0;
   const bool vec = p.vec_store != 0;
   St::drain(stg, lane, [&](int row, int col, u32x4_t v) {
-    const int gm = mw0 + row, gn = nw0 + col;
+    const int gn = nw0 + col;
+    const int gm = GROUPED ? p.sorted[mw0 + row] : mw0 + row;
     if (gm < p.M) store_row8(p.y + (int64_t)gm * p.ldy + gn, gn, p.N, vec, v);
   });
 }
@@ -785,7 +821,7 @@ extern "C" int kore_gemm_a8w8_blockscale(const void* xq, int64_t ldx, const void
   if (M >= (1ll << 31) || N >= (1ll << 31) || K >= (1ll << 31))
     return set_error(KORE_EUNSUPPORTED, "gemm_a8w8_blockscale: dimension >= 2^31");
   constexpr int BM = 256, BN = 128;
-  Fp8Params p;
+  Fp8Params p{};
   p.xq = (const uint8_t*)xq;
   p.wq = (const uint8_t*)wq;
   p.xs = xs;
@@ -955,7 +991,43 @@ int launch_a8w8(const Fp8Params& p0, bool skinny, hipStream_t st) {
   return launch_fp8_pipe<F8Cfg<128, 128, 4, 4, false, MODE>>(p, st);
 }
 
+template <typename C>
+int launch_fp8_grouped(Fp8Params p, int mblocks, hipStream_t st) {
+  p.tiles_m = mblocks;
+  p.tiles_n = p.N / C::BN;
+  const dim3 grid((unsigned)((int64_t)p.tiles_m * p.tiles_n)), block(C::NW * 64);
+  hipLaunchKernelGGL((gemm_fp8_pipe_kernel<C, false, true>), grid, block, 0, st, p);
+  return check_launch("gemm_fp8_pipe_kernel(grouped)");
+}
+
 }  // namespace
+
+int launch_grouped_a8w8(const GroupedA8Args& a, hipStream_t st) {
+  Fp8Params p{};
+  p.xq = (const uint8_t*)a.xq;
+  p.wq = (const uint8_t*)a.wq;
+  p.xs = a.xs;
+  p.ws = a.ws;
+  p.y = (uint16_t*)a.y;
+  p.M = (int)a.M;
+  p.N = (int)a.N;
+  p.K = (int)a.K;
+  p.ldx = a.ldx;
+  p.ldw = a.K;
+  p.ldy = a.ldy;
+  p.xs_m = a.xs_stride;
+  p.ws_n = 1;
+  p.vec_store = a.ldy % 8 == 0 && ((uintptr_t)a.y & 15u) == 0;
+  p.sorted = a.sorted;
+  p.block_expert = a.block_expert;
+  p.w_estride = a.N * a.K;
+  p.ws_estride = a.N;
+  const int mb = (int)(a.capacity / a.block_rows);
+  if (a.block_rows == 256) return launch_fp8_grouped<F8Cfg<256, 256, 8, 2, false, Q_ROW_FP8>>(p, mb, st);
+  if (a.block_rows == 128) return launch_fp8_grouped<F8Cfg<128, 128, 4, 4, false, Q_ROW_FP8>>(p, mb, st);
+  return set_error(KORE_EINVAL, "grouped a8w8: block rows %d (128 or 256)", a.block_rows);
+}
+
 }  // namespace kore
 
 extern "C" int kore_gemm_a8w8(int qtype, const void* xq, int64_t ldx_m, int64_t ldx_k, const void* wq, int64_t ldw_n,
@@ -973,7 +1045,7 @@ extern "C" int kore_gemm_a8w8(int qtype, const void* xq, int64_t ldx_m, int64_t 
                     ldw_n % 16 == 0 && aligned16(xq) && aligned16(wq) && 256 * ldx_m + K < (1ll << 31) &&
                     256 * ldw_n + K < (1ll << 31) && ldx_m >= K && ldw_n >= K;
   if (fast) {
-    Fp8Params p;
+    Fp8Params p{};
     p.xq = (const uint8_t*)xq;
     p.wq = (const uint8_t*)wq;
     p.xs = xs;

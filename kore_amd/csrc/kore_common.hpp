@@ -148,4 +148,24 @@ __device__ __forceinline__ void lds_fence_barrier() { __syncthreads(); }
 namespace kore {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+
+// Top-1 grouped fp8 a8w8 GEMM over an expert-sorted token order (tiles of
+// gemm_fp8_blockscale.hip, called by the grouped entry in moe.hip): xq[M,K] (row
+// stride ldx), wq[E,N,K] and ws[E,N] contiguous, xs[m * xs_stride]; sorted/block_expert
+// come from the align kernel with block `block_rows` (128 or 256) and `capacity` slots.
+struct GroupedA8Args {
+  const void* xq;
+  int64_t ldx;
+  const void* wq;
+  const float* xs;
+  int64_t xs_stride;
+  const float* ws;
+  const int32_t* sorted;
+  const int32_t* block_expert;
+  void* y;
+  int64_t ldy;
+  int64_t M, N, K, capacity;
+  int block_rows;
+};
+int launch_grouped_a8w8(const GroupedA8Args& a, hipStream_t st);
 }  // namespace kore

@@ -25,6 +25,8 @@
 #include "kore_common.hpp"
 #include "tile_engine.hpp"
 
+#include <algorithm>
+
 namespace kore {
 namespace {
 
@@ -34,47 +36,111 @@ namespace {
 constexpr int kAlignThreads = 1024;
 constexpr int kAlignMaxE = 1024;
 
+// One workgroup, three barrier-separated phases, no loop over all experts in one
+// thread.  Wave w owns the contiguous slot range of 64-slot groups
+// [w*G, (w+1)*G), so slot order is wave order, then group order, then lane order.
+//  A. each wave counts its slots per expert (one ballot per distinct expert of a
+//     group, counts added to the wave's own LDS row: no barrier inside the phase);
+//  B. thread per expert: histogram = sum of the wave counts, padded offsets by a
+//     wave-shuffle scan, then each wave's start inside the expert;
+//  C. each wave replays its groups and places slot s at its expert's running start
+//     plus its rank in the group.
+// Padding sentinels and block owners are written in B; ids are read in batches of
+// 8 groups so one memory latency covers 8 groups.
+constexpr int kAlignBatch = 8;
+
 __global__ void __launch_bounds__(kAlignThreads)
     moe_align_kernel(const int32_t* __restrict__ ids, int S, int E, int block, int32_t* __restrict__ offsets,
                      int32_t* __restrict__ sorted, int32_t* __restrict__ block_expert, int cap) {
-  __shared__ int cnt[kAlignMaxE];
-  __shared__ int base[kAlignMaxE];
-  __shared__ int wcnt[kAlignThreads / 64][64];
+  constexpr int NW = kAlignThreads / 64;
+  __shared__ int cnt[kAlignMaxE];       // tokens per expert
+  __shared__ int base[kAlignMaxE];      // padded start of each expert
+  __shared__ int wrun[NW][kAlignMaxE];  // A: per-wave counts; C: per-wave next slot
+  __shared__ int wsum[NW];
   __shared__ int s_total;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  constexpr int NW = kAlignThreads / 64;
-  for (int e = tid; e < E; e += kAlignThreads) cnt[e] = 0;
+  const int ngroups = (S + 63) / 64;
+  const int gpw = (ngroups + NW - 1) / NW;
+  const int g0 = wave * gpw, g1 = min(g0 + gpw, ngroups);
+  for (int e = lane; e < E; e += 64) wrun[wave][e] = 0;  // the wave's own row
+
+  // visit this wave's groups in slot order; for each group, f(s, e, valid) runs the
+  // per-distinct-expert ballot loop (wave-uniform trip count, scalar lane reads)
+  auto for_groups = [&](auto&& f) {
+    for (int gb = g0; gb < g1; gb += kAlignBatch) {
+      int ev[kAlignBatch];
+#pragma unroll
+      for (int u = 0; u < kAlignBatch; ++u) {
+        const int s = (gb + u) * 64 + lane;
+        ev[u] = (gb + u < g1 && s < S) ? ids[s] : -1;
+      }
+#pragma unroll
+      for (int u = 0; u < kAlignBatch; ++u) f((gb + u) * 64 + lane, ev[u], ev[u] >= 0 && ev[u] < E);
+    }
+  };
+  // A: per-wave counts (one LDS add per distinct expert of a group)
+  for_groups([&](int, int e, bool valid) {
+    unsigned long long todo = __ballot(valid);
+    while (todo) {
+      const int leader = __builtin_ctzll(todo);
+      const int le = __builtin_amdgcn_readlane(e, leader);
+      const unsigned long long m = __ballot(valid && e == le);
+      if (lane == leader) atomicAdd(&wrun[wave][le], __popcll(m));
+      todo &= ~m;
+    }
+  });
   __syncthreads();
-  // pass 1: histogram (integer LDS atomics: order-independent result)
-  for (int s = tid; s < S; s += kAlignThreads) {
-    const int e = ids[s];
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  // B: histogram, padded offsets (thread t = expert t; E <= kAlignThreads), wave starts
+  int mine = 0;
+  if (tid < E) {
+    int c = 0;
+    for (int w = 0; w < NW; ++w) c += wrun[w][tid];
+    cnt[tid] = c;
+    mine = (c + block - 1) / block * block;
   }
+  int incl = mine;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(incl, d);
+    if (lane >= d) incl += y;
+  }
+  if (lane == 63) wsum[wave] = incl;
   __syncthreads();
   if (tid == 0) {
-    int run = 0;
-    for (int e = 0; e < E; ++e) {
-      offsets[e] = run;
-      base[e] = run;
-      run += (cnt[e] + block - 1) / block * block;
+    int r = 0;
+    for (int w = 0; w < NW; ++w) {
+      const int v = wsum[w];
+      wsum[w] = r;
+      r += v;
     }
-    offsets[E] = run;
-    s_total = run;
+    s_total = r;
+    offsets[E] = r;
   }
   __syncthreads();
   const int total = s_total;
-  // padding sentinels and block owners
-  for (int e = 0; e < E; ++e) {
-    const int beg = base[e] + cnt[e];
-    const int end = (e + 1 < E) ? base[e + 1] : total;
-    for (int i = beg + tid; i < end; i += kAlignThreads) sorted[i] = S;
+  if (tid < E) {
+    const int excl = wsum[wave] + incl - mine;
+    base[tid] = excl;
+    offsets[tid] = excl;
+    int r = excl;
+    for (int w = 0; w < NW; ++w) {
+      const int v = wrun[w][tid];
+      wrun[w][tid] = r;
+      r += v;
+    }
   }
+  __syncthreads();
+  // padding sentinels (wave w fills the padding of experts w, w + NW, ...), the tail
+  // past the last expert, and block owners (the last expert whose start is <= the
+  // block's first slot; empty experts share the start of the next one)
+  for (int e = wave; e < E; e += NW)
+    for (int i = base[e] + cnt[e] + lane; i < base[e] + (cnt[e] + block - 1) / block * block; i += 64) sorted[i] = S;
   for (int i = total + tid; i < cap; i += kAlignThreads) sorted[i] = S;
   const int nblk = cap / block;
   for (int b = tid; b < nblk; b += kAlignThreads) {
     int owner = -1;
     if (b * block < total) {
-      int lo = 0, hi = E - 1;  // last expert whose offset <= b*block
+      int lo = 0, hi = E - 1;
       while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
         if (base[mid] <= b * block) lo = mid; else hi = mid - 1;
@@ -83,35 +149,24 @@ __global__ void __launch_bounds__(kAlignThreads)
     }
     block_expert[b] = owner;
   }
-  // pass 2: stable placement, chunk by chunk; rank = earlier same-expert slots.
-  const unsigned long long lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int c0 = 0; c0 < S; c0 += kAlignThreads) {
-    const int s = c0 + tid;
-    const int e = (s < S) ? ids[s] : -1;
-    const bool valid = e >= 0 && e < E;
+  // C: stable placement.  Each lane reads its expert's running start for the wave
+  // (one LDS read per group), the ballot loop ranks the lanes of each distinct expert
+  // and its leader (lowest lane) advances the running start by the group's count.
+  for_groups([&](int s, int e, bool valid) {
+    const int first = valid ? wrun[wave][e] : 0;
+    unsigned long long todo = __ballot(valid);
     int rank = 0;
-    for (int e0 = 0; e0 < E; e0 += 64) {
-      for (int e2 = e0; e2 < min(E, e0 + 64); ++e2) {
-        const unsigned long long m = __ballot(valid && e == e2);
-        if (lane == 0) wcnt[wave][e2 - e0] = __popcll(m);
-        if (valid && e == e2) rank = __popcll(m & lt_mask);
-      }
-      __syncthreads();
-      // exclusive scan over waves for experts e0 .. e0+63 (thread per expert)
-      if (tid < 64 && e0 + tid < E) {
-        int run = base[e0 + tid];
-        for (int w = 0; w < NW; ++w) {
-          const int v = wcnt[w][tid];
-          wcnt[w][tid] = run;
-          run += v;
-        }
-        base[e0 + tid] = run;
-      }
-      __syncthreads();
-      if (valid && e >= e0 && e < e0 + 64) sorted[wcnt[wave][e - e0] + rank] = s;
-      __syncthreads();
+    while (todo) {
+      const int leader = __builtin_ctzll(todo);
+      const int le = __builtin_amdgcn_readlane(e, leader);
+      const unsigned long long m = __ballot(valid && e == le);
+      if (valid && e == le)
+        rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+      if (lane == leader) atomicAdd(&wrun[wave][le], __popcll(m));
+      todo &= ~m;
     }
-  }
+    if (valid) sorted[first + rank] = s;
+  });
 }
 
 // ------------------------------------------------------------------------------
@@ -692,8 +747,7 @@ struct GroupedWorkspace {
   size_t bytes;
 };
 
-inline GroupedWorkspace carve_grouped(void* base, int64_t M, int64_t E) {
-  const int BM = moe_block_rows(M, E);
+inline GroupedWorkspace carve_grouped(void* base, int64_t M, int64_t E, int BM) {
   const int64_t cap = align_capacity(M, E, BM);
   GroupedWorkspace w{};
   size_t off = 0;
@@ -734,12 +788,19 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// Block rows of the fp8 grouped tiles: 256x256 when experts average >= 64 rows (one
+// round of large tiles beats ~3 rounds of 128x128 tiles despite the padding).
+inline int grouped_fp8_block_rows(int64_t M, int64_t E) { return M >= 64 * E ? 256 : 128; }
+
 }  // namespace
 }  // namespace kore
 
+// One size serves the bf16 and fp8 grouped entries (every block size they use).
 extern "C" size_t kore_moe_grouped_gemm_workspace_bytes(int64_t M, int64_t E) {
   if (M <= 0 || E <= 0) return 0;
-  return kore::carve_grouped(nullptr, M, E).bytes;
+  size_t b = 0;
+  for (int bm : {32, 128, 256}) b = std::max(b, kore::carve_grouped(nullptr, M, E, bm).bytes);
+  return b;
 }
 
 extern "C" int kore_moe_grouped_gemm(const void* x, int64_t ldx, const void* w, const int32_t* expert_ids, void* out,
@@ -756,11 +817,12 @@ extern "C" int kore_moe_grouped_gemm(const void* x, int64_t ldx, const void* w, 
       ((uintptr_t)out & 15u))
     return set_error(KORE_EINVAL, "moe_grouped_gemm: rows must be 16-byte aligned (ldx, ldo %% 8 == 0)");
   if (M >= (1ll << 30) || N * K >= (1ll << 40)) return set_error(KORE_EUNSUPPORTED, "moe_grouped_gemm: too large");
-  const GroupedWorkspace ws = carve_grouped(workspace, M, E);
-  if (workspace_bytes < ws.bytes)
-    return set_error(KORE_EWORKSPACE, "moe_grouped_gemm: workspace %zu bytes < required %zu", workspace_bytes, ws.bytes);
-  hipStream_t st = (hipStream_t)stream;
   const int BM = moe_block_rows(M, E);
+  const GroupedWorkspace ws = carve_grouped(workspace, M, E, BM);
+  if (workspace_bytes < kore_moe_grouped_gemm_workspace_bytes(M, E))
+    return set_error(KORE_EWORKSPACE, "moe_grouped_gemm: workspace %zu bytes < required %zu", workspace_bytes,
+                     kore_moe_grouped_gemm_workspace_bytes(M, E));
+  hipStream_t st = (hipStream_t)stream;
   const int64_t cap = align_capacity(M, E, BM);
   hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, st, expert_ids, (int)M, (int)E, BM,
                      ws.offsets, ws.sorted, ws.block_expert, (int)cap);
@@ -795,6 +857,52 @@ extern "C" int kore_moe_grouped_gemm(const void* x, int64_t ldx, const void* w, 
                       : launch_moe_gemm<MOE_PLAIN, 256, 128, 2, 2>(p, cap, st);
   }
   return rc;
+}
+
+extern "C" int kore_moe_grouped_gemm_fp8(const void* xq, int64_t ldx, const void* wq, const float* xs,
+                                         int64_t xs_stride, const float* ws, const int32_t* expert_ids, void* out,
+                                         int64_t ldo, int64_t M, int64_t N, int64_t K, int64_t E, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  using namespace kore;
+  if (!xq || !wq || !xs || !ws || !expert_ids || !out || !workspace)
+    return set_error(KORE_EINVAL, "moe_grouped_gemm_fp8: null pointer");
+  if (M <= 0 || N <= 0 || K <= 0 || E <= 0) return set_error(KORE_EINVAL, "moe_grouped_gemm_fp8: sizes must be >= 1");
+  if (E > kAlignMaxE) return set_error(KORE_EUNSUPPORTED, "moe_grouped_gemm_fp8: E > %d", kAlignMaxE);
+  if (N % 128 != 0 || K % 128 != 0)
+    return set_error(KORE_EUNSUPPORTED, "moe_grouped_gemm_fp8: needs N %% 128 == 0 and K %% 128 == 0 (N=%lld K=%lld)",
+                     (long long)N, (long long)K);
+  if (ldx < K || ldx % 16 != 0 || ldo < N || ((uintptr_t)xq & 15u) || ((uintptr_t)wq & 15u))
+    return set_error(KORE_EINVAL, "moe_grouped_gemm_fp8: rows must be 16-byte aligned (ldx %% 16 == 0)");
+  if (M * ldx >= (1ll << 32) || 256 * K >= (1ll << 31) || M >= (1ll << 30) || N >= (1ll << 30))
+    return set_error(KORE_EUNSUPPORTED, "moe_grouped_gemm_fp8: too large");
+  if (workspace_bytes < kore_moe_grouped_gemm_workspace_bytes(M, E))
+    return set_error(KORE_EWORKSPACE, "moe_grouped_gemm_fp8: workspace %zu bytes < required %zu", workspace_bytes,
+                     kore_moe_grouped_gemm_workspace_bytes(M, E));
+  const int BM = N % 256 == 0 ? grouped_fp8_block_rows(M, E) : 128;
+  const GroupedWorkspace w = carve_grouped(workspace, M, E, BM);
+  const int64_t cap = align_capacity(M, E, BM);
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, st, expert_ids, (int)M, (int)E, BM, w.offsets,
+                     w.sorted, w.block_expert, (int)cap);
+  int rc = check_launch("moe_align_kernel");
+  if (rc) return rc;
+  GroupedA8Args a{};
+  a.xq = xq;
+  a.ldx = ldx;
+  a.wq = wq;
+  a.xs = xs;
+  a.xs_stride = xs_stride;
+  a.ws = ws;
+  a.sorted = w.sorted;
+  a.block_expert = w.block_expert;
+  a.y = out;
+  a.ldy = ldo;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.capacity = cap;
+  a.block_rows = BM;
+  return launch_grouped_a8w8(a, st);
 }
 
 namespace kore {

@@ -345,6 +345,53 @@ def grouped_gemm(hidden: torch.Tensor, w: torch.Tensor, expert_ids: torch.Tensor
     return out
 
 
+def grouped_gemm_fp8(xq: torch.Tensor, wq: torch.Tensor, x_scale: torch.Tensor, w_scale: torch.Tensor,
+                     expert_ids: torch.Tensor) -> torch.Tensor:
+    """Top-1 grouped fp8 a8w8 expert GEMM -> bf16 [M,N] in token order:
+    ``out[m] = (xq[m]*x_scale[m]) @ (wq[e]*w_scale[e])^T``, ``e = expert_ids[m]``.
+
+    xq[M,K] / wq[E,N,K] float8_e4m3fn, x_scale[M,1] (or [M]) per token, w_scale[E,N,1]
+    (or [E,N]) per expert and output channel.  Rows whose id is outside [0, E) are
+    zero.  The kernels need N % 128 == 0 and K % 128 == 0; other shapes are zero-padded
+    here first (a copy of ``wq``).
+    """
+    _require_cuda(xq, wq, x_scale, w_scale, expert_ids)
+    if xq.dtype != torch.float8_e4m3fn or wq.dtype != torch.float8_e4m3fn:
+        raise NotImplementedError(f"grouped_gemm_fp8 runs float8_e4m3fn operands (got {xq.dtype}, {wq.dtype})")
+    if xq.dim() != 2 or wq.dim() != 3 or wq.shape[2] != xq.shape[1]:
+        raise ValueError(f"expected xq[M,K], wq[E,N,K] (got {tuple(xq.shape)}, {tuple(wq.shape)})")
+    M, K = xq.shape
+    E, N, _ = wq.shape
+    if expert_ids.numel() != M or x_scale.numel() != M or w_scale.numel() != E * N:
+        raise ValueError("expected expert_ids[M], x_scale[M,1] and w_scale[E,N,1]")
+    ids = expert_ids.reshape(M).to(torch.int32).contiguous()
+    xs = x_scale.reshape(M).to(torch.float32).contiguous()
+    ws = w_scale.reshape(E, N).to(torch.float32).contiguous()
+    if M == 0 or N == 0:
+        return torch.zeros((M, N), dtype=torch.bfloat16, device=xq.device)
+    Kp, Np = -(-K // 128) * 128, -(-N // 128) * 128
+    if Kp != K or Np != N:
+        xp = torch.zeros((M, Kp), dtype=torch.uint8, device=xq.device)
+        xp[:, :K] = xq.view(torch.uint8)
+        wp = torch.zeros((E, Np, Kp), dtype=torch.uint8, device=wq.device)
+        wp[:, :N, :K] = wq.view(torch.uint8)
+        wsp = torch.ones((E, Np), dtype=torch.float32, device=ws.device)
+        wsp[:, :N] = ws
+        return grouped_gemm_fp8(xp.view(torch.float8_e4m3fn), wp.view(torch.float8_e4m3fn), xs, wsp,
+                                ids)[:, :N].contiguous()
+    x = xq if xq.stride(1) == 1 and xq.stride(0) % 16 == 0 else xq.contiguous()
+    wc = wq.contiguous()
+    out = torch.zeros((M, N), dtype=torch.bfloat16, device=x.device)
+    lib = _lib.load()
+    nbytes = lib.kore_moe_grouped_gemm_workspace_bytes(M, E)
+    wsp_ = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    rc = lib.kore_moe_grouped_gemm_fp8(x.data_ptr(), x.stride(0), wc.data_ptr(), xs.data_ptr(), 1, ws.data_ptr(),
+                                       ids.data_ptr(), out.data_ptr(), out.stride(0), M, N, K, E, wsp_.data_ptr(),
+                                       nbytes, _stream(x))
+    _lib.check(rc)
+    return out
+
+
 def _rows(op: str, src: torch.Tensor, idx: torch.Tensor, dst: torch.Tensor, rows: int) -> None:
     lib = _lib.load()
     eb = src.element_size()

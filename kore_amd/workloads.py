@@ -183,6 +183,25 @@ def grouped_inputs(M: int, E: int, N: int, K: int, seed: int = 0, device="cpu",
     return hidden, w, ti[:, 0].contiguous()
 
 
+def grouped_fp8_inputs(M: int, E: int, N: int, K: int, seed: int = 0, device="cpu",
+                       router_bias: torch.Tensor | None = None):
+    """(xq[M,K], wq[E,N,K] e4m3, x_scale[M,1], w_scale[E,N,1] fp32, expert_ids[M] int32)
+    of the fp8 grouped GEMM task: x ~ N(0,1), w ~ N(0,1)/sqrt(K), each quantised per
+    last-dim row (``scale = max(amax, 1e-12)/448``)."""
+    g = _gen(device, seed)
+    xf = torch.randn((M, K), generator=g, device=device)
+    wq = torch.empty((E, N, K), dtype=torch.float8_e4m3fn, device=device)
+    ws = torch.empty((E, N, 1), dtype=torch.float32, device=device)
+    for e in range(E):  # per expert keeps the fp32 temporaries small
+        wq[e], ws[e] = _q8_rowwise(torch.randn((N, K), generator=g, device=device) / K ** 0.5, "fp8")
+    xq, xs = _q8_rowwise(xf, "fp8")
+    logits = torch.randn((M, E), generator=g, device=device)
+    if router_bias is not None:
+        logits = logits + router_bias.to(device)
+    _, ti = route(logits, 1, renorm=False)
+    return xq, wq, xs, ws, ti[:, 0].contiguous()
+
+
 def bench_workloads():
     """Ordered ``name -> builder(device)``; a builder returns ``(fn, op, dims, dtype)``
     where ``fn()`` runs one step of the operator and ``(op, dims, dtype)`` key the
@@ -263,4 +282,14 @@ def bench_workloads():
     # expert-dispatch stages: top-1 grouped GEMM and the token permute (task primaries)
     w["moe_grouped_gemm_4096x32x2048x4096"] = grouped(4096, 32, 2048, 4096)
     w["moe_permute_8192x7168"] = permute(8192, 256, 7168)
+
+    def grouped_fp8(M, E, N, K):
+        def build(dev):
+            xq, wq, xs, ws, ids = grouped_fp8_inputs(M, E, N, K, seed=0, device=dev, router_bias=jagged_bias(E))
+            used = int(torch.unique(ids).numel())
+            return (lambda: kore_amd.grouped_gemm_fp8(xq, wq, xs, ws, ids)), "moe_grouped_gemm", \
+                {"M": M, "E": E, "N": N, "K": K, "E_used": used}, "fp8"
+        return build
+
+    w["moe_grouped_gemm_fp8_4096x32x2048x4096"] = grouped_fp8(4096, 32, 2048, 4096)
     return w

@@ -157,6 +157,28 @@ def grouped_gemm_ref(hidden, w, expert_ids) -> torch.Tensor:
     return out.to(hidden.dtype)
 
 
+def grouped_gemm_fp8_ref(xq, wq, x_scale, w_scale, expert_ids) -> torch.Tensor:
+    """Top-1 grouped fp8 a8w8 expert GEMM oracle -> bf16 [M, N] in token order.
+
+    ``out[m] = (xq[m]*x_scale[m]) @ (wq[e]*w_scale[e])^T`` with ``e = expert_ids[m]``,
+    fp32 of the dequantised operands, one cast; ids outside ``[0, E)`` leave a zero row.
+    Follows ``kore/tasks/_moe_common.py:228-249`` (``grouped_gemm_fp8_fp32``).  Pinned in
+    ``tests/test_oracle_moe.py`` by per-token dequantised matvecs and, with every token
+    on one expert, the dense a8w8 oracle.
+    """
+    M, K = xq.shape
+    E, N, _ = wq.shape
+    xd = xq.float() * x_scale.float().reshape(M, 1)
+    wd = wq.float() * w_scale.float().reshape(E, N, 1)
+    out = torch.zeros((M, N), dtype=torch.float32)
+    eids = expert_ids.reshape(-1).long()
+    for e in range(E):
+        idx = (eids == e).nonzero(as_tuple=True)[0]
+        if idx.numel():
+            out[idx] = xd[idx] @ wd[e].t()
+    return out.to(torch.bfloat16)
+
+
 def permute_ref(hidden, sort_idx) -> torch.Tensor:
     """``out[i] = hidden[sort_idx[i]]`` (``kore/tasks/moe_permute_bf16/reference.py:56-59``)."""
     return hidden[sort_idx.long()]

@@ -8,7 +8,8 @@ import torch
 
 import kore_amd
 from kore_amd import workloads as W
-from oracle.moe import expert_offsets_ref, grouped_gemm_ref, permute_ref, trace32_bias, unpermute_ref
+from oracle.moe import (expert_offsets_ref, grouped_gemm_fp8_ref, grouped_gemm_ref, permute_ref, trace32_bias,
+                        unpermute_ref)
 from tests.fourprong import bit_equal, verdict
 
 pytestmark = pytest.mark.gpu
@@ -78,6 +79,64 @@ def test_grouped_gemm_all_one_expert(gpu):
     out = kore_amd.grouped_gemm(hidden.to(gpu), w.to(gpu), ti.to(gpu)).cpu()
     dense = (hidden.float() @ w[2].float().t()).to(torch.bfloat16)
     verdict(out, dense, "grouped", "bf16", "one expert")
+
+
+def _grouped_fp8(gpu, M, E, N, K, seed=0, ids=None):
+    xq, wq, xs, ws, ti = W.grouped_fp8_inputs(M, E, N, K, seed=seed, device=gpu, router_bias=trace32_bias(E))
+    if ids is not None:
+        ti = ids.to(gpu)
+    out = kore_amd.grouped_gemm_fp8(xq, wq, xs, ws, ti)
+    assert out.shape == (M, N) and out.dtype == torch.bfloat16
+    rows = torch.arange(M, device=gpu)
+    if 2.0 * M * N * K > ROW_SAMPLE_FLOPS:
+        rows = torch.unique(torch.cat([torch.arange(0, M, max(1, M // 96)), torch.tensor([M - 1])])).to(gpu)
+    t = ti[rows].long()
+    valid = (t >= 0) & (t < E)
+    used = torch.unique(t[valid])
+    remap = torch.full((E,), -1, dtype=torch.long, device=gpu)
+    remap[used] = torch.arange(used.numel(), device=gpu)
+    local = torch.where(valid, remap[t.clamp(0, E - 1)], torch.full_like(t, -1))
+    sel = used if used.numel() else torch.zeros(1, dtype=torch.long, device=gpu)
+    ref = grouped_gemm_fp8_ref(xq[rows].cpu(), wq[sel].cpu(), xs[rows].cpu(), ws[sel].cpu(),
+                               local.to(torch.int32).cpu())
+    return out[rows].cpu(), ref
+
+
+# moe_grouped_gemm_fp8/task.yaml:11-16 and the breadth fp8 grouped catalog
+# (moe_ext.py:219-224, K = 4095 padded on the host).
+@pytest.mark.parametrize("M,E,N,K", [(64, 8, 256, 256), (4096, 32, 2048, 4096), (8192, 64, 1024, 2048),
+                                     (1024, 256, 512, 2048), (512, 32, 1536, 4096), (16384, 128, 4096, 4096),
+                                     (4096, 256, 2048, 4096), (512, 64, 4096, 4095)])
+def test_grouped_gemm_fp8_task_shapes(gpu, M, E, N, K):
+    out, ref = _grouped_fp8(gpu, M, E, N, K)
+    verdict(out, ref, "grouped_fp8", "fp8", f"M{M} E{E} N{N} K{K}")
+
+
+@pytest.mark.parametrize("M,E,N,K", [(1, 4, 128, 128), (33, 3, 384, 256), (700, 5, 256, 512), (2000, 2, 640, 384),
+                                     (9000, 4, 512, 256), (1100, 16, 768, 512), (300, 6, 200, 100)])
+def test_grouped_gemm_fp8_ragged(gpu, M, E, N, K):
+    """128-row and (M >= 64 E, N % 256 == 0) 256-row tiles, N not a multiple of 256,
+    one-token experts, and odd N / K padded on the host."""
+    out, ref = _grouped_fp8(gpu, M, E, N, K, seed=M)
+    verdict(out, ref, "grouped_fp8", "fp8", f"M{M} E{E} N{N} K{K}")
+
+
+def test_grouped_gemm_fp8_invalid_ids_one_expert_determinism(gpu):
+    M, E, N, K = 600, 5, 512, 512
+    xq, wq, xs, ws, ti = W.grouped_fp8_inputs(M, E, N, K, seed=4, device=gpu)
+    bad = ti.clone()
+    bad[::9] = -1
+    bad[4::13] = E
+    out, ref = _grouped_fp8(gpu, M, E, N, K, seed=4, ids=bad)
+    assert (out[::9] == 0).all() and (out[4::13] == 0).all()
+    verdict(out, ref, "grouped_fp8", "fp8", "invalid ids")
+    a = kore_amd.grouped_gemm_fp8(xq, wq, xs, ws, ti)
+    assert bit_equal(a, kore_amd.grouped_gemm_fp8(xq, wq, xs, ws, ti))
+    # every token on expert 1 equals the dense a8w8 GEMM with that expert's weight
+    one = torch.full((M,), 1, dtype=torch.int32, device=gpu)
+    g1 = kore_amd.grouped_gemm_fp8(xq, wq, xs, ws, one)
+    d1 = kore_amd.gemm_a8w8(xq, wq[1], xs, ws[1].reshape(1, N))
+    assert bit_equal(g1, d1)
 
 
 def _sort_idx(M, E, seed):

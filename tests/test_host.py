@@ -196,6 +196,7 @@ EXPECTED_ENTRIES = {
     # MoE dispatch stages exposed as tasks (moe_grouped_gemm_bf16/reference.py:25,
     # moe_permute_bf16/reference.py:25; breadth entries are the op names, moe_ext.py:853)
     "moe_grouped_gemm_bf16": ("grouped_gemm", 3), "genb_moe_grouped_gemm_bf16": ("moe_grouped_gemm", 3),
+    "moe_grouped_gemm_fp8": ("grouped_gemm_fp8", 5), "genb_moe_grouped_gemm_fp8_fp8": ("moe_grouped_gemm_fp8", 5),
     "moe_permute_bf16": ("moe_permute", 2), "genb_moe_permute_bf16": ("moe_permute", 2),
     "genb_moe_permute_fp16": ("moe_permute", 2), "genb_moe_unpermute_bf16": ("moe_unpermute", 2),
     "genb_moe_unpermute_fp16": ("moe_unpermute", 2),

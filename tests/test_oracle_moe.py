@@ -17,6 +17,7 @@ import torch.nn.functional as F
 
 from kore_amd import workloads as W
 from oracle.moe import TRACE32, jagged_counts, moe_align_ref, moe_ref, route, trace32_bias
+from oracle.moe import grouped_gemm_fp8_ref
 
 
 def _inputs(T=12, E=4, topk=2, D=32, I=24, seed=0, bias=None):
@@ -192,6 +193,34 @@ def test_grouped_gemm_oracle_two_paths():
     dense = torch.einsum("me,enk,mk->mn", onehot, w.double(), x.double())
     assert torch.allclose(out.float(), dense.float(), atol=1e-2, rtol=1e-2)
     assert torch.all(out[3] == 0)
+
+
+def test_grouped_gemm_fp8_oracle_pinned():
+    """Per-token dequantised matvecs (exact in float64 for e4m3 products at this K) and,
+    with every token on one expert, the dense a8w8 oracle on that expert's weight; a
+    dropped scale or a wrong expert index fails one of them."""
+    from oracle.quant import matmul_a8w8_ref, quant_rowwise_fp8
+
+    g = torch.Generator().manual_seed(6)
+    M, E, N, K = 36, 4, 16, 64
+    xq, xs = quant_rowwise_fp8(torch.randn(M, K, generator=g))
+    wq = torch.empty(E, N, K, dtype=torch.float8_e4m3fn)
+    ws = torch.empty(E, N, 1)
+    for e in range(E):
+        wq[e], ws[e] = quant_rowwise_fp8(torch.randn(N, K, generator=g) * (e + 1))
+    ids = torch.randint(0, E, (M,), generator=g, dtype=torch.int32)
+    ids[5] = -1
+    out = grouped_gemm_fp8_ref(xq, wq, xs, ws, ids)
+    for m in range(M):
+        e = int(ids[m])
+        if e < 0:
+            assert torch.all(out[m] == 0)
+            continue
+        r = (xq[m].double() * xs[m].double()) @ (wq[e].double() * ws[e].double()).t()
+        assert torch.allclose(out[m].float(), r.float(), atol=1e-6, rtol=8e-3), m
+    one = torch.full((M,), 2, dtype=torch.int32)
+    dense = matmul_a8w8_ref(xq, wq[2], xs, ws[2].reshape(1, N))
+    assert torch.equal(grouped_gemm_fp8_ref(xq, wq, xs, ws, one), dense)
 
 
 def test_permute_unpermute_roundtrip_and_offsets():
