@@ -32,6 +32,7 @@ extern "C" {
 /* ---- element types ---- */
 #define KORE_DT_BF16 0
 #define KORE_DT_FP16 1
+#define KORE_DT_FP32 2  /* kore_gemm only: fp32 operands, bias and output (fp32 MFMA) */
 
 /* ---- fused epilogue activations (kore/tasks/_genops.py:294-304 act codes) ---- */
 #define KORE_ACT_NONE 0
@@ -53,7 +54,9 @@ int kore_abi_version(void);
 
 /*
  * Dense GEMM with fused epilogue:  C[M,N] = act(A[M,K] @ B[K,N] + bias[N]).
- * fp32 accumulation, one round-to-nearest-even cast to `dtype` (bf16 or fp16).
+ * fp32 accumulation, one round-to-nearest-even cast to `dtype` (bf16 or fp16); with
+ * KORE_DT_FP32 operands, bias and C are fp32 and the products run on the fp32 MFMA
+ * (v_mfma_f32_32x32x2_f32, no reduced-precision inputs), fast path K % 64 == 0.
  *   A element (m,k) at a[m*lda_m + k*lda_k]; B element (k,n) at b[k*ldb_k + n*ldb_n];
  *   C element (m,n) at c[m*ldc_m + n]; bias may be NULL (no bias), else [N] contiguous.
  * Any strides are accepted; the MFMA fast path needs unit stride along K for A and
@@ -62,7 +65,8 @@ int kore_abi_version(void);
  * be NULL).
  * Replaces: gemm(a, b)            kore/tasks/gemm_bf16/seed_triton.py:64-86
  *           <op>(a, b[, bias])    kore/tasks/_genops.py:715-731 (_GEMM_TMPL entry,
- *                                 gemm_fusion ops listed at _genops.py:274-290)
+ *                                 gemm_fusion ops listed at _genops.py:274-290;
+ *                                 dtypes bf16/fp16/fp32 at _genops.py:41-45)
  */
 int kore_gemm(int dtype, int act,
               const void* a, int64_t lda_m, int64_t lda_k,

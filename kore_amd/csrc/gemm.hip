@@ -401,6 +401,11 @@ int run_gemm(const GemmDesc& d, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   if (d.dtype == KORE_DT_BF16) return dispatch_typed<BF16>(d, s);
   if (d.dtype == KORE_DT_FP16) return dispatch_typed<F16>(d, s);
+  if (d.dtype == KORE_DT_FP32) {
+    if (d.batch != 1) return set_error(KORE_EUNSUPPORTED, "gemm: fp32 is not batched");
+    GemmF32Args f{d.a, d.b, d.bias, d.c, d.M, d.N, d.K, d.sam, d.sak, d.sbk, d.sbn, d.scm, d.act};
+    return launch_gemm_f32(f, s);
+  }
   return set_error(KORE_EINVAL, "gemm: unsupported dtype code %d", d.dtype);
 }
 

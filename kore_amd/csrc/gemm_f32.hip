@@ -1,0 +1,361 @@
+// fp32 GEMM with fused bias + activation on the fp32 matrix cores (gfx950).
+//
+// C[M,N] = act(A[M,K] @ B[K,N] + bias[N]), fp32 in, fp32 out, v_mfma_f32_32x32x2_f32
+// (full fp32 products, fp32 accumulation).  One such MFMA is 4096 FLOP and occupies the
+// matrix core for 64 cycles, so the kernel is MFMA-bound with a register-staged double
+// buffer and one barrier per K step, provided a K step's MFMAs outlast the global load
+// latency of the next step: K steps are 64 values (a 64x32 wave tile issues 64 MFMAs,
+// ~4000 cycles, per step; 32-value steps measured 20% slower at one tile per CU).
+//
+// 4 waves in a 2x2 grid, each (BM/2) x (BN/2) as 32x32 blocks; K step 64 floats.
+//  A tile in LDS: BM rows of 64 floats (256 bytes), 16-byte chunk c of row r stored at
+//    c ^ (r % 16), so a fragment read (16 rows per pass, one chunk each) is
+//    conflict-free.  Lane l reads chunk 2q + l/32 of its row: 4 K values that feed 4
+//    MFMAs (K slot l/32 of MFMA j holds k = 8q + 4(l/32) + j; B uses the same map).
+//  B, K-contiguous ([N,K] rows, the W.t() view): the same layout as A.
+//  B, N-contiguous ([K,N] rows): 64 rows of BN floats, row stride BN + 8 so the two
+//    half-waves (rows k and k+4) fall on different banks; a lane reads the 4 K values
+//    of its column with 4 ds_read_b32.
+// The B fragment is the first MFMA operand, so lane l owns output row l % 32 and four
+// N-consecutive columns per register group: 16-byte stores straight from registers.
+//
+// Any other layout, K % 64 != 0 or unaligned rows: a 64x64 FMA tile (generic).
+#include "../../include/kore_amd.h"
+#include "kore_common.hpp"
+
+#include <type_traits>
+
+namespace kore {
+namespace {
+
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+struct F32Params {
+  const float* a;
+  const float* b;
+  const float* bias;
+  float* c;
+  int M, N, K;
+  int64_t lda, ldb, ldc;  // ldb: between n rows (B_KC) or k rows (B_NC)
+  int tiles_m, tiles_n;
+  int act;
+  int vec_store;
+};
+
+constexpr int kF32BK = 64;          // K values per stage
+constexpr int kF32CH = kF32BK / 4;   // 16-byte chunks per staged row
+
+// 16-byte chunk position of chunk c in row r: XOR with r % 16, so the 16 rows a
+// 16-lane pass of ds_read_b128 touches land on 16 distinct chunk columns (64 banks).
+__device__ __forceinline__ int f32_pos(int r, int c) { return c ^ (r & (kF32CH - 1)); }
+
+// M16: 16x16x4 MFMAs (lane l: row l % 16, K slot l / 16) instead of 32x32x2 (row l % 32,
+// K slot l / 32); the N-contiguous B row stride then puts the four K-slot row groups
+// (rows 4 apart) on distinct banks with BN + 4.
+template <int BM, int BN, bool BNC, bool M16>
+struct F32Cfg {
+  static constexpr int WM = BM / 2, WN = BN / 2;
+  static constexpr int BS = M16 ? 16 : 32;  // MFMA block edge
+  static constexpr int MI = WM / BS, NI = WN / BS;
+  static_assert(MI >= 1 && NI >= 1, "wave tile");
+  static constexpr int A_FLOATS = BM * kF32BK;
+  static constexpr int B_STRIDE = BNC ? BN + (M16 ? 4 : 8) : kF32BK;
+  static constexpr int B_FLOATS = BNC ? kF32BK * B_STRIDE : BN * kF32BK;
+  static constexpr int STAGE = A_FLOATS + B_FLOATS;
+  static constexpr int AL = BM * kF32CH / 256;  // 16-byte A chunks per thread
+  static constexpr int BL = BN * kF32CH / 256;  // 16-byte B chunks per thread
+  static_assert(AL * 256 == BM * kF32CH && BL * 256 == BN * kF32CH, "loads cover the tile");
+  static_assert(2 * STAGE * 4 <= 160 * 1024, "LDS budget");
+};
+
+template <int ACT>
+__device__ __forceinline__ void f32_store(const F32Params& p, float (&v)[4], int m, int n) {
+  float bv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (p.bias != nullptr) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) bv[e] = n + e < p.N ? p.bias[n + e] : 0.0f;
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = apply_act<ACT>(v[e] + bv[e]);
+  float* dst = p.c + (int64_t)m * p.ldc + n;
+  if (p.vec_store && n + 4 <= p.N) {
+    *(f32x4v*)dst = f32x4v{v[0], v[1], v[2], v[3]};
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (n + e < p.N) dst[e] = v[e];
+  }
+}
+
+template <int BM, int BN, bool BNC, bool M16>
+__global__ void __launch_bounds__(256) gemm_f32_kernel(const F32Params p) {
+  using C = F32Cfg<BM, BN, BNC, M16>;
+  using AccT = std::conditional_t<M16, f32x4_t, f32x16_t>;
+  constexpr int BS = C::BS, NACC = M16 ? 4 : 16, KPF = M16 ? 16 : 8;  // K values per fragment group
+  constexpr int MI = C::MI, NI = C::NI, AL = C::AL, BL = C::BL;
+  __shared__ __attribute__((aligned(16))) float lds[2 * C::STAGE];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lr = M16 ? (lane & 15) : (lane & 31), hh = M16 ? (lane >> 4) : (lane >> 5);
+  const int bid = (int)blockIdx.x;
+  const int m0 = (bid % p.tiles_m) * BM, n0 = (bid / p.tiles_m) * BN;
+  const int nk = p.K / kF32BK;
+
+  // ---- global -> register sources (rows clamped; their results are never stored) ----
+  const float* a_src[AL];
+  int a_dst[AL];
+#pragma unroll
+  for (int j = 0; j < AL; ++j) {
+    const int q = tid + 256 * j, r = q / kF32CH, ch = q % kF32CH;
+    a_src[j] = p.a + (int64_t)min(m0 + r, p.M - 1) * p.lda + 4 * ch;
+    a_dst[j] = r * kF32BK + 4 * f32_pos(r, ch);
+  }
+  const float* b_src[BL];
+  int b_dst[BL];
+#pragma unroll
+  for (int j = 0; j < BL; ++j) {
+    const int q = tid + 256 * j;
+    if constexpr (BNC) {
+      // row k = q / (BN/4), 4 columns at (q % (BN/4)) * 4; N % 4 == 0 so a clamped
+      // chunk only ever lands in columns >= N
+      const int k = q / (BN / 4), c4 = (q % (BN / 4)) * 4;
+      b_src[j] = p.b + (int64_t)k * p.ldb + min(n0 + c4, p.N - 4);
+      b_dst[j] = C::A_FLOATS + k * C::B_STRIDE + c4;
+    } else {
+      const int r = q / kF32CH, ch = q % kF32CH;
+      b_src[j] = p.b + (int64_t)min(n0 + r, p.N - 1) * p.ldb + 4 * ch;
+      b_dst[j] = C::A_FLOATS + r * kF32BK + 4 * f32_pos(r, ch);
+    }
+  }
+  const int64_t b_kstep = BNC ? (int64_t)kF32BK * p.ldb : kF32BK;
+
+  f32x4v ra[AL], rb[BL];
+  auto load = [&](int kt) {
+#pragma unroll
+    for (int j = 0; j < AL; ++j) ra[j] = *(const f32x4v*)(a_src[j] + (int64_t)kt * kF32BK);
+#pragma unroll
+    for (int j = 0; j < BL; ++j) rb[j] = *(const f32x4v*)(b_src[j] + (int64_t)kt * b_kstep);
+  };
+  auto store = [&](int buf) {
+    float* s = lds + buf * C::STAGE;
+#pragma unroll
+    for (int j = 0; j < AL; ++j) *(f32x4v*)(s + a_dst[j]) = ra[j];
+#pragma unroll
+    for (int j = 0; j < BL; ++j) *(f32x4v*)(s + b_dst[j]) = rb[j];
+  };
+
+  AccT acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int r = 0; r < NACC; ++r) acc[i][j][r] = 0.0f;
+
+  const int rowA0 = wm * C::WM, rowB0 = wn * C::WN;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 1 < nk) load(kt + 1);
+    const float* s = lds + (kt & 1) * C::STAGE;
+    // fragments of K group q (KPF K values): A chunk (KPF/4) q + hh of each block's row,
+    // and B's matching 4 K values of each block's column
+    f32x4v af[2][MI], bf[2][NI];
+    auto frags = [&](int q, f32x4v (&fa)[MI], f32x4v (&fb)[NI]) {
+      const int chunk = (KPF / 4) * q + hh;
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int r = rowA0 + BS * i + lr;
+        fa[i] = *(const f32x4v*)(s + r * kF32BK + 4 * f32_pos(r, chunk));
+      }
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int n = rowB0 + BS * j + lr;
+        if constexpr (BNC) {
+          const float* col = s + C::A_FLOATS + (KPF * q + 4 * hh) * C::B_STRIDE + n;
+          fb[j] = f32x4v{col[0], col[C::B_STRIDE], col[2 * C::B_STRIDE], col[3 * C::B_STRIDE]};
+        } else {
+          fb[j] = *(const f32x4v*)(s + C::A_FLOATS + n * kF32BK + 4 * f32_pos(n, chunk));
+        }
+      }
+    };
+    // group q + 1's LDS reads are issued before group q's MFMAs, so their latency hides
+    // under 4*MI*NI MFMAs (the compiler otherwise reads each group right before use)
+    frags(0, af[0], bf[0]);
+#pragma unroll
+    for (int q = 0; q < kF32BK / KPF; ++q) {
+      if (q + 1 < kF32BK / KPF) frags(q + 1, af[(q + 1) & 1], bf[(q + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < NI; ++j) {
+            if constexpr (M16)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[q & 1][j][e], af[q & 1][i][e], acc[i][j], 0, 0, 0);
+            else
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[q & 1][j][e], af[q & 1][i][e], acc[i][j], 0, 0, 0);
+          }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (kt + 1 < nk) store((kt + 1) & 1);
+    __syncthreads();
+  }
+
+  auto epi = [&](auto act_tag) {
+    constexpr int ACT = decltype(act_tag)::value;
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int m = m0 + rowA0 + BS * i + lr;
+      if (m >= p.M) continue;
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int g = 0; g < NACC / 4; ++g) {
+          float v[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+          // 32x32: register group g holds columns 8g + 4hh ..; 16x16: columns 4hh ..
+          f32_store<ACT>(p, v, m, n0 + rowB0 + BS * j + (M16 ? 4 * hh : 8 * g + 4 * hh));
+        }
+    }
+  };
+  switch (p.act) {
+    case ACT_RELU: epi(std::integral_constant<int, ACT_RELU>{}); break;
+    case ACT_GELU: epi(std::integral_constant<int, ACT_GELU>{}); break;
+    case ACT_SILU: epi(std::integral_constant<int, ACT_SILU>{}); break;
+    case ACT_TANH: epi(std::integral_constant<int, ACT_TANH>{}); break;
+    case ACT_SIGMOID: epi(std::integral_constant<int, ACT_SIGMOID>{}); break;
+    default: epi(std::integral_constant<int, ACT_NONE>{}); break;
+  }
+}
+
+// Any strides, any K: 64x64 tile, BK 16, fp32 FMA.
+struct F32GenericParams {
+  const float* a;
+  const float* b;
+  const float* bias;
+  float* c;
+  int M, N, K;
+  int64_t sam, sak, sbk, sbn, scm;
+  int act;
+};
+
+__global__ void __launch_bounds__(256) gemm_f32_generic_kernel(const F32GenericParams p) {
+  __shared__ float sA[16][64 + 1];
+  __shared__ float sB[16][64 + 1];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < p.K; k0 += 16) {
+    for (int q = tid; q < 16 * 64; q += 256) {
+      const int kk = q / 64, mm = q % 64;
+      const int gm = m0 + mm, gk = k0 + kk, gn = n0 + mm;
+      sA[kk][mm] = (gm < p.M && gk < p.K) ? p.a[(int64_t)gm * p.sam + (int64_t)gk * p.sak] : 0.0f;
+      sB[kk][mm] = (gn < p.N && gk < p.K) ? p.b[(int64_t)gk * p.sbk + (int64_t)gn * p.sbn] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      float av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = sA[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = sB[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int gm = m0 + ty * 4 + i;
+    if (gm >= p.M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int gn = n0 + tx * 4 + j;
+      if (gn >= p.N) continue;
+      float v = acc[i][j] + (p.bias ? p.bias[gn] : 0.0f);
+      switch (p.act) {
+        case ACT_RELU: v = apply_act<ACT_RELU>(v); break;
+        case ACT_GELU: v = apply_act<ACT_GELU>(v); break;
+        case ACT_SILU: v = apply_act<ACT_SILU>(v); break;
+        case ACT_TANH: v = apply_act<ACT_TANH>(v); break;
+        case ACT_SIGMOID: v = apply_act<ACT_SIGMOID>(v); break;
+        default: break;
+      }
+      p.c[(int64_t)gm * p.scm + gn] = v;
+    }
+  }
+}
+
+inline bool al16(const void* q) { return ((uintptr_t)q & 15u) == 0; }
+
+constexpr bool kF32M16 = false;
+
+template <int BM, int BN, bool BNC>
+int launch_f32(F32Params p, hipStream_t st) {
+  p.tiles_m = (p.M + BM - 1) / BM;
+  p.tiles_n = (p.N + BN - 1) / BN;
+  const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n;
+  if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "gemm fp32: grid too large");
+  hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BNC, kF32M16>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+  return check_launch("gemm_f32_kernel");
+}
+
+template <bool BNC>
+int pick_f32(const F32Params& p, hipStream_t st) {
+  // the largest tile that still gives every CU a tile
+  const int64_t t128 = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128);
+  const int64_t t12864 = (int64_t)((p.M + 127) / 128) * ((p.N + 63) / 64);
+  if (t128 >= 240) return launch_f32<128, 128, BNC>(p, st);
+  if (t12864 >= 200) return launch_f32<128, 64, BNC>(p, st);
+  return launch_f32<64, 64, BNC>(p, st);
+}
+
+}  // namespace
+
+int launch_gemm_f32(const GemmF32Args& d, hipStream_t st) {
+  const bool fits = d.M < (1ll << 31) && d.N < (1ll << 31) && d.K < (1ll << 31);
+  const bool a_ok = d.sak == 1 && d.sam % 4 == 0 && al16(d.a) && d.sam >= d.K;
+  const bool b_kc = d.sbk == 1 && d.sbn % 4 == 0 && al16(d.b) && d.sbn >= d.K;
+  const bool b_nc = d.sbn == 1 && d.sbk % 4 == 0 && al16(d.b) && d.N % 4 == 0 && d.sbk >= d.N;
+  if (fits && d.K % kF32BK == 0 && d.K > 0 && a_ok && (b_kc || b_nc)) {
+    F32Params p{};
+    p.a = (const float*)d.a;
+    p.b = (const float*)d.b;
+    p.bias = (const float*)d.bias;
+    p.c = (float*)d.c;
+    p.M = (int)d.M;
+    p.N = (int)d.N;
+    p.K = (int)d.K;
+    p.lda = d.sam;
+    p.ldb = b_kc ? d.sbn : d.sbk;
+    p.ldc = d.scm;
+    p.act = d.act;
+    p.vec_store = d.scm % 4 == 0 && al16(d.c);
+    return b_kc ? pick_f32<false>(p, st) : pick_f32<true>(p, st);
+  }
+  if (!fits) return set_error(KORE_EUNSUPPORTED, "gemm fp32: dimension >= 2^31");
+  F32GenericParams g{};
+  g.a = (const float*)d.a;
+  g.b = (const float*)d.b;
+  g.bias = (const float*)d.bias;
+  g.c = (float*)d.c;
+  g.M = (int)d.M;
+  g.N = (int)d.N;
+  g.K = (int)d.K;
+  g.sam = d.sam;
+  g.sak = d.sak;
+  g.sbk = d.sbk;
+  g.sbn = d.sbn;
+  g.scm = d.scm;
+  g.act = d.act;
+  dim3 grid((unsigned)((d.N + 63) / 64), (unsigned)((d.M + 63) / 64));
+  hipLaunchKernelGGL(gemm_f32_generic_kernel, grid, dim3(256), 0, st, g);
+  return check_launch("gemm_f32_generic_kernel");
+}
+
+}  // namespace kore

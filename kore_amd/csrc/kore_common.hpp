@@ -168,4 +168,17 @@ struct GroupedA8Args {
   int block_rows;
 };
 int launch_grouped_a8w8(const GroupedA8Args& a, hipStream_t st);
+
+// fp32 GEMM + bias + activation (gemm_f32.hip, called by kore_gemm for KORE_DT_FP32):
+// A (m, k) at a[m*sam + k*sak], B (k, n) at b[k*sbk + n*sbn], C[m*scm + n], bias[N].
+struct GemmF32Args {
+  const void* a;
+  const void* b;
+  const void* bias;
+  void* c;
+  int64_t M, N, K;
+  int64_t sam, sak, sbk, sbn, scm;
+  int act;
+};
+int launch_gemm_f32(const GemmF32Args& d, hipStream_t st);
 }  // namespace kore

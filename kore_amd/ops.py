@@ -33,7 +33,7 @@ import torch
 
 from . import _lib
 
-DT_CODE = {torch.bfloat16: 0, torch.float16: 1}
+DT_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 ACT_CODE = {"none": 0, "relu": 1, "gelu": 2, "silu": 3, "tanh": 4, "sigmoid": 5}
 FP8_DTYPE = torch.float8_e4m3fn  # OCP e4m3 on gfx950 (kore/tasks/aiter_ref.py:37-62)
 
@@ -60,9 +60,10 @@ def _require_cuda(*ts: torch.Tensor) -> None:
 # --------------------------------------------------------------------------- #
 def gemm_fused(a: torch.Tensor, b: torch.Tensor, bias: torch.Tensor | None = None,
                act: str = "none") -> torch.Tensor:
-    """``act(a @ b + bias)`` in ``a.dtype`` (bf16/fp16), fp32 accumulate.
+    """``act(a @ b + bias)`` in ``a.dtype`` (bf16 / fp16 / fp32), fp32 accumulate.
 
-    a[M,K], b[K,N] with any strides (``b = W.t()`` views are the fast path), bias[N].
+    a[M,K], b[K,N] with any strides (``b = W.t()`` views and N-contiguous ``b`` are the
+    fast paths), bias[N].  fp32 runs on the fp32 matrix cores (full fp32 products).
     """
     _require_cuda(a, b)
     if a.dim() != 2 or b.dim() != 2:
@@ -70,7 +71,7 @@ def gemm_fused(a: torch.Tensor, b: torch.Tensor, bias: torch.Tensor | None = Non
     if a.shape[1] != b.shape[0]:
         raise ValueError(f"incompatible dims: a {tuple(a.shape)} @ b {tuple(b.shape)}")
     if a.dtype not in DT_CODE or b.dtype != a.dtype:
-        raise ValueError(f"gemm supports bf16/fp16 operands of one dtype (got {a.dtype}, {b.dtype})")
+        raise ValueError(f"gemm supports bf16/fp16/fp32 operands of one dtype (got {a.dtype}, {b.dtype})")
     if act not in ACT_CODE:
         raise ValueError(f"unknown activation {act!r}")
     M, K = a.shape
@@ -140,7 +141,7 @@ def batched_gemm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     _require_cuda(a, b)
     if a.dim() != 3 or b.dim() != 3 or a.shape[0] != b.shape[0] or a.shape[2] != b.shape[2]:
         raise ValueError(f"batched_gemm expects a[B,M,K], b[B,N,K] (got {tuple(a.shape)}, {tuple(b.shape)})")
-    if a.dtype not in DT_CODE or b.dtype != a.dtype:
+    if a.dtype not in (torch.bfloat16, torch.float16) or b.dtype != a.dtype:
         raise ValueError(f"batched_gemm supports bf16/fp16 (got {a.dtype}, {b.dtype})")
     Bn, M, K = a.shape
     N = b.shape[1]

@@ -12,7 +12,7 @@ the top-1 expert GEMM ``moe_grouped_gemm`` (the scorer's B=1 grouped form counts
 (``F = 0``, ``Q = 2*M*D*e + 4*M``: rows in, rows out, one int32 index per row).
 
 Peaks are MI355X's published dense figures (no sparsity): bf16/fp16 2.5 PFLOP/s,
-fp8 5.0 PFLOP/s, int8 5.0 POP/s, HBM3E 8.0 TB/s.  ``KORE_PEAK_BF16`` / ``KORE_PEAK_FP8`` /
+fp8 5.0 PFLOP/s, int8 5.0 POP/s, fp32 157.3 TFLOP/s, HBM3E 8.0 TB/s.  ``KORE_PEAK_BF16`` / ``KORE_PEAK_FP8`` /
 ``KORE_PEAK_HBM_BW`` override them as in the reference (``rooflines.py:84-97``).
 """
 
@@ -96,7 +96,7 @@ def roofline(operation: str, dims: dict[str, int], dtype: str) -> Roofline:
     f, q = flops_bytes(operation, dims, dtype)
     d = dtype.lower()
     pf = peaks["fp8_flops_per_s"] if "fp8" in d else peaks["int8_flops_per_s"] if "int8" in d else \
-        peaks["bf16_flops_per_s"]
+        peaks["fp32_flops_per_s"] if ("fp32" in d or "float32" in d) else peaks["bf16_flops_per_s"]
     pb = peaks["hbm_bytes_per_s"]
     tc, tm = f / pf, q / pb
     return Roofline(f, q, tc, tm, max(tc, tm), "mfma" if tc >= tm else "hbm", pf, pb)

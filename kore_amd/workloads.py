@@ -246,6 +246,18 @@ def bench_workloads():
     for act in ("gelu", "relu", "silu"):
         w[f"fp16_gemm_bias_{act}_4096"] = fused(act)
     w["bf16_batched_64x1024x1024x128"] = batched
+
+    def fp32_bias(M, N, K):
+        def build(dev):
+            g = _gen(dev, 0)
+            a = torch.randn((M, K), generator=g, device=dev) / K ** 0.5
+            b = torch.randn((K, N), generator=g, device=dev) / K ** 0.5
+            bias = torch.randn((N,), generator=g, device=dev)
+            return (lambda: kore_amd.gemm_bias(a, b, bias)), "gemm", {"M": M, "N": N, "K": K}, "fp32"
+        return build
+
+    # fp32 epilogue GEMM on the fp32 matrix cores (gen_gemm_bias_fp32 primary)
+    w["fp32_gemm_bias_512x4096x4096"] = fp32_bias(512, 4096, 4096)
     for M in (512, 128, 16):
         w[f"fp8_blockscale_{M}x7168x4096"] = fp8(M)
     def a8w8(M, N, K, kind):

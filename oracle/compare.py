@@ -27,6 +27,7 @@ import torch
 TASK_TOL = {
     "gemm": dict(atol=1e-2, rtol=1e-2, snr=30.0),
     "gemm_fusion": dict(atol=1e-2, rtol=1e-2, snr=30.0),
+    "gemm_fusion_fp32": dict(atol=1e-2, rtol=1e-2, snr=40.0),  # _genops.py:44 fp32 gate
     "batched_gemm": dict(atol=1e-2, rtol=1e-2, snr=30.0),
     "blockscale": dict(atol=5e-1, rtol=5e-2, snr=25.0),
     "blockscale_genv": dict(atol=1e-2, rtol=1e-2, snr=25.0),

@@ -153,3 +153,42 @@ def test_gemm_errors(gpu):
         kore_amd.gemm(a, torch.zeros((8, 4), dtype=torch.float16, device=gpu))
     with pytest.raises(ValueError):
         kore_amd.gemm(a.cpu(), torch.zeros((8, 4), dtype=torch.bfloat16))
+
+
+# gen_gemm_<op>_fp32 tasks (kore/tasks/gen_gemm_bias_fp32/task.yaml: minimal 64x256x256,
+# primary 512x4096x4096, validation 1024x2048x2048, 256x14336x4096, 512x4096x4095)
+@pytest.mark.parametrize("op", sorted(kore_amd.GEMM_FUSION_OPS))
+def test_gemm_fusion_fp32_ops(gpu, op):
+    """fp32 operands on the fp32 MFMA: every op on the minimal shape and a ragged one
+    (N-contiguous b, the task's draw), at the fp32 gate (40 dB, allclose 1e-2) and the
+    strict fp32 pair rule."""
+    has_bias, act = kore_amd.GEMM_FUSION_OPS[op]
+    fn = getattr(kore_amd, op)
+    for (M, N, K) in [(64, 256, 256), (300, 520, 224), (77, 132, 100)]:
+        g = torch.Generator().manual_seed(M)
+        sc = 1.0 / K ** 0.5
+        a = torch.randn((M, K), generator=g) * sc
+        b = torch.randn((K, N), generator=g) * sc
+        bias = torch.randn((N,), generator=g) if has_bias else None
+        args = (a, b, bias) if has_bias else (a, b)
+        out = fn(*[t.to(gpu) for t in args])
+        assert out.dtype == torch.float32
+        ref = gemm_fusion_ref(a, b, bias, act)
+        verdict(out, ref, "gemm_fusion_fp32", "fp32", f"{op} fp32 {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 4096, 4096), (1024, 2048, 2048), (256, 14336, 4096), (512, 4096, 4095)])
+@pytest.mark.parametrize("bt", [False, True])
+def test_gemm_fp32_task_shapes(gpu, M, N, K, bt):
+    """The fp32 task shapes, with b N-contiguous (the task's layout) or a W.t() view;
+    K = 4095 takes the generic kernel.  Rows are sampled for the oracle."""
+    g = torch.Generator(device=gpu).manual_seed(K)
+    sc = 1.0 / K ** 0.5
+    a = torch.randn((M, K), generator=g, device=gpu) * sc
+    b = (torch.randn((N, K), generator=g, device=gpu) * sc).t() if bt else torch.randn((K, N), generator=g, device=gpu) * sc
+    bias = torch.randn((N,), generator=g, device=gpu)
+    out = kore_amd.gemm_bias_gelu(a, b, bias)
+    rows = torch.unique(torch.cat([torch.arange(0, M, max(1, M // 64)), torch.tensor([M - 1])])).to(gpu)
+    ref = gemm_fusion_ref(a[rows].cpu(), b.cpu(), bias.cpu(), "gelu")
+    verdict(out[rows].cpu(), ref, "gemm_fusion_fp32", "fp32", f"fp32 {M}x{N}x{K} bt={bt}")
+    pair_only(out[rows].cpu(), ref, "fp32", f"fp32 {M}x{N}x{K}")

@@ -227,7 +227,7 @@ def test_every_fusion_op_has_candidates():
     import kore_amd
 
     for op in kore_amd.GEMM_FUSION_OPS:
-        for dt in ("bf16", "fp16"):
+        for dt in ("bf16", "fp16", "fp32"):
             assert (CAND / f"gen_{op}_{dt}" / "kernel.py").exists()
 
 
