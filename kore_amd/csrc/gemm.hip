@@ -21,6 +21,7 @@
 #include "kore_common.hpp"
 #include "tile_engine.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace kore {
@@ -37,6 +38,7 @@ struct TileParams {
   int64_t ldc;  // C row stride; C is N-contiguous
   int64_t sa, sb, sc;  // batch strides (elements)
   int tiles_m, tiles_n, tiles_per_batch;
+  int batch;  // number of batches (the persistent short-K kernel walks all of them)
   int act;
   int vec_store;  // 16-byte C stores allowed (ldc % 8 == 0, aligned)
   int bias_vec;   // bias is 8-byte aligned: 4-wide bias loads allowed
@@ -192,6 +194,280 @@ __global__ void __launch_bounds__(256)
 }
 
 // ---------------------------------------------------------------------------------
+// Persistent short-K kernel (K = 64 * NKS, NKS = 1 or 2; A K-contiguous).
+//
+// With K = 128 a 128x128 tile is 4 MFLOP against 32 KiB of output, so the time is the
+// output stream.  A store instruction stalls its wave while the memory system pushes
+// back, so a wave that both multiplies and stores serialises the two (measured with
+// s_memtime: ~1.5 us of every ~2.3 us per tile went to issuing the stores while no
+// other work ran).  Here one workgroup per CU has two roles, one wave of each per SIMD:
+//  * waves 0-3 (compute) load A, multiply and pack: wave w owns rows 32w .. 32w + 31
+//    and all 128 columns, and packs its finished rows into the LDS it read its own A
+//    rows from (so no other wave's operands are overwritten);
+//  * waves 4-7 (store) write the previous tile from LDS to memory with 16-byte
+//    row-contiguous buffer stores and never wait on vmcnt, so the output stream runs
+//    while the next tile is multiplied, and a compute wave's vmcnt counts its loads only.
+// Each tile walks three LDS slots: A rows (loaded two tiles ahead, direct-to-LDS), then
+// the packed output, then free.  One workgroup walks "segments": runs of up to SEG tiles
+// down one column of the output (one batch, one 128-column block of B, consecutive
+// 128-row blocks of A); the B block is loaded once per segment (K-contiguous B by direct
+// loads, N-contiguous B -- the B.transpose(1, 2) view of a [B, K, N] tensor -- through
+// registers, 8 K-rows x 8 columns per thread, transposed with v_perm into the same
+// K-contiguous layout).  Rows past M and columns past N get an offset beyond the buffer
+// size, which the hardware drops.
+//
+// Segment order: u = (batch * nseg + seg) * tiles_n + n-block, so consecutive segments
+// share their A blocks; when the grid and the segment count are multiples of 8, XCD x
+// (the workgroups g with g % 8 == x, dispatched round-robin) owns the x-th eighth of the
+// segments and its 32 CUs read the same A blocks from its L2 at the same time.  Tiles
+// past the last row block (when SEG does not divide it) load the last block again and
+// store nothing.
+// ---------------------------------------------------------------------------------
+// Wait until at most n (>= 0) vector-memory ops are outstanding, n rounded down to a
+// multiple of 4 and capped at 60: waiting for fewer is always safe, and with in-order
+// retirement a cap below the number of ops issued after the awaited one still implies it.
+__device__ __forceinline__ void wait_vmcnt_le(int n) {
+  if (n >= 60) wait_vmcnt<60>();
+  else if (n >= 48) { if (n >= 56) wait_vmcnt<56>(); else if (n >= 52) wait_vmcnt<52>(); else wait_vmcnt<48>(); }
+  else if (n >= 32) { if (n >= 44) wait_vmcnt<44>(); else if (n >= 40) wait_vmcnt<40>(); else if (n >= 36) wait_vmcnt<36>(); else wait_vmcnt<32>(); }
+  else if (n >= 16) { if (n >= 28) wait_vmcnt<28>(); else if (n >= 24) wait_vmcnt<24>(); else if (n >= 20) wait_vmcnt<20>(); else wait_vmcnt<16>(); }
+  else if (n >= 12) wait_vmcnt<12>();
+  else if (n >= 8) wait_vmcnt<8>();
+  else if (n >= 4) wait_vmcnt<4>();
+  else wait_vmcnt<0>();
+}
+
+template <typename T, int NKS, int BL>
+__global__ void __launch_bounds__(512) gemm_shortk_kernel(const TileParams p, const int seg) {
+  using Op = MfmaOp<T>;
+  constexpr int BM = 128, BN = 128, NW = 4, WROWS = 32, NI = 4, NA = 3;
+  constexpr int A_ELEMS = BM * kBK, B_ELEMS = BN * kBK;  // one 64-wide K stage
+  // a slot holds the tile's A rows, then its packed output (rows of 256 bytes)
+  constexpr int A_BUF = NKS * A_ELEMS > BM * BN ? NKS * A_ELEMS : BM * BN;
+  constexpr int HALF = A_BUF / 2;                 // 16 KiB: the second K stage / rows 16..31
+  constexpr int B_OFF = NA * A_BUF;
+  constexpr bool NC = BL == B_NC;
+  constexpr int AJ = BM / 8 / NW, BJ = BN / 8 / NW;
+  constexpr int NQ = NKS * 4;                     // 16-wide K sub-steps
+  // sub-steps whose B fragments stay in registers for the whole segment: N-contiguous B
+  // keeps none (its segment-start transposes need those registers; 256 VGPRs at most)
+  constexpr int NQR = NC ? 0 : (NQ < 4 ? NQ : 4);
+  constexpr int L = NKS * AJ;                     // A loads per compute wave per tile
+  constexpr int NCBLK = (NKS * kBK / 8) * (BN / 8);  // 8x8 blocks of an N-contiguous B tile
+  static_assert(NCBLK <= 256, "one 8x8 block per compute thread");
+  static_assert(HALF == 16 * 128 * 4, "a wave's 16 output rows (4 KiB) per half slot");
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[NA * A_BUF + NKS * B_ELEMS];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool storer = wave >= NW;
+  const int w = wave & 3, ctid = tid & 255;
+  const int lr = lane & 31, hh = lane >> 5;
+  const int rowA0 = w * WROWS;
+
+  // ---- this workgroup's segments u = first + k * step, k < nsegs ----
+  const int nseg = (p.tiles_m + seg - 1) / seg;
+  const int total = p.batch * nseg * p.tiles_n;
+  const int G = (int)gridDim.x, g = (int)blockIdx.x;
+  int first, step, nsegs;
+  if ((G & 7) == 0 && (total & 7) == 0) {
+    const int per = total >> 3, c = g >> 3, gx = G >> 3;
+    first = (g & 7) * per + c;
+    step = gx;
+    nsegs = c < per ? (per - c + gx - 1) / gx : 0;
+  } else {
+    first = g;
+    step = G;
+    nsegs = g < total ? (total - g + G - 1) / G : 0;
+  }
+  const int count = nsegs * seg;
+  // tile i of this workgroup: batch, row block mb (live if < tiles_m), column n0
+  auto tile_of = [&](int i, int& batch, int& mb, int& n0) {
+    const int k = i / seg;
+    const int u = first + k * step;
+    const int bs = u / p.tiles_n;
+    n0 = (u - bs * p.tiles_n) * BN;
+    batch = bs / nseg;
+    mb = (bs - batch * nseg) * seg + (i - k * seg);
+  };
+
+  // ---- (compute waves) A rows of tile i into slot `slot`, direct-to-LDS, all of K ----
+  auto issue_a = [&](int i, int slot) {
+    int batch, mb, n0;
+    tile_of(i, batch, mb, n0);
+    const int m0 = min(mb, p.tiles_m - 1) * BM;
+    const int rows_a = min(BM, p.M - m0);
+    const uint16_t* A = p.a + (int64_t)batch * p.sa + (int64_t)m0 * p.lda;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (uint32_t)(((int64_t)(rows_a - 1) * p.lda + p.K) * 2));
+    uint16_t* base = lds + slot * A_BUF;
+#pragma unroll
+    for (int j = 0; j < AJ; ++j) {
+      const int r = (w + NW * j) * 8 + (lane >> 3);
+      const uint32_t v = (uint32_t)((min(r, rows_a - 1) * (int)p.lda + 8 * ((lane & 7) ^ swz8(r))) * 2);
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+        buf_lds16(ra, v, (uint32_t)ks * (kBK * 2), base + ks * A_ELEMS + (w + NW * j) * 8 * kBK);
+    }
+  };
+
+  // ---- (compute waves) the B block of tile i's column into LDS; complete (for this
+  // wave) on return ----
+  auto load_b = [&](int i) {
+    int batch, mb, n0;
+    tile_of(i, batch, mb, n0);
+    uint16_t* sB = lds + B_OFF;
+    if constexpr (!NC) {
+      const int rows_b = min(BN, p.N - n0);
+      const uint16_t* B = p.b + (int64_t)batch * p.sb + (int64_t)n0 * p.ldb;
+      const __amdgpu_buffer_rsrc_t rb = make_rsrc(B, (uint32_t)(((int64_t)(rows_b - 1) * p.ldb + p.K) * 2));
+#pragma unroll
+      for (int j = 0; j < BJ; ++j) {
+        const int r = (w + NW * j) * 8 + (lane >> 3);
+        const uint32_t v = (uint32_t)((min(r, rows_b - 1) * (int)p.ldb + 8 * ((lane & 7) ^ swz8(r))) * 2);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks)
+          buf_lds16(rb, v, (uint32_t)ks * (kBK * 2), sB + ks * B_ELEMS + (w + NW * j) * 8 * kBK);
+      }
+      wait_vmcnt<0>();
+    } else {
+      // compute thread t owns block (kb, nb) = (t / 16, t % 16); N % 8 == 0, so a block is
+      // wholly inside or past N, and blocks past N re-read the last one (never stored)
+      const int kb = ctid / (BN / 8), nb = ctid % (BN / 8);
+      if (ctid < NCBLK) {
+        const uint16_t* src = p.b + (int64_t)batch * p.sb + (int64_t)(8 * kb) * p.ldb + min(n0 + 8 * nb, p.N - 8);
+        u32x4_t rows[8], tr[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) rows[r] = ld16(src + (int64_t)r * p.ldb);
+        transpose8x8(rows, tr);
+        uint16_t* dst = sB + (kb >> 3) * B_ELEMS;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const int n = 8 * nb + jj;
+          *(u32x4_t*)(dst + n * kBK + (((kb & 7) ^ swz8(n)) << 3)) = tr[jj];
+        }
+      }
+    }
+  };
+
+  // Packed output of compute wave w in a slot: its rows 0..15 at w * 4 KiB, rows 16..31
+  // at HALF + w * 4 KiB (exactly where its own A rows of K stages 0 and 1 were);
+  // 256-byte rows whose 16-byte chunk c sits at c ^ (row % 16).
+  auto out_addr = [&](uint16_t* slotp, int ww, int row, int chunk) -> uint16_t* {
+    return slotp + (row >> 4) * HALF + ww * 2048 + (row & 15) * 128 + ((chunk ^ (row & 15)) << 3);
+  };
+
+  // ---- (store waves) write the packed tile i of slot `slot` ----
+  auto store_tile = [&](int i, int slot) {
+    int batch, mb, n0;
+    tile_of(i, batch, mb, n0);
+    const int rows_c = mb < p.tiles_m ? min(BM, p.M - mb * BM) : 0, cols_c = min(BN, p.N - n0);
+    uint16_t* Cb = p.c + (int64_t)batch * p.sc + (int64_t)min(mb, p.tiles_m - 1) * BM * p.ldc + n0;
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(Cb, (uint32_t)(((int64_t)(BM - 1) * p.ldc + cols_c) * 2));
+    uint16_t* slotp = lds + slot * A_BUF;
+    // store wave w writes compute wave w's 32 rows: 4 rows of 16 chunks per instruction
+#pragma unroll
+    for (int it = 0; it < WROWS / 4; ++it) {
+      const int row = it * 4 + (lane >> 4), chunk = lane & 15;
+      const u32x4_t v = *(const u32x4_t*)out_addr(slotp, w, row, chunk);
+      const int r = rowA0 + row, c = chunk * 8;
+      const bool ok = r < rows_c && c < cols_c;  // N % 8 == 0: 8 columns wholly in or out
+      const uint32_t voff = ok ? (uint32_t)((r * (int)p.ldc + c) * 2) : 0xfffffff0u;
+      __builtin_amdgcn_raw_buffer_store_b128(v, rc, voff, 0, 0);
+    }
+  };
+
+  // fragment row R + lr (R % 32 == 0): swz8(R + lr) = (lr & 7) ^ (lr >> 3) ^ (4 * ((R / 32) & 1))
+  int off[2][4];
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int sw = ((lr & 7) ^ (lr >> 3) ^ (4 * par)) & 7;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) off[par][kk] = lr * kBK + (((2 * kk + hh) ^ sw) << 3);
+  }
+
+  if (count == 0) return;  // uniform per workgroup, before any barrier
+  if (!storer) {
+    issue_a(0, 0);
+    if (count > 1) issue_a(1, 1);
+  }
+  // (compute waves) B fragments of the segment's first NQR sub-steps, held in registers;
+  // the rest are read from LDS per tile (all of them would exceed 256 VGPRs)
+  u32x4_t bq[NQR > 0 ? NQR : 1][NI];
+  int slot = 0;
+  for (int i = 0; i < count; ++i) {
+    const int pslot = slot == 0 ? NA - 1 : slot - 1;  // slot of tile i - 1, then of tile i + 2
+    if (i % seg == 0) {
+      // a new segment: every compute wave finished its B reads before the last barrier
+      if (!storer) load_b(i);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      exec_barrier();
+      if (!storer) {
+#pragma unroll
+        for (int q = 0; q < NQR; ++q)
+#pragma unroll
+          for (int b = 0; b < NI; ++b)
+            bq[q][b] = *(const u32x4_t*)(lds + B_OFF + (q >> 2) * B_ELEMS + b * 32 * kBK + off[b & 1][q & 3]);
+      }
+    }
+    if (!storer) {
+      // A loads issued after tile i's: tile i + 1's (B loads were waited for completely)
+      if (i + 1 < count) wait_vmcnt<L>();
+      else wait_vmcnt<0>();
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    exec_barrier();
+
+    if (!storer) {
+      uint16_t* slotp = lds + slot * A_BUF;
+      f32x16_t acc[NI];
+#pragma unroll
+      for (int b = 0; b < NI; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[b][r] = 0.0f;
+      // fragments of sub-step q + 1 (A, and B past the registered ones) are read before
+      // the MFMAs of sub-step q
+      const uint16_t* sA = slotp + rowA0 * kBK;
+      const int par = w & 1;
+      u32x4_t af[2], bl[2][NI];
+      auto frags = [&](int q, u32x4_t& fa, u32x4_t (&fb)[NI]) {
+        fa = *(const u32x4_t*)(sA + (q >> 2) * A_ELEMS + off[par][q & 3]);
+        if (q >= NQR) {
+#pragma unroll
+          for (int b = 0; b < NI; ++b)
+            fb[b] = *(const u32x4_t*)(lds + B_OFF + (q >> 2) * B_ELEMS + b * 32 * kBK + off[b & 1][q & 3]);
+        }
+      };
+      frags(0, af[0], bl[0]);
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        if (q + 1 < NQ) frags(q + 1, af[(q + 1) & 1], bl[(q + 1) & 1]);
+#pragma unroll
+        for (int b = 0; b < NI; ++b) acc[b] = Op::mma32(q < NQR ? bq[q < NQR ? q : 0][b] : bl[q & 1][b], af[q & 1], acc[b]);
+      }
+      // pack into this wave's own A rows (its reads of them have completed)
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int b = 0; b < NI; ++b)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const int col = out_col(b, gq, lane);
+          *(u32x2_t*)(out_addr(slotp, w, lr, col >> 3) + (col & 7)) =
+              u32x2_t{Op::pack2(acc[b][4 * gq], acc[b][4 * gq + 1]), Op::pack2(acc[b][4 * gq + 2], acc[b][4 * gq + 3])};
+        }
+    } else if (i >= 1) {
+      store_tile(i - 1, pslot);
+    }
+    // the packed tile i is complete; tile i - 1's slot has been read by the store waves
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    exec_barrier();
+    if (!storer && i + 2 < count) issue_a(i + 2, pslot);
+    slot = slot + 1 == NA ? 0 : slot + 1;
+  }
+  // the last packed tile (its slot: the one before `slot`)
+  if (storer) store_tile(count - 1, slot == 0 ? NA - 1 : slot - 1);
+}
+
+// ---------------------------------------------------------------------------------
 // Generic-stride kernel: 64x64 tile, BK 16, fp32 FMA, any strides / K / alignment.
 // ---------------------------------------------------------------------------------
 struct GenericParams {
@@ -294,6 +570,7 @@ int launch_tile(const GemmDesc& d, hipStream_t stream) {
   p.tiles_m = (int)((d.M + BM - 1) / BM);
   p.tiles_n = (int)((d.N + BN - 1) / BN);
   p.tiles_per_batch = p.tiles_m * p.tiles_n;
+  p.batch = (int)d.batch;
   p.act = d.act;
   p.vec_store = (d.scm % 8 == 0) && aligned16(d.c) && (d.sc % 8 == 0);
   p.bias_vec = d.bias != nullptr && ((uintptr_t)d.bias & 7u) == 0;
@@ -323,6 +600,7 @@ int launch_buf(const GemmDesc& d, hipStream_t stream) {
   p.tiles_m = (int)((d.M + BM - 1) / BM);
   p.tiles_n = (int)((d.N + BN - 1) / BN);
   p.tiles_per_batch = p.tiles_m * p.tiles_n;
+  p.batch = (int)d.batch;
   p.act = d.act;
   p.vec_store = (d.scm % 8 == 0) && aligned16(d.c) && (d.sc % 8 == 0);
   p.bias_vec = d.bias != nullptr && ((uintptr_t)d.bias & 7u) == 0;
@@ -330,6 +608,59 @@ int launch_buf(const GemmDesc& d, hipStream_t stream) {
   if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "gemm: grid too large");
   hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
   return check_launch("gemm_buf_kernel");
+}
+
+// CUs of the current device (cached per device; 256 on MI355X).
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Persistent short-K launch: one 128 KiB-LDS workgroup per CU, at most one per tile.
+template <typename T, int BL>
+int launch_shortk(const GemmDesc& d, hipStream_t stream) {
+  TileParams p;
+  p.a = (const uint16_t*)d.a;
+  p.b = (const uint16_t*)d.b;
+  p.bias = nullptr;
+  p.c = (uint16_t*)d.c;
+  p.M = (int)d.M;
+  p.N = (int)d.N;
+  p.K = (int)d.K;
+  p.lda = d.sam;
+  p.ldb = (BL == B_KC) ? d.sbn : d.sbk;
+  p.ldc = d.scm;
+  p.sa = d.sa;
+  p.sb = d.sb;
+  p.sc = d.sc;
+  p.tiles_m = (int)((d.M + 127) / 128);
+  p.tiles_n = (int)((d.N + 127) / 128);
+  p.tiles_per_batch = p.tiles_m * p.tiles_n;
+  p.batch = (int)d.batch;
+  p.act = KORE_ACT_NONE;
+  p.vec_store = 0;
+  p.bias_vec = 0;
+  const int64_t tiles = (int64_t)p.tiles_per_batch * d.batch;
+  // segment length: about the tiles per CU, at most one column
+  const int64_t per_cu = tiles / device_cus();
+  const int seg = (int)std::max<int64_t>(1, std::min<int64_t>(p.tiles_m, per_cu));
+  const int64_t nseg = (p.tiles_m + seg - 1) / seg;
+  const int64_t total = nseg * p.tiles_n * d.batch;
+  if (total > 0x7fffffff || total * seg > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "gemm: grid too large");
+  const int grid = (int)std::min<int64_t>(total, device_cus());
+  const dim3 gr((unsigned)grid), blk(512);
+  if (BL == B_KC && d.K == 64) hipLaunchKernelGGL((gemm_shortk_kernel<T, 1, B_KC>), gr, blk, 0, stream, p, seg);
+  if (BL == B_KC && d.K == 128) hipLaunchKernelGGL((gemm_shortk_kernel<T, 2, B_KC>), gr, blk, 0, stream, p, seg);
+  if (BL == B_NC && d.K == 64) hipLaunchKernelGGL((gemm_shortk_kernel<T, 1, B_NC>), gr, blk, 0, stream, p, seg);
+  if (BL == B_NC && d.K == 128) hipLaunchKernelGGL((gemm_shortk_kernel<T, 2, B_NC>), gr, blk, 0, stream, p, seg);
+  return check_launch("gemm_shortk_kernel");
 }
 
 template <typename T>
@@ -380,6 +711,14 @@ int dispatch_typed(const GemmDesc& d, hipStream_t stream) {
     const bool short_k = d.K <= 256;
     const bool small = mid_tiles < 128;
     if (b_kc && big && buf_ok && !short_k) return launch_buf<T, 256, 256>(d, stream);
+    // K of one or two 64-wide steps, no epilogue, enough 128x128 tiles to give every
+    // CU several: the persistent short-K kernel (16-byte buffer stores need N % 8 == 0
+    // and 16-byte aligned C rows; per-tile byte offsets must stay below 2^31).
+    const bool shortk = (d.K == 64 || d.K == 128) && d.act == KORE_ACT_NONE && d.bias == nullptr &&
+                        d.N % 8 == 0 && d.scm % 8 == 0 && d.sc % 8 == 0 && aligned16(d.c) &&
+                        d.sam * 2 * 128 + d.K * 2 < (1ll << 31) && (b_nc || d.sbn * 2 * 128 + d.K * 2 < (1ll << 31)) &&
+                        d.scm * 2 * 128 < (1ll << 31) && mid_tiles >= 4 * (int64_t)device_cus();
+    if (shortk) return b_kc ? launch_shortk<T, B_KC>(d, stream) : launch_shortk<T, B_NC>(d, stream);
     if (b_kc) {
       if (big && !short_k) return launch_tile<T, B_KC, 256, 256>(d, stream);
       return small ? launch_tile<T, B_KC, 64, 64>(d, stream) : launch_tile<T, B_KC, 128, 128>(d, stream);

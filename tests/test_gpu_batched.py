@@ -44,3 +44,34 @@ def test_batched_metamorphic_and_determinism(gpu):
     permuted = kore_amd.batched_gemm(a[perm], b[perm])
     assert bit_equal(permuted, full[perm]), "batch permutation equivariance"
     assert bit_equal(kore_amd.batched_gemm(a, b), full), "determinism"
+
+
+# Persistent short-K kernel (K of 64 or 128, >= 4 tiles of 128x128 per CU): ragged M/N,
+# both B layouts, tile counts that are and are not multiples of 8 (the XCD schedule).
+@pytest.mark.parametrize("Bn,M,N,K,bnc", [(40, 1000, 1016, 128, True), (20, 1000, 1024, 64, True),
+                                          (33, 520, 1032, 64, False), (24, 1024, 1028, 128, False), (5, 4000, 1024, 128, False), (3, 3000, 2048, 64, True),
+                                          (64, 1024, 1024, 128, False)])
+def test_batched_short_k(gpu, Bn, M, N, K, bnc):
+    g = torch.Generator().manual_seed(M + N + K)
+    a = (torch.randn((Bn, M, K), generator=g) * 0.1).bfloat16()
+    if bnc:
+        b = (torch.randn((Bn, K, N), generator=g) * 0.1).bfloat16().transpose(1, 2)
+    else:
+        b = (torch.randn((Bn, N, K), generator=g) * 0.1).bfloat16()
+    out = kore_amd.batched_gemm(a.to(gpu), b.to(gpu))
+    ref = batched_gemm_ref(a, b)
+    tag = f"short-K B{Bn} {M}x{N}x{K} {'NC' if bnc else 'KC'}"
+    verdict(out, ref, "batched_gemm", "bf16", tag)
+    pair_only(out, ref, "bf16", tag)
+    assert bit_equal(kore_amd.batched_gemm(a.to(gpu), b.to(gpu)), out), "determinism"
+
+
+def test_dense_short_k(gpu):
+    """Dense A.W^T with K = 128 and enough tiles takes the persistent short-K kernel too
+    (ragged M and N, 4-tile column segments)."""
+    g = torch.Generator().manual_seed(5)
+    a = (torch.randn((4000, 128), generator=g) * 0.1).bfloat16()
+    w = (torch.randn((4104, 128), generator=g) * 0.1).bfloat16()
+    out = kore_amd.gemm(a.to(gpu), w.to(gpu).t())
+    from oracle.gemm import matmul_ref
+    verdict(out, matmul_ref(a, w.t()), "gemm", "bf16", "short-K dense 4000x4104x128")
