@@ -194,6 +194,42 @@ __global__ void __launch_bounds__(256)
 }
 
 // ---------------------------------------------------------------------------------
+// Small problems (fewer than 128 tiles of 128x128, e.g. 1024^3 with 64): the time is
+// load latency, not MFMA work (a 64x64 tile with a register double buffer waits one
+// full memory round trip per 64-wide K step).  32 x BN tiles on the skinny ring
+// engine instead: four times the tiles of 64x64 at BN = 128 (256 for 1024^3, one per
+// CU) and an NSLOT-deep ring of direct-to-LDS K stages, NSLOT - 1 of them in flight
+// per CU.  Waves sit side by side over N (32 x BN/4 each); the epilogue is the dense
+// one (bias, activation, 16-byte row stores).  K % 64 == 0, A and B K-contiguous.
+// ---------------------------------------------------------------------------------
+template <typename T, int BN, int NSLOT>
+__global__ void __launch_bounds__(256) gemm_ring_kernel(const TileParams p) {
+  using E = SkinnyRingEngine<T, BN, 1, NSLOT>;
+  constexpr int NI = E::NI;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int batch, m0, n0;
+  tile_coords(p, E::BM, BN, batch, m0, n0);
+  const uint16_t* A = p.a + batch * p.sa + (int64_t)m0 * p.lda;
+  const uint16_t* B = p.b + batch * p.sb + (int64_t)n0 * p.ldb;
+  const int rows_a = min(E::BM, p.M - m0), rows_b = min(BN, p.N - n0);
+  E eng;
+  eng.ra = make_rsrc(A, (uint32_t)(((int64_t)(rows_a - 1) * p.lda + p.K) * 2));
+  eng.rb = make_rsrc(B, (uint32_t)(((int64_t)(rows_b - 1) * p.ldb + p.K) * 2));
+  const int ar = E::a_row(wave, lane);
+  eng.a_voff = (uint32_t)(((int64_t)min(ar, rows_a - 1) * p.lda + 8 * E::chunk(ar, lane)) * 2);
+#pragma unroll
+  for (int j = 0; j < E::BJ; ++j) {
+    const int r = E::b_row(wave, lane, j);
+    eng.b_voff[j] = (uint32_t)(((int64_t)min(r, rows_b - 1) * p.ldb + 8 * E::chunk(r, lane)) * 2);
+  }
+  f32x16_t acc[1][NI];
+  E::zero(acc);
+  eng.mainloop(lds, 0, p.K, acc);
+  dense_epilogue<T, 1, NI, E::BM, E::WCOLS>(acc, lds, p, m0, n0, 0, wave, wave, lane, p.c + batch * p.sc);
+}
+
+// ---------------------------------------------------------------------------------
 // Persistent short-K kernel (K = 64 * NKS, NKS = 1 or 2; A K-contiguous).
 //
 // With K = 128 a 128x128 tile is 4 MFLOP against 32 KiB of output, so the time is the
@@ -610,19 +646,6 @@ int launch_buf(const GemmDesc& d, hipStream_t stream) {
   return check_launch("gemm_buf_kernel");
 }
 
-// CUs of the current device (cached per device; 256 on MI355X).
-int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 // Persistent short-K launch: one 128 KiB-LDS workgroup per CU, at most one per tile.
 template <typename T, int BL>
 int launch_shortk(const GemmDesc& d, hipStream_t stream) {
@@ -661,6 +684,36 @@ int launch_shortk(const GemmDesc& d, hipStream_t stream) {
   if (BL == B_NC && d.K == 64) hipLaunchKernelGGL((gemm_shortk_kernel<T, 1, B_NC>), gr, blk, 0, stream, p, seg);
   if (BL == B_NC && d.K == 128) hipLaunchKernelGGL((gemm_shortk_kernel<T, 2, B_NC>), gr, blk, 0, stream, p, seg);
   return check_launch("gemm_shortk_kernel");
+}
+
+template <typename T>
+int launch_ring(const GemmDesc& d, hipStream_t stream) {
+  constexpr int BM = 32, BN = 128, NSLOT = 7;
+  TileParams p;
+  p.a = (const uint16_t*)d.a;
+  p.b = (const uint16_t*)d.b;
+  p.bias = (const uint16_t*)d.bias;
+  p.c = (uint16_t*)d.c;
+  p.M = (int)d.M;
+  p.N = (int)d.N;
+  p.K = (int)d.K;
+  p.lda = d.sam;
+  p.ldb = d.sbn;
+  p.ldc = d.scm;
+  p.sa = d.sa;
+  p.sb = d.sb;
+  p.sc = d.sc;
+  p.tiles_m = (int)((d.M + BM - 1) / BM);
+  p.tiles_n = (int)((d.N + BN - 1) / BN);
+  p.tiles_per_batch = p.tiles_m * p.tiles_n;
+  p.batch = (int)d.batch;
+  p.act = d.act;
+  p.vec_store = (d.scm % 8 == 0) && aligned16(d.c) && (d.sc % 8 == 0);
+  p.bias_vec = d.bias != nullptr && ((uintptr_t)d.bias & 7u) == 0;
+  const int64_t blocks = (int64_t)p.tiles_per_batch * d.batch;
+  if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "gemm: grid too large");
+  hipLaunchKernelGGL((gemm_ring_kernel<T, BN, NSLOT>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+  return check_launch("gemm_ring_kernel");
 }
 
 template <typename T>
@@ -719,6 +772,8 @@ int dispatch_typed(const GemmDesc& d, hipStream_t stream) {
                         d.sam * 2 * 128 + d.K * 2 < (1ll << 31) && (b_nc || d.sbn * 2 * 128 + d.K * 2 < (1ll << 31)) &&
                         d.scm * 2 * 128 < (1ll << 31) && mid_tiles >= 4 * (int64_t)device_cus();
     if (shortk) return b_kc ? launch_shortk<T, B_KC>(d, stream) : launch_shortk<T, B_NC>(d, stream);
+    // few tiles and a long K: the latency-bound case, on the deep direct-to-LDS ring
+    if (b_kc && small && buf_ok && d.K >= 512) return launch_ring<T>(d, stream);
     if (b_kc) {
       if (big && !short_k) return launch_tile<T, B_KC, 256, 256>(d, stream);
       return small ? launch_tile<T, B_KC, 64, 64>(d, stream) : launch_tile<T, B_KC, 128, 128>(d, stream);

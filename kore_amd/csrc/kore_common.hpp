@@ -148,6 +148,8 @@ __device__ __forceinline__ void lds_fence_barrier() { __syncthreads(); }
 namespace kore {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+// Compute units of the current device (cached per device; 256 on MI355X).
+int device_cus();
 
 // Top-1 grouped fp8 a8w8 GEMM over an expert-sorted token order (tiles of
 // gemm_fp8_blockscale.hip, called by the grouped entry in moe.hip): xq[M,K] (row

@@ -37,6 +37,28 @@ def test_gemm_config_1024_bt(gpu, seed):
     verdict(out, matmul_ref(a, b), "gemm", "bf16", f"1024^3 seed {seed}")
 
 
+@pytest.mark.parametrize("M,N,K,dtype,op", [(1000, 1000, 1024, torch.bfloat16, "gemm"),
+                                             (300, 520, 640, torch.float16, "gemm_bias_gelu"),
+                                             (1, 4096, 4096, torch.bfloat16, "gemm"),
+                                             (64, 4096, 4096, torch.float16, "gemm_bias_silu")])
+def test_gemm_ring_small(gpu, M, N, K, dtype, op):
+    """Few tiles and K >= 512 with b = W.t() run the 32x128 ring kernel: ragged M and N,
+    a single row, and the fused epilogues on it."""
+    g = torch.Generator().manual_seed(M + N)
+    a = (torch.randn((M, K), generator=g) / K ** 0.5).to(dtype)
+    w = (torch.randn((N, K), generator=g) / K ** 0.5).to(dtype)
+    bias = (torch.randn((N,), generator=g) * 0.1).to(dtype)
+    if op == "gemm":
+        out = kore_amd.gemm_fused(a.to(gpu), w.to(gpu).t())
+        ref = gemm_fusion_ref(a, w.t(), None, "none")
+    else:
+        out = getattr(kore_amd, op)(a.to(gpu), w.to(gpu).t(), bias.to(gpu))
+        ref = gemm_fusion_ref(a, w.t(), bias, kore_amd.GEMM_FUSION_OPS[op][1])
+    dt = "bf16" if dtype == torch.bfloat16 else "fp16"
+    verdict(out, ref, "gemm_fusion", dt, f"ring {op} {M}x{N}x{K}")
+    pair_only(out, ref, dt, f"ring {op} {M}x{N}x{K}")
+
+
 @pytest.mark.parametrize("M,N,K", [(64, 512, 512), (1, 4096, 4096), (4096, 4096, 4095),
                                    (513, 1000, 200), (4096, 4096, 4096)])
 def test_gemm_reference_task_shapes(gpu, M, N, K):
