@@ -373,7 +373,21 @@ __global__ void __launch_bounds__(256)
   const int wm = wave / E::WN, wn = wave % E::WN;
 
   const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-  const int mb = bid % p.max_mblocks, nt = bid / p.max_mblocks;
+  int mb, nt;
+  if constexpr (MODE == MOE_PLAIN) {
+    mb = bid % p.max_mblocks;
+    nt = bid / p.max_mblocks;
+  } else {
+    // grouped raster: GM row blocks sweep the column tiles together
+    constexpr int GM = 1024 / BM;
+    const int width = GM * p.ntiles;
+    const int grp = bid / width;
+    const int first_m = grp * GM;
+    const int gsz = min(p.max_mblocks - first_m, GM);
+    const int tl = bid - grp * width;
+    mb = first_m + tl % gsz;
+    nt = tl / gsz;
+  }
   const int total = p.offsets[p.E];
   if (mb * BM >= total) return;  // uniform: the whole workgroup leaves
   const int e = p.block_expert[(mb * BM) / p.abm];
