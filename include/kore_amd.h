@@ -88,6 +88,22 @@ int kore_batched_gemm(int dtype,
                       int64_t batch, int64_t M, int64_t N, int64_t K, void* stream);
 
 /*
+ * GEMM backward of the linear layer Y = X @ W^T (X [M,K], W [N,K], dY [M,N]):
+ *   dX [M,K] = dY @ W,   dW [N,K] = dY^T @ X,   fp32 accumulate, `dtype` out (bf16/fp16).
+ *   Row strides ldx, ldw, lddy, lddx, lddw (unit stride along rows).  W^T, X^T and
+ *   dY^T are formed in `workspace` (so both GEMMs read K-contiguous operands), which
+ *   must hold kore_gemm_backward_workspace_bytes(M, N, K) bytes.
+ * Replaces: gemm_backward(x, w, dy) -> (dx, dw)
+ *           kore/tasks/gemm_backward_bf16/seed_triton.py:74-86 (ENTRY reference.py:22,
+ *           oracle reference.py:64-72)
+ */
+size_t kore_gemm_backward_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int kore_gemm_backward(int dtype, const void* x, int64_t ldx, const void* w, int64_t ldw,
+                       const void* dy, int64_t lddy, void* dx, int64_t lddx, void* dw,
+                       int64_t lddw, int64_t M, int64_t N, int64_t K,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * fp8 a8w8 block-scaled GEMM (OCP e4m3):
  *   Y[M,N] (bf16) = sum_k (xq[m,k]*xs[m,k/128]) * (wq[n,k]*ws[n/128,k/128])
  *   xq [M,K] row stride ldx; wq [N,K] row stride ldw; xs [M,K/128] fp32 with strides

@@ -25,6 +25,9 @@ SIGNATURES = {
                          _i64, _i64, _i64, _vp]),
     "kore_batched_gemm": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
                                  _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "kore_gemm_backward_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "kore_gemm_backward": (_i32, [_i32, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64,
+                                  _vp, _sz, _vp]),
     "kore_gemm_a8w8_blockscale": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _vp, _i64,
                                          _i64, _vp, _i64, _i64, _i64, _i64, _vp]),
     "kore_gemm_a8w8": (_i32, [_i32, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64,

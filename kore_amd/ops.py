@@ -157,6 +157,39 @@ def batched_gemm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
 
 
 # --------------------------------------------------------------------------- #
+# GEMM backward (linear layer Y = X @ W^T)
+# --------------------------------------------------------------------------- #
+def gemm_backward(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor):
+    """``(dx, dw) = (dy @ w, dy^T @ x)`` in ``x.dtype`` (bf16/fp16), fp32 accumulate.
+
+    x[M,K], w[N,K], dy[M,N] with unit stride along rows (the task's layouts); the
+    entry of ``kore/tasks/gemm_backward_bf16`` (``gemm_backward(x, w, dy)``).
+    """
+    _require_cuda(x, w, dy)
+    if x.dim() != 2 or w.dim() != 2 or dy.dim() != 2:
+        raise ValueError("gemm_backward expects 2-D x[M,K], w[N,K], dy[M,N]")
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K or tuple(dy.shape) != (M, N):
+        raise ValueError(f"incompatible shapes x{tuple(x.shape)} w{tuple(w.shape)} dy{tuple(dy.shape)}")
+    if x.dtype not in (torch.bfloat16, torch.float16) or w.dtype != x.dtype or dy.dtype != x.dtype:
+        raise ValueError(f"gemm_backward takes bf16/fp16 tensors of one dtype (got {x.dtype}, {w.dtype}, {dy.dtype})")
+    x, w, dy = (t if t.stride(1) == 1 else t.contiguous() for t in (x, w, dy))
+    dx = torch.empty((M, K), dtype=x.dtype, device=x.device)
+    dw = torch.empty((N, K), dtype=x.dtype, device=x.device)
+    if M == 0 or N == 0 or K == 0:
+        return dx.zero_(), dw.zero_()
+    lib = _lib.load()
+    nbytes = lib.kore_gemm_backward_workspace_bytes(M, N, K)
+    ws = torch.empty((nbytes,), dtype=torch.uint8, device=x.device)
+    rc = lib.kore_gemm_backward(DT_CODE[x.dtype], x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0),
+                                dy.data_ptr(), dy.stride(0), dx.data_ptr(), dx.stride(0), dw.data_ptr(),
+                                dw.stride(0), M, N, K, ws.data_ptr(), nbytes, _stream(x))
+    _lib.check(rc)
+    return dx, dw
+
+
+# --------------------------------------------------------------------------- #
 # fp8 a8w8 block-scaled GEMM
 # --------------------------------------------------------------------------- #
 def gemm_a8w8_blockscale(xq: torch.Tensor, wq: torch.Tensor, x_scale: torch.Tensor,

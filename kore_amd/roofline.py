@@ -61,6 +61,10 @@ def flops_bytes(operation: str, dims: dict[str, int], dtype: str) -> tuple[float
         M, N, K = dims["M"], dims["N"], dims["K"]
         Eu = dims.get("E_used", dims["E"])
         return 2.0 * M * N * K, float((M * K + Eu * N * K + M * N) * e)
+    if op == "gemm_backward":
+        # two GEMMs (dX = dY.W, dW = dY^T.X): the reference's dense formula counts one
+        M, N, K = dims["M"], dims["N"], dims["K"]
+        return 4.0 * M * N * K, float((2 * M * K + 2 * N * K + M * N) * e)
     if op in ("moe_permute", "moe_unpermute"):
         M, D = dims["M"], dims["D"]
         return 0.0, float(2 * M * D * e + 4 * M)

@@ -36,6 +36,18 @@ def dense_inputs(M: int, N: int, K: int, seed: int = 0, device="cpu", dtype=torc
     return a, bt.t()
 
 
+def backward_inputs(M: int, N: int, K: int, seed: int = 0, device="cpu", dtype=torch.bfloat16):
+    """gemm_backward inputs (x[M,K], w[N,K], dy[M,N]): x, w ~ N(0,1)/sqrt(K), dy ~ N(0,1),
+    as the reference draws them (kore/tasks/gemm_backward_bf16/reference.py:39-55), from
+    one CPU generator here."""
+    g = _gen(device, seed)
+    sc = 1.0 / (K ** 0.5)
+    x = (torch.randn((M, K), generator=g, device=device) * sc).to(dtype)
+    w = (torch.randn((N, K), generator=g, device=device) * sc).to(dtype)
+    dy = torch.randn((M, N), generator=g, device=device).to(dtype)
+    return x, w, dy
+
+
 def fused_inputs(M: int, N: int, K: int, seed: int = 0, device="cpu", dtype=torch.float16,
                  with_bias: bool = True):
     g = _gen(device, seed)
@@ -246,6 +258,15 @@ def bench_workloads():
     for act in ("gelu", "relu", "silu"):
         w[f"fp16_gemm_bias_{act}_4096"] = fused(act)
     w["bf16_batched_64x1024x1024x128"] = batched
+
+    def backward(M, N, K):
+        def build(dev):
+            x, wt, dy = backward_inputs(M, N, K, seed=0, device=dev)
+            return (lambda: kore_amd.gemm_backward(x, wt, dy)), "gemm_backward", {"M": M, "N": N, "K": K}, "bf16"
+        return build
+
+    # gemm_backward_bf16 primary shape (task.yaml): dX = dY.W and dW = dY^T.X
+    w["bf16_gemm_backward_8192x4096x4096"] = backward(8192, 4096, 4096)
 
     def fp32_bias(M, N, K):
         def build(dev):

@@ -68,3 +68,15 @@ def batched_gemm_ref(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     Pinned per batch against ``matmul_ref`` and a batch-permutation relation.
     """
     return torch.bmm(a.float(), b.float().transpose(1, 2)).to(a.dtype)
+
+
+def gemm_backward_ref(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor):
+    """Linear-layer backward oracle for ``Y = X @ W^T``: fp32 ``(dX, dW)``.
+
+    ``dX = dY @ W`` and ``dW = dY^T @ X`` on fp32 upcasts -- the gradients torch
+    autograd gives for the fp32 forward, which is the reference's oracle
+    (``kore/tasks/gemm_backward_bf16/reference.py:64-72``).  Pinned against autograd
+    and central finite differences in ``tests/test_oracle_gemm.py``.
+    """
+    xf, wf, dyf = x.float(), w.float(), dy.float()
+    return dyf @ wf, dyf.t() @ xf

@@ -21,7 +21,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 from kore_amd import workloads as W  # noqa: E402
-from oracle.gemm import batched_gemm_ref, gemm_fusion_ref, matmul_ref  # noqa: E402
+from oracle.gemm import batched_gemm_ref, gemm_backward_ref, gemm_fusion_ref, matmul_ref  # noqa: E402
 from oracle.moe import moe_align_ref, moe_ref, trace32_bias  # noqa: E402
 from oracle.quant import matmul_a8w8_ref, matmul_blockscale_ref  # noqa: E402
 
@@ -38,6 +38,9 @@ def build() -> dict:
         g["gemm_bias_act_fp16"][f"out_{act}"] = gemm_fusion_ref(a, b, bias, act)
     a, b = W.batched_inputs(3, 32, 64, 128, seed=13)
     g["batched_bf16"] = {"a": a.contiguous(), "bt": b.transpose(1, 2).contiguous(), "out": batched_gemm_ref(a, b)}
+    x, w, dy = W.backward_inputs(48, 40, 72, seed=18)
+    dx, dw = gemm_backward_ref(x, w, dy)
+    g["gemm_backward_bf16"] = {"x": x, "w": w, "dy": dy, "dx": dx, "dw": dw}
     xq, wq, xs, ws = W.fp8_inputs(40, 256, 384, seed=14)
     g["fp8_blockscale"] = {"xq": xq.view(torch.uint8), "wq": wq.view(torch.uint8), "xs": xs, "ws": ws,
                            "out": matmul_blockscale_ref(xq, wq, xs, ws)}

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from kore_amd import workloads as W
-from oracle.gemm import batched_gemm_ref, gemm_fusion_ref, matmul_ref
+from oracle.gemm import batched_gemm_ref, gemm_backward_ref, gemm_fusion_ref, matmul_ref
 from oracle.moe import moe_align_ref, moe_ref, trace32_bias
 from oracle.quant import matmul_a8w8_ref, matmul_blockscale_ref
 from tests.fourprong import verdict
@@ -38,24 +38,44 @@ def test_golden_inputs_are_the_seeded_draws():
     assert _eq(ti, GOLDEN["fused_moe"]["ti"]) and _eq(w2, GOLDEN["fused_moe"]["w2"])
     xq, wq, xs, ws = W.a8w8_inputs(24, 256, 384, "int8", "pertoken", seed=17)
     assert _eq(xq, GOLDEN["a8w8_int8"]["xq"]) and _eq(ws, GOLDEN["a8w8_int8"]["ws"])
+    x, w, dy = W.backward_inputs(48, 40, 72, seed=18)
+    g = GOLDEN["gemm_backward_bf16"]
+    assert _eq(x, g["x"]) and _eq(w, g["w"]) and _eq(dy, g["dy"])
+
+
+def _ulp_eq(x, y):
+    """Oracle outputs against the fixture: equal, except that a host whose BLAS sums in
+    another order may round an element to the neighbouring value (one unit in the last
+    place of the output dtype)."""
+    if x.dtype != y.dtype or x.shape != y.shape:
+        return False
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        return torch.equal(x, y)
+    ulp = 2.0 ** (-7 if x.dtype == torch.bfloat16 else -10)
+    yf = y.float()
+    return bool(((x.float() - yf).abs() <= ulp * yf.abs().clamp(min=2.0 ** -14)).all())
 
 
 def test_oracle_reproduces_golden_outputs():
     g = GOLDEN["gemm_bf16"]
-    assert _eq(matmul_ref(g["a"], g["bt"].t()), g["out"])
+    assert _ulp_eq(matmul_ref(g["a"], g["bt"].t()), g["out"])
     g = GOLDEN["gemm_bias_act_fp16"]
     for act in ("gelu", "relu", "silu"):
-        assert _eq(gemm_fusion_ref(g["a"], g["bt"].t(), g["bias"], act), g[f"out_{act}"])
+        assert _ulp_eq(gemm_fusion_ref(g["a"], g["bt"].t(), g["bias"], act), g[f"out_{act}"])
     g = GOLDEN["batched_bf16"]
-    assert _eq(batched_gemm_ref(g["a"], g["bt"].transpose(1, 2)), g["out"])
+    assert _ulp_eq(batched_gemm_ref(g["a"], g["bt"].transpose(1, 2)), g["out"])
     g = GOLDEN["fp8_blockscale"]
-    assert _eq(matmul_blockscale_ref(g["xq"].view(FP8), g["wq"].view(FP8), g["xs"], g["ws"]), g["out"])
+    assert _ulp_eq(matmul_blockscale_ref(g["xq"].view(FP8), g["wq"].view(FP8), g["xs"], g["ws"]), g["out"])
     g = GOLDEN["fused_moe"]
-    assert _eq(moe_ref(g["hidden"], g["w1"], g["w2"], g["tw"], g["ti"]), g["out"])
+    assert _ulp_eq(moe_ref(g["hidden"], g["w1"], g["w2"], g["tw"], g["ti"]), g["out"])
     g = GOLDEN["a8w8_fp8"]
-    assert _eq(matmul_a8w8_ref(g["xq"].view(FP8), g["wq"].view(FP8), g["xs"], g["ws"]), g["out"])
+    assert _ulp_eq(matmul_a8w8_ref(g["xq"].view(FP8), g["wq"].view(FP8), g["xs"], g["ws"]), g["out"])
     g = GOLDEN["a8w8_int8"]
-    assert _eq(matmul_a8w8_ref(g["xq"], g["wq"], g["xs"], g["ws"]), g["out"])
+    assert _ulp_eq(matmul_a8w8_ref(g["xq"], g["wq"], g["xs"], g["ws"]), g["out"])
+    g = GOLDEN["gemm_backward_bf16"]
+    dx, dw = gemm_backward_ref(g["x"], g["w"], g["dy"])
+    # fp32 gradients: another CPU's BLAS may sum in another order, so within fp32 rounding
+    assert torch.allclose(dx, g["dx"], rtol=1e-5, atol=1e-5) and torch.allclose(dw, g["dw"], rtol=1e-5, atol=1e-5)
     g = GOLDEN["moe_align"]
     off, srt, blk = moe_align_ref(g["ti"], int(g["E"]), int(g["block"]))
     assert np.array_equal(off, g["offsets"].numpy()) and np.array_equal(srt, g["sorted"].numpy())
@@ -88,6 +108,10 @@ def test_hip_matches_golden(gpu):
     g = GOLDEN["fused_moe"]
     out = kore_amd.fused_moe(d(g["hidden"]), d(g["w1"]), d(g["w2"]), d(g["tw"]), d(g["ti"]))
     verdict(out, g["out"], "fused_moe", "bf16", "golden fused_moe")
+    g = GOLDEN["gemm_backward_bf16"]
+    dx, dw = kore_amd.gemm_backward(d(g["x"]), d(g["w"]), d(g["dy"]))
+    verdict(dx, g["dx"], "gemm_backward_dx", "bf16", "golden gemm_backward dx")
+    verdict(dw, g["dw"], "gemm_backward_dw", "bf16", "golden gemm_backward dw")
     g = GOLDEN["moe_align"]
     off, srt, blk = kore_amd.moe_align(d(g["ti"]), int(g["E"]), int(g["block"]))
     n = int(g["offsets"][-1])

@@ -214,3 +214,39 @@ def test_gemm_fp32_task_shapes(gpu, M, N, K, bt):
     ref = gemm_fusion_ref(a[rows].cpu(), b.cpu(), bias.cpu(), "gelu")
     verdict(out[rows].cpu(), ref, "gemm_fusion_fp32", "fp32", f"fp32 {M}x{N}x{K} bt={bt}")
     pair_only(out[rows].cpu(), ref, "fp32", f"fp32 {M}x{N}x{K}")
+
+
+# gemm_backward_bf16 (kore/tasks/gemm_backward_bf16/task.yaml: minimal 256^3, primary
+# 8192x4096x4096, validation 32768x4096x4096, 4096x14336x4096, 8192x4096x8192,
+# 4096x4095x4096) plus a ragged small shape
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (8192, 4096, 4096), (4096, 4095, 4096), (4096, 14336, 4096),
+                                   (300, 200, 136)])
+def test_gemm_backward_task_shapes(gpu, M, N, K):
+    """dX = dY.W and dW = dY^T.X against the fp32 oracle at the task tolerances (dx
+    atol 5e-2, dw atol 2e-1, rtol 2e-2, SNR >= 25 dB); the multi-GB shapes are checked
+    on sampled rows of dX and columns of dW, plus determinism."""
+    from oracle.gemm import gemm_backward_ref
+
+    x, w, dy = W.backward_inputs(M, N, K, seed=M + N)
+    xg, wg, dyg = x.to(gpu), w.to(gpu), dy.to(gpu)
+    dx, dw = kore_amd.gemm_backward(xg, wg, dyg)
+    assert dx.shape == (M, K) and dw.shape == (N, K) and dx.dtype == dw.dtype == torch.bfloat16
+    step_m, step_k = max(1, M // 48), max(1, K // 48)
+    rows = torch.unique(torch.cat([torch.arange(0, M, step_m), torch.tensor([M - 1])]))
+    cols = torch.unique(torch.cat([torch.arange(0, K, step_k), torch.tensor([K - 1])]))
+    rdx, _ = gemm_backward_ref(x[rows], w, dy[rows])
+    _, rdw = gemm_backward_ref(x[:, cols], w[:, cols], dy)
+    verdict(dx[rows.to(gpu)].cpu(), rdx, "gemm_backward_dx", "bf16", f"dx {M}x{N}x{K}")
+    verdict(dw[:, cols.to(gpu)].cpu(), rdw, "gemm_backward_dw", "bf16", f"dw {M}x{N}x{K}")
+    dx2, dw2 = kore_amd.gemm_backward(xg, wg, dyg)
+    assert bit_equal(dx2, dx) and bit_equal(dw2, dw), "determinism"
+
+
+def test_gemm_backward_errors(gpu):
+    x = torch.zeros((8, 16), dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError):
+        kore_amd.gemm_backward(x, torch.zeros((4, 8), dtype=torch.bfloat16, device=gpu),
+                               torch.zeros((8, 4), dtype=torch.bfloat16, device=gpu))
+    with pytest.raises(ValueError):
+        kore_amd.gemm_backward(x, torch.zeros((4, 16), dtype=torch.float16, device=gpu),
+                               torch.zeros((8, 4), dtype=torch.bfloat16, device=gpu))

@@ -203,6 +203,8 @@ EXPECTED_ENTRIES = {
     "genb_moe_align_block_offsets_bf16": ("moe_align_block_offsets", 3),
     "genb_moe_align_block_offsets_fp16": ("moe_align_block_offsets", 3),
     "genb_moe_expert_offsets_bf16": ("moe_expert_offsets", 2), "genb_moe_expert_offsets_fp16": ("moe_expert_offsets", 2),
+    # gemm_backward_bf16/reference.py:22 ENTRY, candidate_grads calls fn(x, w, dy)
+    "gemm_backward_bf16": ("gemm_backward", 3),
 }
 
 

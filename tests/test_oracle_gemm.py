@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle.gemm import act_fp32, batched_gemm_ref, gemm_fusion_ref, matmul_ref
+from oracle.gemm import act_fp32, batched_gemm_ref, gemm_backward_ref, gemm_fusion_ref, matmul_ref
 
 
 def bf16_rne(x: np.ndarray) -> np.ndarray:
@@ -146,3 +146,34 @@ def test_batched_ref_per_batch_and_permutation():
         assert torch.equal(got[i], matmul_ref(a[i], b[i].t()))
     perm = torch.tensor([2, 0, 3, 1])
     assert torch.equal(batched_gemm_ref(a[perm], b[perm]), got[perm])
+
+
+def test_gemm_backward_oracle_is_the_autograd_gradient():
+    """The backward oracle equals torch autograd of the fp32 forward X @ W^T (the
+    reference's oracle, kore/tasks/gemm_backward_bf16/reference.py:64-72) and central
+    finite differences of L = sum(dY * (X @ W^T)) in float64; swapping the two
+    gradients (or dropping the transpose on dY) fails both."""
+    from kore_amd import workloads as W
+
+    x, w, dy = W.backward_inputs(16, 12, 20, seed=3)
+    dx, dw = gemm_backward_ref(x, w, dy)
+    assert dx.shape == (16, 20) and dw.shape == (12, 20) and dx.dtype == torch.float32
+    xf = x.float().requires_grad_(True)
+    wf = w.float().requires_grad_(True)
+    (xf @ wf.t()).backward(dy.float())
+    assert torch.allclose(dx, xf.grad, rtol=1e-5, atol=1e-6)
+    assert torch.allclose(dw, wf.grad, rtol=1e-5, atol=1e-6)
+    xd, wd, dyd = x.double(), w.double(), dy.double()
+
+    def loss(a, b):
+        return float((dyd * (a @ b.t())).sum())
+
+    h = 1e-3
+    for i, j in [(0, 0), (5, 7), (15, 19)]:
+        e = torch.zeros_like(xd)
+        e[i, j] = h
+        assert abs((loss(xd + e, wd) - loss(xd - e, wd)) / (2 * h) - float(dx[i, j])) < 1e-4
+    for i, j in [(0, 0), (3, 11), (11, 19)]:
+        e = torch.zeros_like(wd)
+        e[i, j] = h
+        assert abs((loss(xd, wd + e) - loss(xd, wd - e)) / (2 * h) - float(dw[i, j])) < 1e-4
