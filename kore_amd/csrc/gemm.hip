@@ -158,12 +158,13 @@ __global__ void __launch_bounds__(kEngineThreads)
 }
 
 
-// Buffer-load pipelined variant for K-contiguous A and B (the A.B^T / A.W^T layouts)
-// with K % 64 == 0.
-template <typename T, int BM, int BN>
+// Buffer-load pipelined variant for K-contiguous A, K % 64 == 0 and either B layout:
+// K-contiguous B (the A.B^T / A.W^T layouts) or N-contiguous B (natural [K, N], N % 8 ==
+// 0), whose fragments come out of LDS through transpose reads.
+template <typename T, int BM, int BN, int BL>
 __global__ void __launch_bounds__(256)
     gemm_buf_kernel(const TileParams p) {
-  using E = BufPipeEngine<T, BM, BN>;
+  using E = BufPipeEngine<T, BM, BN, 2, 2, 1, BL>;
   constexpr int MI = E::MI, NI = E::NI;
   __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -171,21 +172,34 @@ __global__ void __launch_bounds__(256)
   int batch, m0, n0;
   tile_coords(p, BM, BN, batch, m0, n0);
   const uint16_t* A = p.a + batch * p.sa + (int64_t)m0 * p.lda;
-  const uint16_t* B = p.b + batch * p.sb + (int64_t)n0 * p.ldb;
   uint16_t* C = p.c + batch * p.sc;
   const int rows_a = min(BM, p.M - m0), rows_b = min(BN, p.N - n0);
   E eng;
   eng.ra = make_rsrc(A, (uint32_t)(((int64_t)(rows_a - 1) * p.lda + p.K) * 2));
-  eng.rb = make_rsrc(B, (uint32_t)(((int64_t)(rows_b - 1) * p.ldb + p.K) * 2));
 #pragma unroll
   for (int j = 0; j < E::AJ; ++j) {
     const int r = E::a_row(wave, lane, j);
     eng.a_voff[j] = (uint32_t)(((int64_t)min(r, rows_a - 1) * p.lda + 8 * E::chunk(r, lane)) * 2);
   }
+  if constexpr (BL == B_KC) {
+    const uint16_t* B = p.b + batch * p.sb + (int64_t)n0 * p.ldb;
+    eng.rb = make_rsrc(B, (uint32_t)(((int64_t)(rows_b - 1) * p.ldb + p.K) * 2));
 #pragma unroll
-  for (int j = 0; j < E::BJ; ++j) {
-    const int r = E::b_row(wave, lane, j);
-    eng.b_voff[j] = (uint32_t)(((int64_t)min(r, rows_b - 1) * p.ldb + 8 * E::chunk(r, lane)) * 2);
+    for (int j = 0; j < E::BJ; ++j) {
+      const int r = E::b_row(wave, lane, j);
+      eng.b_voff[j] = (uint32_t)(((int64_t)min(r, rows_b - 1) * p.ldb + 8 * E::chunk(r, lane)) * 2);
+    }
+  } else {
+    // K-rows of the n0 column block; chunks past N (N % 8 == 0) re-read the last chunk,
+    // which only feeds output columns that are never stored.
+    const uint16_t* B = p.b + batch * p.sb + n0;
+    eng.rb = make_rsrc(B, (uint32_t)(((int64_t)(p.K - 1) * p.ldb + rows_b) * 2));
+    eng.b_kstep = (uint32_t)(kBK * p.ldb * 2);
+#pragma unroll
+    for (int j = 0; j < E::BJ; ++j) {
+      const int kr = E::nc_krow(wave, lane, j);
+      eng.b_voff[j] = (uint32_t)(((int64_t)kr * p.ldb + min(8 * E::nc_chunk(kr, lane), rows_b - 8)) * 2);
+    }
   }
   f32x16_t acc[MI][NI];
   E::zero(acc);
@@ -667,7 +681,7 @@ int launch_tile(const GemmDesc& d, hipStream_t stream) {
 }
 
 
-template <typename T, int BM, int BN>
+template <typename T, int BM, int BN, int BL>
 int launch_buf(const GemmDesc& d, hipStream_t stream) {
   TileParams p;
   p.a = (const uint16_t*)d.a;
@@ -678,7 +692,7 @@ int launch_buf(const GemmDesc& d, hipStream_t stream) {
   p.N = (int)d.N;
   p.K = (int)d.K;
   p.lda = d.sam;
-  p.ldb = d.sbn;
+  p.ldb = (BL == B_KC) ? d.sbn : d.sbk;
   p.ldc = d.scm;
   p.sa = d.sa;
   p.sb = d.sb;
@@ -692,7 +706,7 @@ int launch_buf(const GemmDesc& d, hipStream_t stream) {
   p.bias_vec = d.bias != nullptr && ((uintptr_t)d.bias & 7u) == 0;
   const int64_t blocks = (int64_t)p.tiles_per_batch * d.batch;
   if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "gemm: grid too large");
-  hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
   return check_launch("gemm_buf_kernel");
 }
 
@@ -813,7 +827,12 @@ int dispatch_typed(const GemmDesc& d, hipStream_t stream) {
     const int64_t mid_tiles = ((d.M + 127) / 128) * ((d.N + 127) / 128) * d.batch;
     const bool short_k = d.K <= 256;
     const bool small = mid_tiles < 128;
-    if (b_kc && big && buf_ok && !short_k) return launch_buf<T, 256, 256>(d, stream);
+    if (b_kc && big && buf_ok && !short_k) return launch_buf<T, 256, 256, B_KC>(d, stream);
+    // N-contiguous B on the same engine: B bytes from the tile's first column through
+    // the last K-row must fit the 32-bit buffer offsets.
+    const bool buf_nc_ok = d.K % 64 == 0 && d.sam * 2 * 256 + d.K * 2 < (1ll << 31) &&
+                           d.sbk * 2 * d.K + d.N * 2 < (1ll << 31);
+    if (!b_kc && b_nc && big && buf_nc_ok && !short_k) return launch_buf<T, 256, 256, B_NC>(d, stream);
     // K of one or two 64-wide steps, no epilogue, enough 128x128 tiles to give every
     // CU several: the persistent short-K kernel (16-byte buffer stores need N % 8 == 0
     // and 16-byte aligned C rows; per-tile byte offsets must stay below 2^31).

@@ -298,7 +298,33 @@ __device__ __forceinline__ void buf_lds16(__amdgpu_buffer_rsrc_t r, uint32_t vof
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_dst, 16, (int)voff, (int)soff, 0, 0);
 }
 
-template <typename T, int BM, int BN, int WM_ = 2, int WN_ = 2, int AP = 1>
+// LDS transpose read (gfx950 ds_read_b64_tr_b16).  Within each group of 16 lanes, lane
+// c supplies the address of 4 consecutive 16-bit values S[c][0..3]; lane i receives
+// S[4e + i/4][i % 4] for e = 0..3.  So when lane c points at K-row k0 + c/4, columns
+// n0 + 4 (c % 4) .. + 3 of an N-contiguous tile, lane i gets column n0 + i at K-rows
+// k0 .. k0 + 3: four K-consecutive values of one column, an MFMA operand fragment.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t* lds_s16x4_ptr;
+
+__device__ __forceinline__ u32x2_t lds_read_tr16(const uint16_t* p) {
+  return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)p));
+}
+
+// Direct-to-LDS load issued as inline asm (M0 = LDS destination).  With the builtin the
+// compiler records an LDS DMA write and, unable to prove that a following transpose
+// read does not alias it, puts a vmcnt(0) wait in front of every such read, draining
+// the load pipeline.  Loads issued this way are invisible to the compiler: the callers
+// order them with explicit vmcnt waits and barriers, and no compiler-generated M0 use
+// may sit between them (M0 is not preserved).
+__device__ __forceinline__ void buf_lds16_asm(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                              const uint16_t* lds_dst) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds_dst);
+  // one wait state between the SALU write of M0 and the LDS DMA that reads it
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :: "v"(voff), "s"(r), "s"(soff), "s"(m0) : "memory");
+}
+
+template <typename T, int BM, int BN, int WM_ = 2, int WN_ = 2, int AP = 1, int BL = B_KC>
 struct BufPipeEngine {
   static constexpr int WM = WM_, WN = WN_, NW = WM * WN;
   static_assert(NW == 4, "4 waves");
@@ -320,19 +346,38 @@ struct BufPipeEngine {
   // Logical 16-byte chunk lane `lane` fetches for `row` (element offset 8 * chunk).
   static __device__ __forceinline__ int chunk(int row, int lane) { return (lane & 7) ^ swz8(row); }
 
+  // N-contiguous B (BL == B_NC): a stage holds 64 K-rows of BN elements, so one direct
+  // load instruction (512 elements) fills NCR whole K-rows.  16-byte chunk c of K-row k
+  // lives at chunk c ^ nc_x(k & 3) with nc_x = {0, 4, 10, 14}: the four K-rows one
+  // transpose read touches (32 bytes each, 2 chunks) then sit in four distinct 32-byte
+  // bank slots of a 128-byte window, and with the next 16 lanes' chunk pair (same
+  // K-rows) in eight distinct slots of a 256-byte window.
+  static constexpr bool NC = BL == B_NC;
+  static constexpr int NCR = 512 / BN, NCH = BN / 8;
+  static_assert(!NC || BN == 128 || BN == 256, "N-contiguous B tile width");
+  static __device__ __forceinline__ int nc_x(int r) { return ((r & 1) * 4) ^ ((r >> 1) * 10); }
+  static __device__ __forceinline__ int nc_krow(int wave, int lane, int j) { return (wave + NW * j) * NCR + lane / NCH; }
+  static __device__ __forceinline__ int nc_chunk(int krow, int lane) { return (lane % NCH) ^ nc_x(krow & 3); }
+
   __amdgpu_buffer_rsrc_t ra, ra2, rb;  // ra2: second A plane (same offsets), AP == 2
   uint32_t a_voff[AJ], b_voff[BJ];      // bytes: row * row_stride + 16 * chunk
+  uint32_t b_kstep;                     // NC: bytes of B between consecutive 64-row K stages
 
-  __device__ __forceinline__ void issue_one(uint16_t* lds, int slot, uint32_t soff, int wave, int q) {
+  __device__ __forceinline__ void issue_one(uint16_t* lds, int slot, uint32_t soff, uint32_t soffb, int wave,
+                                            int q) {
     uint16_t* sA = lds + slot * STAGE;
+    auto ld = [&](__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t so, uint16_t* dst) {
+      if constexpr (NC) buf_lds16_asm(r, voff, so, dst);
+      else buf_lds16(r, voff, so, dst);
+    };
     if (q < AJ) {
-      buf_lds16(ra, a_voff[q], soff, sA + (wave + NW * q) * 8 * kBK);
+      ld(ra, a_voff[q], soff, sA + (wave + NW * q) * 8 * kBK);
     } else if (AP == 2 && q < 2 * AJ) {
       const int j = q - AJ;
-      buf_lds16(ra2, a_voff[j], soff, sA + A_ELEMS + (wave + NW * j) * 8 * kBK);
+      ld(ra2, a_voff[j], soff, sA + A_ELEMS + (wave + NW * j) * 8 * kBK);
     } else {
       const int j = q - AP * AJ;
-      buf_lds16(rb, b_voff[j], soff, sA + B_OFF + (wave + NW * j) * 8 * kBK);
+      ld(rb, b_voff[j], soffb, sA + B_OFF + (wave + NW * j) * 8 * kBK);
     }
   }
 
@@ -366,6 +411,18 @@ struct BufPipeEngine {
       }
     }
     const int rowA0 = wm * WROWS, rowB0 = wn * WCOLS;
+    // NC: lane (16-lane group g, index c) reads K-rows 16 ks + 8 (lane / 32) + c / 4
+    // (+ 4 for the upper half of the fragment), columns rowB0 + 32 j + 16 (g & 1) +
+    // 4 (c % 4); the chunk swizzle touches chunk bits 0-3 only, so the per-lane part
+    // depends on j % 4 (offNC) and the rest is a constant offset.
+    constexpr int NCJ = NI < 4 ? NI : 4;
+    int offNC[NCJ];
+    if constexpr (NC) {
+      const int c = lane & 15, x = nc_x(c >> 2), low = 2 * ((lane >> 4) & 1) + ((c & 3) >> 1);
+#pragma unroll
+      for (int j = 0; j < NCJ; ++j)
+        offNC[j] = (8 * hh + (c >> 2)) * BN + rowB0 + (((4 * j + low) ^ x) << 3) + 4 * (c & 1);
+    }
     // Fragment f of a sub-step: f < AP*MI -> A plane f/MI block f%MI, else B block.
     auto read_one = [&](int slot, int ks, int f, u32x4_t (&af)[AP * MI], u32x4_t (&bf)[NI]) {
       if (f < AP * MI) {
@@ -373,7 +430,13 @@ struct BufPipeEngine {
         af[f] = *(const u32x4_t*)(lds + slot * STAGE + pl * A_ELEMS + rowA0 * kBK + i * 32 * kBK + offA[i & 1][ks]);
       } else {
         const int j = f - AP * MI;
-        bf[j] = *(const u32x4_t*)(lds + slot * STAGE + B_OFF + rowB0 * kBK + j * 32 * kBK + offB[j & 1][ks]);
+        if constexpr (NC) {
+          const uint16_t* q = lds + slot * STAGE + B_OFF + offNC[j & 3] + 128 * (j >> 2) + 16 * ks * BN;
+          const u32x2_t lo = lds_read_tr16(q), hi = lds_read_tr16(q + 4 * BN);
+          bf[j] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+        } else {
+          bf[j] = *(const u32x4_t*)(lds + slot * STAGE + B_OFF + rowB0 * kBK + j * 32 * kBK + offB[j & 1][ks]);
+        }
       }
     };
     auto read = [&](int slot, int ks, u32x4_t (&af)[AP * MI], u32x4_t (&bf)[NI]) {
@@ -392,10 +455,11 @@ struct BufPipeEngine {
     // K offset is clamped, re-loading the last stage into the idle slot (no branch).
     const uint32_t kmax = (uint32_t)(nk - 1) * (kBK * 2);
     auto soff_of = [&](int stage) { return min((uint32_t)stage * (kBK * 2), kmax); };
+    auto soffb_of = [&](int stage) { return NC ? (uint32_t)min(stage, nk - 1) * b_kstep : soff_of(stage); };
 #pragma unroll
-    for (int q = 0; q < LPS; ++q) issue_one(lds, 0, 0u, wave, q);
+    for (int q = 0; q < LPS; ++q) issue_one(lds, 0, 0u, 0u, wave, q);
 #pragma unroll
-    for (int q = 0; q < HALF; ++q) issue_one(lds, 1, soff_of(1), wave, q);
+    for (int q = 0; q < HALF; ++q) issue_one(lds, 1, soff_of(1), soffb_of(1), wave, q);
     wait_vmcnt<HALF>();
     exec_barrier();
     u32x4_t fa[2][AP * MI], fb[2][NI];
@@ -409,6 +473,7 @@ struct BufPipeEngine {
     for (int s = 0; s < nk; ++s) {
       const int slot = s & 1;
       const uint32_t soff1 = soff_of(s + 1), soff2 = soff_of(s + 2);
+      const uint32_t soffb1 = soffb_of(s + 1), soffb2 = soffb_of(s + 2);
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const int c = ks & 1;
@@ -429,8 +494,8 @@ struct BufPipeEngine {
           acc[i][j] = Op::mma32(fb[c][j], fa[c][pl * MI + i], acc[i][j]);
           if (m < NRD) read_one(rslot, rks, m, fa[c ^ 1], fb[c ^ 1]);
           if (m < HALF) {
-            if (ks == 0) issue_one(lds, slot ^ 1, soff1, wave, HALF + m);  // 2nd half of s+1
-            else if (ks == 3) issue_one(lds, slot, soff2, wave, m);       // 1st half of s+2
+            if (ks == 0) issue_one(lds, slot ^ 1, soff1, soffb1, wave, HALF + m);  // 2nd half of s+1
+            else if (ks == 3) issue_one(lds, slot, soff2, soffb2, wave, m);       // 1st half of s+2
           }
         }
         __builtin_amdgcn_sched_barrier(0);

@@ -238,6 +238,86 @@ def write_pmc(a) -> None:
     print("\n".join(section[-len(vals):]))
 
 
+# The verifier's "grounding" counter set in its single-pass groups
+# (kore/verifier/pmc.py:91-127 for the set, GROUNDING_PASSES for the passes; every
+# group fits one rocprofv3 hardware pass on gfx950).
+GROUNDING_PASSES = [
+    ["SQ_WAVES", "SQ_BUSY_CYCLES", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU", "SQ_INSTS_VMEM", "SQ_INSTS_SALU",
+     "SQ_WAIT_INST_ANY", "SQ_WAIT_INST_LDS", "GRBM_GUI_ACTIVE", "GRBM_COUNT"],
+    ["SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_VALU_MFMA_MOPS_F16", "SQ_INSTS_VALU_MFMA_MOPS_F32", "SQ_INSTS_LDS",
+     "SQ_ACTIVE_INST_VMEM"],
+    ["TCC_HIT_sum", "TCC_MISS_sum", "TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_32B_sum"],
+    ["TCC_EA0_WRREQ_sum", "TCC_EA0_WRREQ_64B_sum"],
+    ["SQ_INSTS_VALU_MFMA_MOPS_F8", "SQ_INSTS_VALU_MFMA_MOPS_F6F4", "SQ_INSTS_VALU_MFMA_MOPS_XF32"],
+]
+GROUNDING_FILE = os.path.join(PROFILES, "grounding_counters.md")
+
+
+def grounding_counters(dirs: list[str], kernel_substr: str) -> dict[str, float]:
+    """Median per dispatch of every counter found in the pass directories, for the
+    kernels whose name contains ``kernel_substr`` (dimension instances summed)."""
+    out: dict[str, float] = {}
+    for d in dirs:
+        paths = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        if not paths:
+            continue  # a pass that did not run (e.g. counters absent on the device)
+        per: dict[str, dict[str, float]] = {}
+        with open(paths[0]) as f:
+            for r in csv.DictReader(f):
+                if kernel_substr.lower() not in r["Kernel_Name"].lower():
+                    continue
+                c = per.setdefault(r["Counter_Name"], {})
+                c[r["Dispatch_Id"]] = c.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"])
+        for name, vals in per.items():
+            out[name] = statistics.median(vals.values())
+    return out
+
+
+def grounding_derived(c: dict[str, float], simds: int = 1024) -> dict[str, float]:
+    """The verifier's derived quantities (kore/verifier/pmc.py: l2_hit_rate, hbm_bytes
+    with the exact 32B/64B split) plus MFMA busy and MFMA operations (512 per MOPS unit)."""
+    d: dict[str, float] = {}
+    if "SQ_VALU_MFMA_BUSY_CYCLES" in c and c.get("GRBM_GUI_ACTIVE"):
+        d["mfma_busy_pct"] = 100.0 * c["SQ_VALU_MFMA_BUSY_CYCLES"] / (c["GRBM_GUI_ACTIVE"] * simds)
+    if "TCC_HIT_sum" in c and "TCC_MISS_sum" in c and c["TCC_HIT_sum"] + c["TCC_MISS_sum"] > 0:
+        d["l2_hit_rate"] = c["TCC_HIT_sum"] / (c["TCC_HIT_sum"] + c["TCC_MISS_sum"])
+    if "TCC_EA0_RDREQ_sum" in c:
+        rd = c["TCC_EA0_RDREQ_sum"]
+        rd32 = min(c.get("TCC_EA0_RDREQ_32B_sum", 0.0), rd)
+        d["hbm_read_bytes"] = 32.0 * rd32 + 64.0 * (rd - rd32)
+    if "TCC_EA0_WRREQ_sum" in c:
+        wr = c["TCC_EA0_WRREQ_sum"]
+        wr64 = min(c.get("TCC_EA0_WRREQ_64B_sum", 0.0), wr)
+        d["hbm_write_bytes"] = 64.0 * wr64 + 32.0 * (wr - wr64)
+    mops = sum(c.get(k, 0.0) for k in c if k.startswith("SQ_INSTS_VALU_MFMA_MOPS_"))
+    if mops:
+        d["mfma_ops"] = 512.0 * mops
+    return d
+
+
+def write_grounding(a) -> None:
+    c = grounding_counters(a.dirs, a.kernel)
+    if not c:
+        raise SystemExit(f"no counters for {a.kernel!r} in {a.dirs}")
+    d = grounding_derived(c)
+    section = ["Commands (from the repository root, on one MI355X), one per pass:", "", "```", a.cmd, "```", "",
+               f"Kernel: `{a.kernel}`; medians per dispatch.", "", "| counter | value |", "|---|---|"]
+    section += [f"| `{k}` | {v:.6g} |" for k, v in sorted(c.items())]
+    section += ["", "| derived | value |", "|---|---|"]
+    section += [f"| {k} | {v:.6g} |" for k, v in d.items()]
+    if a.note:
+        section += ["", a.note]
+    header = ["# rocprofv3 grounding counters (the KORE verifier's set)", "",
+              "The counter set and its five single-pass groups are the reference verifier's",
+              "`grounding` set (`kore/verifier/pmc.py:91-127`).  Derived: MFMA busy =",
+              "SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs); L2 hit rate = HIT / (HIT + MISS);",
+              "HBM bytes from the EA request counts with the 32B/64B split (read = 32 x RDREQ_32B +",
+              "64 x (RDREQ - RDREQ_32B), write = 64 x WRREQ_64B + 32 x (WRREQ - WRREQ_64B)); MFMA",
+              "operations = 512 x the MOPS counters."]
+    _replace_section(a.out, header, a.workload, section)
+    print("\n".join(section))
+
+
 def read_traffic(workload: str, path: str = TRAFFIC_FILE):
     """Bytes per launch recorded for ``workload`` in the traffic summary, or None."""
     try:
@@ -282,6 +362,14 @@ def main(argv=None) -> int:
     m.add_argument("--out", default=PMC_FILE)
     m.add_argument("--cmd", required=True)
     m.add_argument("--note", default="")
+    sub.add_parser("grounding-passes", help="print the grounding counter groups, one pass per line")
+    gr = sub.add_parser("grounding")
+    gr.add_argument("dirs", nargs="+")
+    gr.add_argument("--workload", required=True)
+    gr.add_argument("--kernel", required=True)
+    gr.add_argument("--out", default=GROUNDING_FILE)
+    gr.add_argument("--cmd", required=True)
+    gr.add_argument("--note", default="")
     a = p.parse_args(argv)
     if a.action == "run":
         _run(a.workload, a.iters, a.warmup)
@@ -291,6 +379,10 @@ def main(argv=None) -> int:
         write_stats(a.dir, a.out, a.cmd, a.title)
     elif a.action == "pmc":
         write_pmc(a)
+    elif a.action == "grounding-passes":
+        print("\n".join(" ".join(g) for g in GROUNDING_PASSES))
+    elif a.action == "grounding":
+        write_grounding(a)
     else:
         write_traffic(a)
     return 0

@@ -233,6 +233,16 @@ def bench_workloads():
             return (lambda: kore_amd.gemm(a, b)), "gemm", {"M": n, "N": n, "K": n}, "bf16"
         return build
 
+    def dense_kn(n):
+        # the gemm_bf16 task's own operands: b is a contiguous [K, N] tensor
+        # (kore/tasks/gemm_bf16/reference.py:28-36)
+        def build(dev):
+            g = _gen(dev, 0)
+            a = (torch.randn((n, n), generator=g, device=dev) / n ** 0.5).to(torch.bfloat16)
+            b = torch.randn((n, n), generator=g, device=dev).to(torch.bfloat16)
+            return (lambda: kore_amd.gemm(a, b)), "gemm", {"M": n, "N": n, "K": n}, "bf16"
+        return build
+
     def fused(act):
         def build(dev):
             a, b, bias = fused_inputs(4096, 4096, 4096, seed=0, device=dev)
@@ -254,7 +264,8 @@ def bench_workloads():
 
     w = {"fp8_blockscale_2048x7168x4096": fp8(2048),
          "bf16_gemm_4096": dense(4096),
-         "bf16_gemm_1024": dense(1024)}
+         "bf16_gemm_1024": dense(1024),
+         "bf16_gemm_4096_kn": dense_kn(4096)}
     for act in ("gelu", "relu", "silu"):
         w[f"fp16_gemm_bias_{act}_4096"] = fused(act)
     w["bf16_batched_64x1024x1024x128"] = batched

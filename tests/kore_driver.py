@@ -140,7 +140,7 @@ def _tasks() -> dict[str, Task]:
             lambda s, seed, dev: tuple(x.to(dev) for x in W.moe_inputs(s["M"], s["E"], s["topk"], s["D"], s["I"],
                                                                         seed=seed, wscale=0.05)),
             lambda a: om.moe_ref(*a),
-            lambda a: om.moe_ref(*a),  # the torch per-expert loop on the GPU (AITER absent)
+            lambda a: _moe_torch(*a),  # a torch per-expert loop on the GPU (AITER absent)
             atol=3e-2, rtol=3e-2, snr=25.0),
         "gemm_backward_bf16": Task(
             "gemm_backward", {"M": 8192, "N": 4096, "K": 4096},
@@ -153,6 +153,24 @@ def _tasks() -> dict[str, Task]:
         for dt, name in ((torch.bfloat16, "bf16"), (torch.float16, "fp16"), (torch.float32, "fp32")):
             t[f"gen_{op}_{name}"] = _fusion_task(op, dt)
     return t
+
+
+def _moe_torch(hidden, w1, w2, topk_weight, topk_ids):
+    """Vendor-path bar for the MoE task: per expert, two hipBLASLt GEMMs in the input
+    dtype with SiLU-and-mul in fp32 between them, weighted scatter-add into the output."""
+    I = w2.shape[2]
+    out = torch.zeros(hidden.shape, dtype=torch.float32, device=hidden.device)
+    ids = topk_ids.long()
+    for e in range(w1.shape[0]):
+        mask = ids == e
+        idx = mask.any(dim=1).nonzero(as_tuple=True)[0]
+        if idx.numel() == 0:
+            continue
+        gu = torch.matmul(hidden[idx], w1[e].t()).float()
+        h = (torch.nn.functional.silu(gu[:, :I]) * gu[:, I:]).to(hidden.dtype)
+        y = torch.matmul(h, w2[e].t()).float()
+        out.index_add_(0, idx, y * (topk_weight.float() * mask.float()).sum(dim=1)[idx, None])
+    return out.to(hidden.dtype)
 
 
 def _dequant_matmul(xq, wq, xs, ws):

@@ -50,3 +50,23 @@ def test_driver_bench_mode(gpu):
                 "--iters", "9"])
     v = kd.parse(out, 25.0)
     assert v["passed"] and v["median_ms"] is not None and out.count("wall_ms:") == 9, out
+
+
+@pytest.mark.parametrize("task,shape", [("fused_moe_silu_bf16", "M=64,E=8,topk=2,D=256,I=512"),
+                                        ("gemm_fp8_a8w8_blockscale", "M=128,N=256,K=512"),
+                                        ("gemm_backward_bf16", "M=256,N=128,K=256")])
+def test_driver_reference_impls(gpu, task, shape):
+    """The vendor-path implementations timed against the candidates compute the task:
+    each agrees with the CPU oracle under the task's gate."""
+    from oracle.compare import compare_outputs
+
+    t = kd._tasks()[task]
+    sh = kd.parse_shape(shape, t.default)
+    args = t.inputs(sh, 3, "cuda")
+    got = kd._as_tuple(t.reference(args))
+    want = kd._as_tuple(t.oracle(tuple(x.cpu() for x in args)))
+    for o, r in zip(got, want):
+        snr, _, close = compare_outputs(o, r, atol=t.atol, rtol=t.rtol)
+        assert close and snr >= t.snr, (task, snr)
+    out = _run([task, "--bench-both", "--shape", shape, "--repeat", "1", "--warmup", "2", "--iters", "8"])
+    assert kd.parse(out, t.snr)["passed"], out

@@ -69,6 +69,31 @@ def test_gemm_reference_task_shapes(gpu, M, N, K):
     verdict(out, matmul_ref(a, b), "gemm", "bf16", f"{M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("M,N,K,dtype,op", [(4096, 4096, 4096, torch.bfloat16, "gemm_bias_gelu"),
+                                             (3000, 4104, 1024, torch.float16, "gemm_bias_silu"),
+                                             (2048, 7168, 4096, torch.bfloat16, "gemm"),
+                                             (3840, 3336, 1024, torch.float16, "gemm_relu")])
+@pytest.mark.parametrize("strided", [False, True])
+def test_gemm_nc_buffer_engine(gpu, M, N, K, dtype, op, strided):
+    """N-contiguous B (the tasks' natural [K,N] layout) at >= 192 tiles of 256x256 runs the
+    buffer-load engine with LDS transpose reads: ragged M and N (N % 256 != 0), fused
+    epilogues, and a B view whose K-rows are wider than N (row stride N + 128)."""
+    has_bias, act = kore_amd.GEMM_FUSION_OPS.get(op, (False, "none"))
+    g = torch.Generator().manual_seed(M + N + K)
+    sc = 1.0 / K ** 0.5
+    a = (torch.randn((M, K), generator=g) * sc).to(dtype)
+    bfull = (torch.randn((K, N + 128), generator=g) * sc).to(dtype)
+    b = bfull[:, 64:64 + N] if strided else bfull[:, :N].contiguous()
+    bias = torch.randn((N,), generator=g).to(dtype) if has_bias else None
+    bd = bfull.to(gpu)[:, 64:64 + N] if strided else b.to(gpu)
+    assert bd.stride(1) == 1 and bd.stride(0) == (N + 128 if strided else N)
+    out = kore_amd.gemm_fused(a.to(gpu), bd, bias.to(gpu) if has_bias else None, act)
+    ref = gemm_fusion_ref(a, b, bias, act)
+    dt = "bf16" if dtype == torch.bfloat16 else "fp16"
+    verdict(out, ref, "gemm_fusion", dt, f"nc {op} {M}x{N}x{K} strided={strided}")
+    pair_only(out, ref, dt, f"nc {op} {M}x{N}x{K}")
+
+
 def test_gemm_metric_4096_bt(gpu):
     a, b = W.dense_inputs(4096, 4096, 4096, seed=0)
     out = kore_amd.gemm(a.to(gpu), b.to(gpu))

@@ -89,3 +89,21 @@ def test_pmc_summary_sections(tmp_path):
     assert text.count("## w1") == 1 and text.count("## w2") == 1 and "cmd3" in text and "cmd1" not in text
     row = [ln for ln in text.splitlines() if ln.startswith("| `gemm_fp8_pipe_kernel")][0]
     assert "| 44.0 |" in row and "0.250" in row  # medians; the non-kore kernel is ignored
+
+
+def test_grounding_passes_and_derived():
+    """The grounding groups stay within one rocprofv3 pass each (<= 8 SQ, <= 4 TCC,
+    <= 2 GRBM counters) and the derived values follow the verifier's formulas."""
+    from kore_amd import profiling as P
+
+    for g in P.GROUNDING_PASSES:
+        assert sum(c.startswith("SQ_") for c in g) <= 8
+        assert sum(c.startswith("TCC_") for c in g) <= 4
+        assert sum(c.startswith("GRBM_") for c in g) <= 2
+    d = P.grounding_derived({"TCC_HIT_sum": 3.0, "TCC_MISS_sum": 1.0, "TCC_EA0_RDREQ_sum": 10.0,
+                             "TCC_EA0_RDREQ_32B_sum": 4.0, "TCC_EA0_WRREQ_sum": 5.0, "TCC_EA0_WRREQ_64B_sum": 5.0,
+                             "SQ_VALU_MFMA_BUSY_CYCLES": 512.0, "GRBM_GUI_ACTIVE": 1.0,
+                             "SQ_INSTS_VALU_MFMA_MOPS_BF16": 2.0})
+    assert d["l2_hit_rate"] == 0.75
+    assert d["hbm_read_bytes"] == 32 * 4 + 64 * 6 and d["hbm_write_bytes"] == 64 * 5
+    assert d["mfma_busy_pct"] == 50.0 and d["mfma_ops"] == 1024.0
