@@ -158,23 +158,15 @@ __global__ void __launch_bounds__(kEngineThreads)
 }
 
 
-// Buffer-load pipelined variant for K-contiguous A, K % 64 == 0 and either B layout:
-// K-contiguous B (the A.B^T / A.W^T layouts) or N-contiguous B (natural [K, N], N % 8 ==
-// 0), whose fragments come out of LDS through transpose reads.
-template <typename T, int BM, int BN, int BL>
-__global__ void __launch_bounds__(256)
-    gemm_buf_kernel(const TileParams p) {
-  using E = BufPipeEngine<T, BM, BN, 2, 2, 1, BL>;
-  constexpr int MI = E::MI, NI = E::NI;
-  __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / E::WN, wn = wave % E::WN;
-  int batch, m0, n0;
-  tile_coords(p, BM, BN, batch, m0, n0);
+// Buffer resources and per-lane byte offsets of the direct-to-LDS engines.  Rows of A
+// and of B^T past the tile's last valid row re-read that row; N-contiguous B is read
+// as K-rows of the n0 column block whose chunks past N (N % 8 == 0) re-read the last
+// chunk.  Either way the extra values only feed outputs that are never stored.
+template <typename E, int BM, int BN, int BL>
+__device__ __forceinline__ void setup_operands(E& eng, const TileParams& p, int batch, int m0, int n0, int wave,
+                                               int lane) {
   const uint16_t* A = p.a + batch * p.sa + (int64_t)m0 * p.lda;
-  uint16_t* C = p.c + batch * p.sc;
   const int rows_a = min(BM, p.M - m0), rows_b = min(BN, p.N - n0);
-  E eng;
   eng.ra = make_rsrc(A, (uint32_t)(((int64_t)(rows_a - 1) * p.lda + p.K) * 2));
 #pragma unroll
   for (int j = 0; j < E::AJ; ++j) {
@@ -190,8 +182,6 @@ __global__ void __launch_bounds__(256)
       eng.b_voff[j] = (uint32_t)(((int64_t)min(r, rows_b - 1) * p.ldb + 8 * E::chunk(r, lane)) * 2);
     }
   } else {
-    // K-rows of the n0 column block; chunks past N (N % 8 == 0) re-read the last chunk,
-    // which only feeds output columns that are never stored.
     const uint16_t* B = p.b + batch * p.sb + n0;
     eng.rb = make_rsrc(B, (uint32_t)(((int64_t)(p.K - 1) * p.ldb + rows_b) * 2));
     eng.b_kstep = (uint32_t)(kBK * p.ldb * 2);
@@ -201,10 +191,45 @@ __global__ void __launch_bounds__(256)
       eng.b_voff[j] = (uint32_t)(((int64_t)kr * p.ldb + min(8 * E::nc_chunk(kr, lane), rows_b - 8)) * 2);
     }
   }
+}
+
+// Buffer-load pipelined variant for K-contiguous A, K % 64 == 0 and either B layout:
+// K-contiguous B (the A.B^T / A.W^T layouts) or N-contiguous B (natural [K, N], N % 8 ==
+// 0), whose fragments come out of LDS through transpose reads.
+template <typename T, int BM, int BN, int BL>
+__global__ void __launch_bounds__(256)
+    gemm_buf_kernel(const TileParams p) {
+  using E = BufPipeEngine<T, BM, BN, 2, 2, 1, BL>;
+  constexpr int MI = E::MI, NI = E::NI;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / E::WN, wn = wave % E::WN;
+  int batch, m0, n0;
+  tile_coords(p, BM, BN, batch, m0, n0);
+  E eng;
+  setup_operands<E, BM, BN, BL>(eng, p, batch, m0, n0, wave, lane);
   f32x16_t acc[MI][NI];
   E::zero(acc);
   eng.mainloop(lds, p.K, acc);
-  dense_epilogue<T, MI, NI, E::WROWS, E::WCOLS>(acc, lds, p, m0, n0, wm, wn, wave, lane, C);
+  dense_epilogue<T, MI, NI, E::WROWS, E::WCOLS>(acc, lds, p, m0, n0, wm, wn, wave, lane, p.c + batch * p.sc);
+}
+
+// Mid-size problems (a few hundred tiles, long K) on the deep ring engine: NSLOT - 1
+// K stages in flight per CU instead of one or two.  Either B layout, K % 64 == 0.
+template <typename T, int BM, int BN, int WM, int WN, int NSLOT, int BL>
+__global__ void __launch_bounds__(256) gemm_deep_kernel(const TileParams p) {
+  using E = RingEngine<T, BM, BN, WM, WN, NSLOT, BL>;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int batch, m0, n0;
+  tile_coords(p, BM, BN, batch, m0, n0);
+  E eng;
+  setup_operands<E, BM, BN, BL>(eng, p, batch, m0, n0, wave, lane);
+  f32x16_t acc[E::MI][E::NI];
+  E::zero(acc);
+  eng.mainloop(lds, p.K, acc);
+  dense_epilogue<T, E::MI, E::NI, E::WROWS, E::WCOLS>(acc, lds, p, m0, n0, wave / WN, wave % WN, wave, lane,
+                                                      p.c + batch * p.sc);
 }
 
 // ---------------------------------------------------------------------------------
@@ -710,6 +735,36 @@ int launch_buf(const GemmDesc& d, hipStream_t stream) {
   return check_launch("gemm_buf_kernel");
 }
 
+template <typename T, int BM, int BN, int WM, int WN, int NSLOT, int BL>
+int launch_deep(const GemmDesc& d, hipStream_t stream) {
+  TileParams p;
+  p.a = (const uint16_t*)d.a;
+  p.b = (const uint16_t*)d.b;
+  p.bias = (const uint16_t*)d.bias;
+  p.c = (uint16_t*)d.c;
+  p.M = (int)d.M;
+  p.N = (int)d.N;
+  p.K = (int)d.K;
+  p.lda = d.sam;
+  p.ldb = (BL == B_KC) ? d.sbn : d.sbk;
+  p.ldc = d.scm;
+  p.sa = d.sa;
+  p.sb = d.sb;
+  p.sc = d.sc;
+  p.tiles_m = (int)((d.M + BM - 1) / BM);
+  p.tiles_n = (int)((d.N + BN - 1) / BN);
+  p.tiles_per_batch = p.tiles_m * p.tiles_n;
+  p.batch = (int)d.batch;
+  p.act = d.act;
+  p.vec_store = (d.scm % 8 == 0) && aligned16(d.c) && (d.sc % 8 == 0);
+  p.bias_vec = d.bias != nullptr && ((uintptr_t)d.bias & 7u) == 0;
+  const int64_t blocks = (int64_t)p.tiles_per_batch * d.batch;
+  if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "gemm: grid too large");
+  hipLaunchKernelGGL((gemm_deep_kernel<T, BM, BN, WM, WN, NSLOT, BL>), dim3((unsigned)blocks), dim3(256), 0, stream,
+                     p);
+  return check_launch("gemm_deep_kernel");
+}
+
 // Persistent short-K launch: one 128 KiB-LDS workgroup per CU, at most one per tile.
 template <typename T, int BL>
 int launch_shortk(const GemmDesc& d, hipStream_t stream) {
@@ -828,11 +883,20 @@ int dispatch_typed(const GemmDesc& d, hipStream_t stream) {
     const bool short_k = d.K <= 256;
     const bool small = mid_tiles < 128;
     if (b_kc && big && buf_ok && !short_k) return launch_buf<T, 256, 256, B_KC>(d, stream);
-    // N-contiguous B on the same engine: B bytes from the tile's first column through
-    // the last K-row must fit the 32-bit buffer offsets.
+    // N-contiguous B on the direct-to-LDS engines: B bytes from the tile's first column
+    // through the last K-row must fit the 32-bit buffer offsets.
     const bool buf_nc_ok = d.K % 64 == 0 && d.sam * 2 * 256 + d.K * 2 < (1ll << 31) &&
                            d.sbk * 2 * d.K + d.N * 2 < (1ll << 31);
     if (!b_kc && b_nc && big && buf_nc_ok && !short_k) return launch_buf<T, 256, 256, B_NC>(d, stream);
+    // Mid-size with a long K: the deep ring, 128x128 tiles when they fill the chip,
+    // else 64x128 when those do.
+    const bool deep_ok = (b_kc ? buf_ok : buf_nc_ok) && d.K >= 256;
+    const int64_t fill = (int64_t)device_cus() * 7 / 8;
+    const int64_t half_tiles = ((d.M + 63) / 64) * ((d.N + 127) / 128) * d.batch;
+    if (deep_ok && !big && mid_tiles >= fill)
+      return b_kc ? launch_deep<T, 128, 128, 2, 2, 4, B_KC>(d, stream) : launch_deep<T, 128, 128, 2, 2, 4, B_NC>(d, stream);
+    if (deep_ok && !big && half_tiles >= fill)
+      return b_kc ? launch_deep<T, 64, 128, 2, 2, 6, B_KC>(d, stream) : launch_deep<T, 64, 128, 2, 2, 6, B_NC>(d, stream);
     // K of one or two 64-wide steps, no epilogue, enough 128x128 tiles to give every
     // CU several: the persistent short-K kernel (16-byte buffer stores need N % 8 == 0
     // and 16-byte aligned C rows; per-tile byte offsets must stay below 2^31).
@@ -843,6 +907,7 @@ int dispatch_typed(const GemmDesc& d, hipStream_t stream) {
     if (shortk) return b_kc ? launch_shortk<T, B_KC>(d, stream) : launch_shortk<T, B_NC>(d, stream);
     // few tiles and a long K: the latency-bound case, on the deep direct-to-LDS ring
     if (b_kc && small && buf_ok && d.K >= 512) return launch_ring<T>(d, stream);
+    if (!b_kc && small && buf_nc_ok && d.K >= 512) return launch_deep<T, 32, 128, 1, 4, 7, B_NC>(d, stream);
     if (b_kc) {
       if (big && !short_k) return launch_tile<T, B_KC, 256, 256>(d, stream);
       return small ? launch_tile<T, B_KC, 64, 64>(d, stream) : launch_tile<T, B_KC, 128, 128>(d, stream);

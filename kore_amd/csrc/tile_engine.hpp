@@ -324,6 +324,27 @@ __device__ __forceinline__ void buf_lds16_asm(__amdgpu_buffer_rsrc_t r, uint32_t
                :: "v"(voff), "s"(r), "s"(soff), "s"(m0) : "memory");
 }
 
+// N-contiguous B stage layout shared by the direct-to-LDS engines: 64 K-rows of BN
+// elements (BN = 128 or 256), one direct load instruction (512 elements) fills
+// 512 / BN whole K-rows, and 16-byte chunk c of K-row k lives at chunk c ^ nc_x(k & 3)
+// with nc_x = {0, 4, 10, 14}: the four K-rows one transpose read touches (32 bytes
+// each) then sit in four distinct 32-byte bank slots of a 128-byte window, and with
+// the next 16 lanes' chunk pair (same K-rows) in eight distinct slots of 256 bytes.
+__device__ __forceinline__ int nc_x(int r) { return ((r & 1) * 4) ^ ((r >> 1) * 10); }
+
+// Element offsets (within a stage's B region, sub-step 0, low half) of the transpose
+// reads for the NI 32-column fragments of a wave whose columns start at col0: lane
+// (16-lane group g, index c) reads K-rows 8 (lane / 32) + c / 4 (+ 4 for the high
+// half, + 16 per sub-step), columns col0 + 32 j + 16 (g & 1) + 4 (c % 4) .. + 3.
+template <int BN, int NI>
+__device__ __forceinline__ void nc_frag_offsets(int lane, int col0, int (&off)[NI]) {
+  const int c = lane & 15, x = nc_x(c >> 2), hh = lane >> 5;
+  const int low = 2 * ((lane >> 4) & 1) + ((c & 3) >> 1);
+#pragma unroll
+  for (int j = 0; j < NI; ++j)
+    off[j] = (8 * hh + (c >> 2)) * BN + (((col0 / 8 + 4 * j + low) ^ x) << 3) + 4 * (c & 1);
+}
+
 template <typename T, int BM, int BN, int WM_ = 2, int WN_ = 2, int AP = 1, int BL = B_KC>
 struct BufPipeEngine {
   static constexpr int WM = WM_, WN = WN_, NW = WM * WN;
@@ -346,16 +367,11 @@ struct BufPipeEngine {
   // Logical 16-byte chunk lane `lane` fetches for `row` (element offset 8 * chunk).
   static __device__ __forceinline__ int chunk(int row, int lane) { return (lane & 7) ^ swz8(row); }
 
-  // N-contiguous B (BL == B_NC): a stage holds 64 K-rows of BN elements, so one direct
-  // load instruction (512 elements) fills NCR whole K-rows.  16-byte chunk c of K-row k
-  // lives at chunk c ^ nc_x(k & 3) with nc_x = {0, 4, 10, 14}: the four K-rows one
-  // transpose read touches (32 bytes each, 2 chunks) then sit in four distinct 32-byte
-  // bank slots of a 128-byte window, and with the next 16 lanes' chunk pair (same
-  // K-rows) in eight distinct slots of a 256-byte window.
+  // N-contiguous B (BL == B_NC): K-rows of BN elements, NCR per direct load
+  // instruction, chunk swizzle nc_x.
   static constexpr bool NC = BL == B_NC;
   static constexpr int NCR = 512 / BN, NCH = BN / 8;
   static_assert(!NC || BN == 128 || BN == 256, "N-contiguous B tile width");
-  static __device__ __forceinline__ int nc_x(int r) { return ((r & 1) * 4) ^ ((r >> 1) * 10); }
   static __device__ __forceinline__ int nc_krow(int wave, int lane, int j) { return (wave + NW * j) * NCR + lane / NCH; }
   static __device__ __forceinline__ int nc_chunk(int krow, int lane) { return (lane % NCH) ^ nc_x(krow & 3); }
 
@@ -411,18 +427,8 @@ struct BufPipeEngine {
       }
     }
     const int rowA0 = wm * WROWS, rowB0 = wn * WCOLS;
-    // NC: lane (16-lane group g, index c) reads K-rows 16 ks + 8 (lane / 32) + c / 4
-    // (+ 4 for the upper half of the fragment), columns rowB0 + 32 j + 16 (g & 1) +
-    // 4 (c % 4); the chunk swizzle touches chunk bits 0-3 only, so the per-lane part
-    // depends on j % 4 (offNC) and the rest is a constant offset.
-    constexpr int NCJ = NI < 4 ? NI : 4;
-    int offNC[NCJ];
-    if constexpr (NC) {
-      const int c = lane & 15, x = nc_x(c >> 2), low = 2 * ((lane >> 4) & 1) + ((c & 3) >> 1);
-#pragma unroll
-      for (int j = 0; j < NCJ; ++j)
-        offNC[j] = (8 * hh + (c >> 2)) * BN + rowB0 + (((4 * j + low) ^ x) << 3) + 4 * (c & 1);
-    }
+    int offNC[NI];
+    if constexpr (NC) nc_frag_offsets<BN, NI>(lane, rowB0, offNC);
     // Fragment f of a sub-step: f < AP*MI -> A plane f/MI block f%MI, else B block.
     auto read_one = [&](int slot, int ks, int f, u32x4_t (&af)[AP * MI], u32x4_t (&bf)[NI]) {
       if (f < AP * MI) {
@@ -431,7 +437,7 @@ struct BufPipeEngine {
       } else {
         const int j = f - AP * MI;
         if constexpr (NC) {
-          const uint16_t* q = lds + slot * STAGE + B_OFF + offNC[j & 3] + 128 * (j >> 2) + 16 * ks * BN;
+          const uint16_t* q = lds + slot * STAGE + B_OFF + offNC[j] + 16 * ks * BN;
           const u32x2_t lo = lds_read_tr16(q), hi = lds_read_tr16(q + 4 * BN);
           bf[j] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
         } else {
@@ -602,6 +608,134 @@ struct SkinnyRingEngine {
         for (int pl = 0; pl < AP; ++pl)
 #pragma unroll
           for (int j = 0; j < NI; ++j) acc[0][j] = Op::mma32(bf[j], af[pl], acc[0][j]);
+      }
+      slot = slot + 1 == NSLOT ? 0 : slot + 1;
+    }
+    wait_vmcnt<0>();  // the clamped trailing loads must land before LDS is reused
+    __syncthreads();
+  }
+};
+
+}  // namespace kore
+
+namespace kore {
+
+// ---------------------------------------------------------------------------------
+// Deep ring engine (mid-size GEMMs: a few hundred tiles and a long K).
+//
+// A mid-size tile streams 1-2 MiB of operands through its CU; with two 64-wide K
+// stages in flight the CU waits most of a memory round trip per stage.  Here an
+// NSLOT-deep ring of stages is filled by direct-to-LDS buffer loads NSLOT - 1 stages
+// ahead of the MFMAs (~100 KiB in flight per CU).  Four waves in a WM x WN grid.
+// Per K step: wait for the own loads of the stage, one barrier (all loads of the
+// stage landed, every wave finished the previous stage, whose slot is refilled
+// next), issue the stage NSLOT - 1 ahead, then 4 sub-steps of MFMAs.  Past the last
+// stage the K offset is clamped (the last stage is re-loaded into a slot nobody
+// reads), so every wave issues the same loads and the vmcnt arithmetic is uniform.
+// A and K-contiguous B use 128-byte rows with the swz8 chunk swizzle; N-contiguous B
+// uses the nc_x layout and LDS transpose reads (loads then go out as inline asm).
+// ---------------------------------------------------------------------------------
+template <typename T, int BM, int BN, int WM, int WN, int NSLOT, int BL>
+struct RingEngine {
+  static constexpr int NW = 4;
+  static_assert(WM * WN == NW, "4 waves");
+  static constexpr int WROWS = BM / WM, WCOLS = BN / WN;
+  static constexpr int MI = WROWS / 32, NI = WCOLS / 32;
+  static_assert(WROWS % 32 == 0 && WCOLS % 32 == 0 && MI >= 1 && NI >= 1, "wave tile");
+  static constexpr int A_ELEMS = BM * kBK, B_ELEMS = BN * kBK;
+  static constexpr int B_OFF = A_ELEMS, STAGE = A_ELEMS + B_ELEMS, LDS_ELEMS = NSLOT * STAGE;
+  static constexpr int AJ = BM / 32, BJ = BN / 32;  // 512-element loads per wave per stage
+  static_assert(AJ * 32 == BM && BJ * 32 == BN, "wave loads must cover the tile");
+  static constexpr int LPS = AJ + BJ;
+  static_assert(NSLOT >= 2 && (NSLOT - 2) * LPS <= 63, "vmcnt range");
+  static constexpr bool NC = BL == B_NC;
+  static constexpr int NCR = 512 / BN, NCH = BN / 8;
+  static_assert(!NC || BN == 128 || BN == 256, "N-contiguous B tile width");
+
+  static __device__ __forceinline__ int a_row(int wave, int lane, int j) { return (wave + NW * j) * 8 + (lane >> 3); }
+  static __device__ __forceinline__ int b_row(int wave, int lane, int j) { return (wave + NW * j) * 8 + (lane >> 3); }
+  static __device__ __forceinline__ int chunk(int row, int lane) { return (lane & 7) ^ swz8(row); }
+  static __device__ __forceinline__ int nc_krow(int wave, int lane, int j) { return (wave + NW * j) * NCR + lane / NCH; }
+  static __device__ __forceinline__ int nc_chunk(int krow, int lane) { return (lane % NCH) ^ nc_x(krow & 3); }
+
+  __amdgpu_buffer_rsrc_t ra, rb;
+  uint32_t a_voff[AJ], b_voff[BJ];
+  uint32_t b_kstep;  // NC: bytes of B between consecutive 64-row K stages
+
+  __device__ __forceinline__ void issue(uint16_t* lds, int slot, uint32_t soff, uint32_t soffb, int wave) const {
+    uint16_t* st = lds + slot * STAGE;
+    auto ld = [&](__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t so, uint16_t* dst) {
+      if constexpr (NC) buf_lds16_asm(r, voff, so, dst);
+      else buf_lds16(r, voff, so, dst);
+    };
+#pragma unroll
+    for (int j = 0; j < AJ; ++j) ld(ra, a_voff[j], soff, st + (wave + NW * j) * 8 * kBK);
+#pragma unroll
+    for (int j = 0; j < BJ; ++j) ld(rb, b_voff[j], soffb, st + B_OFF + (wave + NW * j) * 8 * kBK);
+  }
+
+  static __device__ __forceinline__ void zero(f32x16_t (&acc)[MI][NI]) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  }
+
+  // K must be a positive multiple of 64.
+  __device__ __forceinline__ void mainloop(uint16_t* lds, int K, f32x16_t (&acc)[MI][NI]) {
+    using Op = MfmaOp<T>;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    const int lr = lane & 31, hh = lane >> 5;
+    const int rowA0 = wm * WROWS, rowB0 = wn * WCOLS;
+    // fragment row R + lr (R % 32 == 0): swz8(R + lr) = (lr & 7) ^ (lr >> 3) ^ (4 * ((R / 32) & 1))
+    int offA[2][4], offB[2][4], offNC[NI];
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+      const int qa = (wm * MI + par) & 1, qb = (wn * NI + par) & 1;
+      const int swa = ((lr & 7) ^ (lr >> 3) ^ (4 * qa)) & 7;
+      const int swb = ((lr & 7) ^ (lr >> 3) ^ (4 * qb)) & 7;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        offA[par][ks] = lr * kBK + (((2 * ks + hh) ^ swa) << 3);
+        offB[par][ks] = lr * kBK + (((2 * ks + hh) ^ swb) << 3);
+      }
+    }
+    if constexpr (NC) nc_frag_offsets<BN, NI>(lane, rowB0, offNC);
+    const int nk = K / kBK;
+    auto soff_of = [&](int stage) { return (uint32_t)min(stage, nk - 1) * (kBK * 2); };
+    auto soffb_of = [&](int stage) { return NC ? (uint32_t)min(stage, nk - 1) * b_kstep : soff_of(stage); };
+#pragma unroll
+    for (int s = 0; s < NSLOT - 1; ++s) issue(lds, s, soff_of(s), soffb_of(s), wave);
+    int slot = 0;
+    for (int s = 0; s < nk; ++s) {
+      wait_vmcnt<(NSLOT - 2) * LPS>();
+      exec_barrier();
+      const int nslot = slot == 0 ? NSLOT - 1 : slot - 1;  // slot of stage s - 1
+      issue(lds, nslot, soff_of(s + NSLOT - 1), soffb_of(s + NSLOT - 1), wave);
+      const uint16_t* sA = lds + slot * STAGE + rowA0 * kBK;
+      const uint16_t* sB = lds + slot * STAGE + B_OFF;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        u32x4_t af[MI], bf[NI];
+#pragma unroll
+        for (int i = 0; i < MI; ++i) af[i] = *(const u32x4_t*)(sA + i * 32 * kBK + offA[i & 1][ks]);
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+          if constexpr (NC) {
+            const uint16_t* q = sB + offNC[j] + 16 * ks * BN;
+            const u32x2_t lo = lds_read_tr16(q), hi = lds_read_tr16(q + 4 * BN);
+            bf[j] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+          } else {
+            bf[j] = *(const u32x4_t*)(sB + rowB0 * kBK + j * 32 * kBK + offB[j & 1][ks]);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < NI; ++j) acc[i][j] = Op::mma32(bf[j], af[i], acc[i][j]);
       }
       slot = slot + 1 == NSLOT ? 0 : slot + 1;
     }

@@ -94,6 +94,49 @@ def test_gemm_nc_buffer_engine(gpu, M, N, K, dtype, op, strided):
     pair_only(out, ref, dt, f"nc {op} {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("M,N,K,dtype,op", [(2048, 2048, 2048, torch.bfloat16, "gemm"),
+                                             (1024, 4096, 4096, torch.float16, "gemm_bias_gelu"),
+                                             (256, 14336, 4096, torch.bfloat16, "gemm_bias_silu"),
+                                             (512, 4096, 4096, torch.bfloat16, "gemm_bias_gelu"),
+                                             (1024, 2048, 2048, torch.float16, "gemm_sigmoid"),
+                                             (500, 4000, 1024, torch.bfloat16, "gemm_bias"),
+                                             (1000, 1000, 1024, torch.bfloat16, "gemm_tanh"),
+                                             (1, 4096, 4096, torch.bfloat16, "gemm")])
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+def test_gemm_deep_ring(gpu, M, N, K, dtype, op, layout):
+    """Mid-size and small problems with a long K on the deep-ring kernel (128x128 tiles
+    when they fill the chip, else 64x128; 32x128 for small N-contiguous problems), both
+    B layouts ([K,N] and the W.t() view), ragged M and N, fused epilogues."""
+    has_bias, act = kore_amd.GEMM_FUSION_OPS.get(op, (False, "none"))
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    sc = 1.0 / K ** 0.5
+    a = (torch.randn((M, K), generator=g) * sc).to(dtype)
+    if layout == "kn":
+        b = (torch.randn((K, N), generator=g) * sc).to(dtype)
+        bd = b.to(gpu)
+    else:
+        w = (torch.randn((N, K), generator=g) * sc).to(dtype)
+        b, bd = w.t(), w.to(gpu).t()
+    bias = torch.randn((N,), generator=g).to(dtype) if has_bias else None
+    out = kore_amd.gemm_fused(a.to(gpu), bd, bias.to(gpu) if has_bias else None, act)
+    ref = gemm_fusion_ref(a, b, bias, act)
+    dt = "bf16" if dtype == torch.bfloat16 else "fp16"
+    verdict(out, ref, "gemm_fusion", dt, f"deep {op} {M}x{N}x{K} {layout}")
+    pair_only(out, ref, dt, f"deep {op} {M}x{N}x{K} {layout}")
+
+
+def test_batched_deep_ring(gpu):
+    """A batched problem with >= 224 tiles of 128x128 and K = 512 runs the deep ring per
+    batch (batch strides on A, B and C)."""
+    from oracle.gemm import batched_gemm_ref
+
+    g = torch.Generator().manual_seed(5)
+    a = (torch.randn((16, 512, 512), generator=g) / 512 ** 0.5).bfloat16()
+    b = (torch.randn((16, 512, 512), generator=g) / 512 ** 0.5).bfloat16()
+    out = kore_amd.batched_gemm(a.to(gpu), b.to(gpu))
+    verdict(out, batched_gemm_ref(a, b), "gemm", "bf16", "batched deep 16x512x512x512")
+
+
 def test_gemm_metric_4096_bt(gpu):
     a, b = W.dense_inputs(4096, 4096, 4096, seed=0)
     out = kore_amd.gemm(a.to(gpu), b.to(gpu))
