@@ -273,12 +273,22 @@ def grounding_counters(dirs: list[str], kernel_substr: str) -> dict[str, float]:
     return out
 
 
-def grounding_derived(c: dict[str, float], simds: int = 1024) -> dict[str, float]:
-    """The verifier's derived quantities (kore/verifier/pmc.py: l2_hit_rate, hbm_bytes
-    with the exact 32B/64B split) plus MFMA busy and MFMA operations (512 per MOPS unit)."""
+def grounding_derived(c: dict[str, float], xcds: int = 8, simds: int = 1024) -> dict[str, float]:
+    """Derived quantities of the grounding set.
+
+    The verifier's own formulas (kore/verifier/pmc.py): ``l2_hit_rate`` = HIT / (HIT +
+    MISS); HBM bytes with the exact 32B/64B split; ``mfma_busy_fraction`` =
+    min(1, SQ_VALU_MFMA_BUSY_CYCLES / GRBM_GUI_ACTIVE) and ``mfma_ops`` = the sum of
+    the MFMA counters (pmc.py:479-495).  On MI355X SQ_VALU_MFMA_BUSY_CYCLES sums busy
+    cycles over all 1024 SIMDs and GRBM_GUI_ACTIVE sums the 8 XCDs' active cycles, so
+    the verifier's fraction saturates at 1; ``mfma_busy_pct`` normalises per SIMD-cycle
+    (busy / (GRBM_GUI_ACTIVE / 8 x 1024)).  ``mfma_flops`` = 512 x the MOPS counters.
+    """
     d: dict[str, float] = {}
-    if "SQ_VALU_MFMA_BUSY_CYCLES" in c and c.get("GRBM_GUI_ACTIVE"):
-        d["mfma_busy_pct"] = 100.0 * c["SQ_VALU_MFMA_BUSY_CYCLES"] / (c["GRBM_GUI_ACTIVE"] * simds)
+    busy, active = c.get("SQ_VALU_MFMA_BUSY_CYCLES"), c.get("GRBM_GUI_ACTIVE")
+    if busy is not None and active:
+        d["mfma_busy_fraction"] = max(0.0, min(1.0, busy / active))
+        d["mfma_busy_pct"] = 100.0 * busy / (active / xcds * simds)
     if "TCC_HIT_sum" in c and "TCC_MISS_sum" in c and c["TCC_HIT_sum"] + c["TCC_MISS_sum"] > 0:
         d["l2_hit_rate"] = c["TCC_HIT_sum"] / (c["TCC_HIT_sum"] + c["TCC_MISS_sum"])
     if "TCC_EA0_RDREQ_sum" in c:
@@ -289,9 +299,12 @@ def grounding_derived(c: dict[str, float], simds: int = 1024) -> dict[str, float
         wr = c["TCC_EA0_WRREQ_sum"]
         wr64 = min(c.get("TCC_EA0_WRREQ_64B_sum", 0.0), wr)
         d["hbm_write_bytes"] = 64.0 * wr64 + 32.0 * (wr - wr64)
-    mops = sum(c.get(k, 0.0) for k in c if k.startswith("SQ_INSTS_VALU_MFMA_MOPS_"))
+    mf = [k for k in c if "MFMA" in k.upper()]
+    if mf:
+        d["mfma_ops"] = sum(c[k] for k in mf)
+    mops = sum(c[k] for k in c if k.startswith("SQ_INSTS_VALU_MFMA_MOPS_"))
     if mops:
-        d["mfma_ops"] = 512.0 * mops
+        d["mfma_flops"] = 512.0 * mops
     return d
 
 
@@ -309,11 +322,13 @@ def write_grounding(a) -> None:
         section += ["", a.note]
     header = ["# rocprofv3 grounding counters (the KORE verifier's set)", "",
               "The counter set and its five single-pass groups are the reference verifier's",
-              "`grounding` set (`kore/verifier/pmc.py:91-127`).  Derived: MFMA busy =",
-              "SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs); L2 hit rate = HIT / (HIT + MISS);",
-              "HBM bytes from the EA request counts with the 32B/64B split (read = 32 x RDREQ_32B +",
-              "64 x (RDREQ - RDREQ_32B), write = 64 x WRREQ_64B + 32 x (WRREQ - WRREQ_64B)); MFMA",
-              "operations = 512 x the MOPS counters."]
+              "`grounding` set (`kore/verifier/pmc.py:91-127`).  Derived with the verifier's formulas:",
+              "`l2_hit_rate` = HIT / (HIT + MISS); HBM bytes from the EA request counts with the",
+              "32B/64B split (read = 32 x RDREQ_32B + 64 x (RDREQ - RDREQ_32B), write = 64 x WRREQ_64B",
+              "+ 32 x (WRREQ - WRREQ_64B)); `mfma_busy_fraction` = min(1, MFMA_BUSY / GRBM_GUI_ACTIVE);",
+              "`mfma_ops` = sum of the MFMA counters.  On MI355X MFMA_BUSY sums all 1024 SIMDs and",
+              "GRBM_GUI_ACTIVE sums the 8 XCDs, so that fraction saturates; `mfma_busy_pct` =",
+              "MFMA_BUSY / (GRBM_GUI_ACTIVE / 8 x 1024) is per SIMD-cycle.  `mfma_flops` = 512 x MOPS."]
     _replace_section(a.out, header, a.workload, section)
     print("\n".join(section))
 

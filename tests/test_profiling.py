@@ -106,4 +106,5 @@ def test_grounding_passes_and_derived():
                              "SQ_INSTS_VALU_MFMA_MOPS_BF16": 2.0})
     assert d["l2_hit_rate"] == 0.75
     assert d["hbm_read_bytes"] == 32 * 4 + 64 * 6 and d["hbm_write_bytes"] == 64 * 5
-    assert d["mfma_busy_pct"] == 50.0 and d["mfma_ops"] == 1024.0
+    assert d["mfma_busy_fraction"] == 1.0 and d["mfma_busy_pct"] == 400.0
+    assert d["mfma_flops"] == 1024.0 and d["mfma_ops"] == 514.0
