@@ -39,6 +39,8 @@ struct TileParams {
   int64_t sa, sb, sc;  // batch strides (elements)
   int tiles_m, tiles_n, tiles_per_batch;
   int batch;  // number of batches (the persistent short-K kernel walks all of them)
+  int kb;     // valid K-rows of an N-contiguous B on the direct-to-LDS engines (rows
+              // from kb on fall outside the buffer resource and read as zero)
   int act;
   int vec_store;  // 16-byte C stores allowed (ldc % 8 == 0, aligned)
   int bias_vec;   // bias is 8-byte aligned: 4-wide bias loads allowed
@@ -183,7 +185,7 @@ __device__ __forceinline__ void setup_operands(E& eng, const TileParams& p, int 
     }
   } else {
     const uint16_t* B = p.b + batch * p.sb + n0;
-    eng.rb = make_rsrc(B, (uint32_t)(((int64_t)(p.K - 1) * p.ldb + rows_b) * 2));
+    eng.rb = make_rsrc(B, (uint32_t)(((int64_t)(p.kb - 1) * p.ldb + rows_b) * 2));
     eng.b_kstep = (uint32_t)(kBK * p.ldb * 2);
 #pragma unroll
     for (int j = 0; j < E::BJ; ++j) {
@@ -663,6 +665,42 @@ __global__ void __launch_bounds__(256) transpose16_kernel(const uint16_t* in, in
 }
 
 // ---------------------------------------------------------------------------------
+// Operand packing for layouts the direct-to-LDS engines cannot read in place (K not a
+// multiple of 8 so rows are not 16-byte aligned, transposed or strided operands):
+// out[b][r][k] = in[b * sbat + r * sr + k * sk] for k < K and 0 for K <= k < Kp, with
+// out rows of Kp (a multiple of 64) elements.  64 x 64 tiles through LDS; the loads
+// walk whichever of r and k is unit-stride so they coalesce, the stores are 16-byte
+// row chunks.
+// ---------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) pack16_kernel(const uint16_t* in, int64_t sr, int64_t sk, int64_t sbat,
+                                                     uint16_t* out, int64_t obat, int R, int K, int Kp) {
+  __shared__ uint16_t t[64][66];  // [r][k]
+  const int tid = threadIdx.x;
+  const int r0 = (int)blockIdx.y * 64, k0 = (int)blockIdx.x * 64;
+  const uint16_t* src = in + (int64_t)blockIdx.z * sbat;
+  uint16_t* dst = out + (int64_t)blockIdx.z * obat;
+  const bool r_unit = sr == 1 && sk != 1;
+  // each wave instruction reads 64 consecutive elements along the unit-stride index
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int u = tid & 63, v = 4 * i + (tid >> 6);
+    const int r = r_unit ? u : v, k = r_unit ? v : u;
+    const int gr = r0 + r, gk = k0 + k;
+    t[r][k] = (gr < R && gk < K) ? src[(int64_t)gr * sr + (int64_t)gk * sk] : (uint16_t)0;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int idx = tid + 256 * q, r = idx >> 3, ch = idx & 7;
+    if (r0 + r >= R) continue;
+    u32x4_t v;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) v[w] = (uint32_t)t[r][8 * ch + 2 * w] | ((uint32_t)t[r][8 * ch + 2 * w + 1] << 16);
+    *(u32x4_t*)(dst + (int64_t)(r0 + r) * Kp + k0 + 8 * ch) = v;
+  }
+}
+
+// ---------------------------------------------------------------------------------
 // Host dispatch
 // ---------------------------------------------------------------------------------
 struct GemmDesc {
@@ -672,6 +710,7 @@ struct GemmDesc {
   int64_t M, N, K, batch;
   int64_t sam, sak, sbk, sbn, scm;  // element strides; B given as (k, n)
   int64_t sa, sb, sc;               // batch strides
+  int64_t kvalid = 0;               // > 0: K-rows of an N-contiguous B that exist (K is padded)
 };
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -716,6 +755,7 @@ int launch_buf(const GemmDesc& d, hipStream_t stream) {
   p.M = (int)d.M;
   p.N = (int)d.N;
   p.K = (int)d.K;
+  p.kb = (int)(d.kvalid > 0 ? d.kvalid : d.K);
   p.lda = d.sam;
   p.ldb = (BL == B_KC) ? d.sbn : d.sbk;
   p.ldc = d.scm;
@@ -745,6 +785,7 @@ int launch_deep(const GemmDesc& d, hipStream_t stream) {
   p.M = (int)d.M;
   p.N = (int)d.N;
   p.K = (int)d.K;
+  p.kb = (int)(d.kvalid > 0 ? d.kvalid : d.K);
   p.lda = d.sam;
   p.ldb = (BL == B_KC) ? d.sbn : d.sbk;
   p.ldc = d.scm;
@@ -860,6 +901,72 @@ int launch_generic(const GemmDesc& d, hipStream_t stream) {
   return check_launch("gemm_generic_kernel");
 }
 
+// Direct-to-LDS engine for an already conforming problem (A and B K-contiguous or B
+// N-contiguous, 16-byte rows, K % 64 == 0, buffer ranges checked by the caller).
+template <typename T, int BL>
+int launch_engine(const GemmDesc& d, hipStream_t stream) {
+  const int64_t big_tiles = ((d.M + 255) / 256) * ((d.N + 255) / 256) * d.batch;
+  const int64_t mid_tiles = ((d.M + 127) / 128) * ((d.N + 127) / 128) * d.batch;
+  const int64_t half_tiles = ((d.M + 63) / 64) * ((d.N + 127) / 128) * d.batch;
+  const int64_t fill = (int64_t)device_cus() * 7 / 8;
+  if (big_tiles >= 192) return launch_buf<T, 256, 256, BL>(d, stream);
+  if (mid_tiles >= fill) return launch_deep<T, 128, 128, 2, 2, 4, BL>(d, stream);
+  if (half_tiles >= fill) return launch_deep<T, 64, 128, 2, 2, 6, BL>(d, stream);
+  return launch_deep<T, 32, 128, 1, 4, 7, BL>(d, stream);
+}
+
+// Layouts the engines cannot read in place (rows not 16-byte aligned, e.g. K = 4095;
+// transposed or strided operands): A, and B unless it is N-contiguous with aligned
+// K-rows, are packed K-contiguous with the K tail zero-padded to a multiple of 64
+// into stream-ordered scratch on the caller's stream (scratch_alloc / scratch_free).
+// An N-contiguous B is read in place: its buffer resource ends at the last real
+// K-row, so the padded rows read as zero.  Returns KORE_EUNSUPPORTED when the packed
+// problem does not fit the engines' 32-bit buffer offsets or scratch is unavailable.
+template <typename T>
+int launch_padded(const GemmDesc& d, hipStream_t stream) {
+  const int64_t Kp = (d.K + 63) / 64 * 64;
+  const bool b_nc = d.sbn == 1 && d.sbk % 8 == 0 && aligned16(d.b) && d.sb % 8 == 0 && d.N % 8 == 0 &&
+                    d.sbk * 2 * d.K + d.N * 2 < (1ll << 31);
+  if (d.M >= (1ll << 31) || d.N >= (1ll << 31) || Kp * 2 * 256 + Kp * 2 >= (1ll << 31) || d.batch > 65535)
+    return KORE_EUNSUPPORTED;
+  const size_t a_bytes = (size_t)(d.batch * d.M * Kp * 2 + 255) / 256 * 256;
+  const size_t b_bytes = b_nc ? 0 : (size_t)(d.batch * d.N * Kp * 2);
+  void* ws = scratch_alloc(a_bytes + b_bytes, stream);
+  if (ws == nullptr) return KORE_EUNSUPPORTED;
+  uint16_t* ap = (uint16_t*)ws;
+  uint16_t* bp = (uint16_t*)((char*)ws + a_bytes);
+  hipLaunchKernelGGL(pack16_kernel, dim3((unsigned)(Kp / 64), (unsigned)((d.M + 63) / 64), (unsigned)d.batch), dim3(256),
+                     0, stream, (const uint16_t*)d.a, d.sam, d.sak, d.sa, ap, d.M * Kp, (int)d.M, (int)d.K, (int)Kp);
+  int rc = check_launch("pack16_kernel");
+  GemmDesc q = d;
+  q.a = ap;
+  q.sam = Kp;
+  q.sak = 1;
+  q.sa = d.M * Kp;
+  q.K = Kp;
+  if (rc == KORE_OK && !b_nc) {
+    // B^T rows (n) with K-contiguous, zero-padded K
+    hipLaunchKernelGGL(pack16_kernel, dim3((unsigned)(Kp / 64), (unsigned)((d.N + 63) / 64), (unsigned)d.batch),
+                       dim3(256), 0, stream, (const uint16_t*)d.b, d.sbn, d.sbk, d.sb, bp, d.N * Kp, (int)d.N, (int)d.K,
+                       (int)Kp);
+    rc = check_launch("pack16_kernel");
+    q.b = bp;
+    q.sbk = 1;
+    q.sbn = Kp;
+    q.sb = d.N * Kp;
+  }
+  if (rc == KORE_OK) {
+    if (b_nc) {
+      q.kvalid = d.K;
+      rc = launch_engine<T, B_NC>(q, stream);
+    } else {
+      rc = launch_engine<T, B_KC>(q, stream);
+    }
+  }
+  scratch_free(ws, stream);
+  return rc;
+}
+
 template <typename T>
 int dispatch_typed(const GemmDesc& d, hipStream_t stream) {
   // Fast-path preconditions: A K-contiguous with 16-byte aligned rows, K % 8 == 0,
@@ -914,6 +1021,12 @@ int dispatch_typed(const GemmDesc& d, hipStream_t stream) {
     }
     if (big && !short_k) return launch_tile<T, B_NC, 256, 256>(d, stream);
     return small ? launch_tile<T, B_NC, 64, 64>(d, stream) : launch_tile<T, B_NC, 128, 128>(d, stream);
+  }
+  // Large problems in other layouts: pack, then the engines (small ones are cheaper on
+  // the generic kernel than a pack pass).
+  if (d.M * d.N * d.K >= (1ll << 27) && d.K >= 64) {
+    const int rc = launch_padded<T>(d, stream);
+    if (rc != KORE_EUNSUPPORTED) return rc;
   }
   return launch_generic<T>(d, stream);
 }

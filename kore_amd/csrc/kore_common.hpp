@@ -150,6 +150,8 @@ int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 // Compute units of the current device (cached per device; 256 on MI355X).
 int device_cus();
+void* scratch_alloc(size_t bytes, hipStream_t stream);  // nullptr when unavailable
+void scratch_free(void* p, hipStream_t stream);
 
 // Top-1 grouped fp8 a8w8 GEMM over an expert-sorted token order (tiles of
 // gemm_fp8_blockscale.hip, called by the grouped entry in moe.hip): xq[M,K] (row

@@ -37,6 +37,39 @@ int device_cus() {
   return cached[dev];
 }
 
+// Stream-ordered scratch from a library-owned pool per device whose release threshold
+// is unbounded, so memory freed by one call is reused by the next without going back
+// to the driver (the process default pool is left as the caller configured it).
+void* scratch_alloc(size_t bytes, hipStream_t stream) {
+  static hipMemPool_t pools[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  if (pools[dev] == nullptr) {
+    hipMemPoolProps props = {};
+    props.allocType = hipMemAllocationTypePinned;
+    props.location.type = hipMemLocationTypeDevice;
+    props.location.id = dev;
+    hipMemPool_t pool = nullptr;
+    if (hipMemPoolCreate(&pool, &props) != hipSuccess || pool == nullptr) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    uint64_t keep = ~0ull;
+    (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+    pools[dev] = pool;
+  }
+  void* p = nullptr;
+  if (hipMallocFromPoolAsync(&p, bytes, pools[dev], stream) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  return p;
+}
+
+void scratch_free(void* p, hipStream_t stream) {
+  if (p != nullptr) (void)hipFreeAsync(p, stream);
+}
+
 }  // namespace kore
 
 extern "C" const char* kore_last_error(void) { return kore::g_last_error; }

@@ -63,7 +63,8 @@ def test_gemm_ring_small(gpu, M, N, K, dtype, op):
                                    (513, 1000, 200), (4096, 4096, 4096)])
 def test_gemm_reference_task_shapes(gpu, M, N, K):
     """gemm_bf16 task.yaml shapes (kore/tasks/gemm_bf16/task.yaml:8-14) with the task's
-    natural N-contiguous B, plus a ragged shape; 4095 exercises the generic kernel."""
+    natural N-contiguous B, plus a ragged shape; K = 4095 takes the packed path (A padded
+    into scratch, B read in place up to its last real K-row)."""
     a, b = _ref_style_inputs(M, N, K, seed=1)
     out = kore_amd.gemm(a.to(gpu), b.to(gpu))
     verdict(out, matmul_ref(a, b), "gemm", "bf16", f"{M}x{N}x{K}")
@@ -135,6 +136,51 @@ def test_batched_deep_ring(gpu):
     b = (torch.randn((16, 512, 512), generator=g) / 512 ** 0.5).bfloat16()
     out = kore_amd.batched_gemm(a.to(gpu), b.to(gpu))
     verdict(out, batched_gemm_ref(a, b), "gemm", "bf16", "batched deep 16x512x512x512")
+
+
+@pytest.mark.parametrize("M,N,K,dtype,op,layout", [(512, 4096, 4095, torch.float16, "gemm_bias_gelu", "kn"),
+                                                    (512, 4096, 4095, torch.bfloat16, "gemm_bias_silu", "nk"),
+                                                    (1024, 2048, 2047, torch.bfloat16, "gemm_relu", "kn_at"),
+                                                    (300, 1000, 777, torch.float16, "gemm_bias", "nk_at"),
+                                                    (2048, 2048, 1000, torch.bfloat16, "gemm", "strided")])
+def test_gemm_packed_path(gpu, M, N, K, dtype, op, layout):
+    """Operands the engines cannot read in place -- K tails that leave rows unaligned (the
+    gen_gemm_* K = 4095 validation shape), a transposed A, a B with a row stride that is
+    not a multiple of 8 -- are packed into stream-ordered scratch first."""
+    has_bias, act = kore_amd.GEMM_FUSION_OPS.get(op, (False, "none"))
+    g = torch.Generator().manual_seed(M + 3 * N + K)
+    sc = 1.0 / K ** 0.5
+    a = (torch.randn((M, K), generator=g) * sc).to(dtype)
+    ad = a.t().contiguous().to(gpu).t() if layout.endswith("_at") else a.to(gpu)
+    if layout.startswith("kn"):
+        b = (torch.randn((K, N), generator=g) * sc).to(dtype)
+        bd = b.to(gpu)
+    elif layout == "strided":
+        full = (torch.randn((K, N + 3), generator=g) * sc).to(dtype)
+        b, bd = full[:, :N], full.to(gpu)[:, :N]
+    else:
+        w = (torch.randn((N, K), generator=g) * sc).to(dtype)
+        b, bd = w.t(), w.to(gpu).t()
+    bias = torch.randn((N,), generator=g).to(dtype) if has_bias else None
+    out = kore_amd.gemm_fused(ad, bd, bias.to(gpu) if has_bias else None, act)
+    ref = gemm_fusion_ref(a, b, bias, act)
+    dt = "bf16" if dtype == torch.bfloat16 else "fp16"
+    verdict(out, ref, "gemm_fusion", dt, f"packed {op} {M}x{N}x{K} {layout}")
+    pair_only(out, ref, dt, f"packed {op} {M}x{N}x{K} {layout}")
+    # a second call reuses the scratch pool: same result bit for bit
+    again = kore_amd.gemm_fused(ad, bd, bias.to(gpu) if has_bias else None, act)
+    assert torch.equal(out, again)
+
+
+def test_batched_packed_path(gpu):
+    """A batched problem with an odd K runs the packed path per batch."""
+    from oracle.gemm import batched_gemm_ref
+
+    g = torch.Generator().manual_seed(9)
+    a = (torch.randn((4, 512, 999), generator=g) / 999 ** 0.5).bfloat16()
+    b = (torch.randn((4, 384, 999), generator=g) / 999 ** 0.5).bfloat16()
+    out = kore_amd.batched_gemm(a.to(gpu), b.to(gpu))
+    verdict(out, batched_gemm_ref(a, b), "gemm", "bf16", "batched packed 4x512x384x999")
 
 
 def test_gemm_metric_4096_bt(gpu):
