@@ -235,6 +235,88 @@ __global__ void __launch_bounds__(256) gemm_deep_kernel(const TileParams p) {
 }
 
 // ---------------------------------------------------------------------------------
+// Split-K for small problems with a long K (decode-sized M: 1x4096x4096 has 32 tiles of
+// 32x128 for 256 CUs).  Workgroup (tile, s) runs the 32x128 deep ring over K slice s and
+// writes its fp32 partial tile to part[s]; splitk_reduce_kernel then sums the slices in
+// a fixed order (deterministic), applies bias and activation and stores C.
+// ---------------------------------------------------------------------------------
+template <typename T, int BL>
+__global__ void __launch_bounds__(256) gemm_splitk_kernel(const TileParams p, float* part, int splits, int kper) {
+  using E = RingEngine<T, 32, 128, 1, 4, 7, BL>;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int s = (int)blockIdx.x % splits, t = (int)blockIdx.x / splits;
+  const int m0 = (t % p.tiles_m) * 32, n0 = (t / p.tiles_m) * 128;
+  const int k_begin = s * kper, k_end = min(p.K, k_begin + kper);
+  E eng;
+  setup_operands<E, 32, 128, BL>(eng, p, 0, m0, n0, wave, lane);
+  f32x16_t acc[1][1];
+  E::zero(acc);
+  eng.mainloop_range(lds, k_begin, k_end, acc);
+  float* dst = part + (int64_t)s * p.M * p.N;
+  const int m = m0 + out_row(0, lane);
+  if (m >= p.M) return;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int n = n0 + wave * 32 + out_col(0, g, lane);
+    float* q = dst + (int64_t)m * p.N + n;
+    if ((p.N & 3) == 0 && n + 4 <= p.N) {
+      *(f32x4_t*)q = f32x4_t{acc[0][0][4 * g], acc[0][0][4 * g + 1], acc[0][0][4 * g + 2], acc[0][0][4 * g + 3]};
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (n + e < p.N) q[e] = acc[0][0][4 * g + e];
+    }
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const float* part, int splits, int M, int N,
+                                                            const uint16_t* bias, int act, uint16_t* C, int64_t ldc,
+                                                            int vec) {
+  using Op = MfmaOp<T>;
+  const int nc = (N + 7) / 8;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)M * nc) return;
+  const int m = (int)(idx / nc), n = (int)(idx % nc) * 8;
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+  for (int s = 0; s < splits; ++s) {
+    const float* q = part + ((int64_t)s * M + m) * N + n;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (n + e < N) v[e] += q[e];
+  }
+  if (bias != nullptr) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (n + e < N) v[e] += Op::to_f32(bias[n + e]);
+  }
+  auto fin = [&](auto act_tag) {
+    constexpr int ACT = decltype(act_tag)::value;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = apply_act<ACT>(v[e]);
+  };
+  switch (act) {
+    case ACT_RELU: fin(std::integral_constant<int, ACT_RELU>{}); break;
+    case ACT_GELU: fin(std::integral_constant<int, ACT_GELU>{}); break;
+    case ACT_SILU: fin(std::integral_constant<int, ACT_SILU>{}); break;
+    case ACT_TANH: fin(std::integral_constant<int, ACT_TANH>{}); break;
+    case ACT_SIGMOID: fin(std::integral_constant<int, ACT_SIGMOID>{}); break;
+    default: break;
+  }
+  uint16_t* out = C + (int64_t)m * ldc + n;
+  if (vec && n + 8 <= N) {
+    *(u32x4_t*)out = u32x4_t{Op::pack2(v[0], v[1]), Op::pack2(v[2], v[3]), Op::pack2(v[4], v[5]), Op::pack2(v[6], v[7])};
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (n + e < N) out[e] = (uint16_t)(Op::pack2(v[e], 0.0f) & 0xffffu);
+  }
+}
+
+// ---------------------------------------------------------------------------------
 // Small problems (fewer than 128 tiles of 128x128, e.g. 1024^3 with 64): the time is
 // load latency, not MFMA work (a 64x64 tile with a register double buffer waits one
 // full memory round trip per 64-wide K step).  32 x BN tiles on the skinny ring
@@ -901,6 +983,44 @@ int launch_generic(const GemmDesc& d, hipStream_t stream) {
   return check_launch("gemm_generic_kernel");
 }
 
+// Split-K launch (batch 1): `splits` slices of `kper` (a multiple of 64) K elements.
+template <typename T, int BL>
+int launch_splitk(const GemmDesc& d, int splits, int kper, hipStream_t stream) {
+  TileParams p = {};
+  p.a = (const uint16_t*)d.a;
+  p.b = (const uint16_t*)d.b;
+  p.bias = (const uint16_t*)d.bias;
+  p.c = (uint16_t*)d.c;
+  p.M = (int)d.M;
+  p.N = (int)d.N;
+  p.K = (int)d.K;
+  p.kb = (int)(d.kvalid > 0 ? d.kvalid : d.K);
+  p.lda = d.sam;
+  p.ldb = (BL == B_KC) ? d.sbn : d.sbk;
+  p.ldc = d.scm;
+  p.tiles_m = (int)((d.M + 31) / 32);
+  p.tiles_n = (int)((d.N + 127) / 128);
+  p.tiles_per_batch = p.tiles_m * p.tiles_n;
+  p.batch = 1;
+  p.act = d.act;
+  const size_t bytes = (size_t)splits * d.M * d.N * sizeof(float);
+  float* part = (float*)scratch_alloc(bytes, stream);
+  if (part == nullptr) return KORE_EUNSUPPORTED;
+  hipLaunchKernelGGL((gemm_splitk_kernel<T, BL>), dim3((unsigned)(p.tiles_per_batch * splits)), dim3(256), 0, stream, p,
+                     part, splits, kper);
+  int rc = check_launch("gemm_splitk_kernel");
+  if (rc == KORE_OK) {
+    const int vec = (d.scm % 8 == 0) && aligned16(d.c);
+    const int64_t threads = d.M * ((d.N + 7) / 8);
+    hipLaunchKernelGGL((splitk_reduce_kernel<T>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
+                       (const float*)part, splits, (int)d.M, (int)d.N, (const uint16_t*)d.bias, d.act, (uint16_t*)d.c,
+                       d.scm, vec);
+    rc = check_launch("splitk_reduce_kernel");
+  }
+  scratch_free(part, stream);
+  return rc;
+}
+
 // Direct-to-LDS engine for an already conforming problem (A and B K-contiguous or B
 // N-contiguous, 16-byte rows, K % 64 == 0, buffer ranges checked by the caller).
 template <typename T, int BL>
@@ -918,7 +1038,7 @@ int launch_engine(const GemmDesc& d, hipStream_t stream) {
 // Layouts the engines cannot read in place (rows not 16-byte aligned, e.g. K = 4095;
 // transposed or strided operands): A, and B unless it is N-contiguous with aligned
 // K-rows, are packed K-contiguous with the K tail zero-padded to a multiple of 64
-// into stream-ordered scratch on the caller's stream (scratch_alloc / scratch_free).
+// into the caller stream's scratch buffer (scratch_alloc).
 // An N-contiguous B is read in place: its buffer resource ends at the last real
 // K-row, so the padded rows read as zero.  Returns KORE_EUNSUPPORTED when the packed
 // problem does not fit the engines' 32-bit buffer offsets or scratch is unavailable.
@@ -1012,6 +1132,16 @@ int dispatch_typed(const GemmDesc& d, hipStream_t stream) {
                         d.sam * 2 * 128 + d.K * 2 < (1ll << 31) && (b_nc || d.sbn * 2 * 128 + d.K * 2 < (1ll << 31)) &&
                         d.scm * 2 * 128 < (1ll << 31) && mid_tiles >= 4 * (int64_t)device_cus();
     if (shortk) return b_kc ? launch_shortk<T, B_KC>(d, stream) : launch_shortk<T, B_NC>(d, stream);
+    // Few 32x128 tiles for the CUs and a long K (decode-sized M): split K.
+    const int64_t t32 = ((d.M + 31) / 32) * ((d.N + 127) / 128);
+    if (d.batch == 1 && (b_kc ? buf_ok : buf_nc_ok) && d.K >= 1024 && t32 * 2 <= device_cus()) {
+      const int nk = (int)(d.K / 64);
+      const int want = (int)std::min<int64_t>(device_cus() / t32, nk / 4);
+      const int per = (nk + want - 1) / want, splits = (nk + per - 1) / per;
+      const int rc = b_kc ? launch_splitk<T, B_KC>(d, splits, per * 64, stream)
+                          : launch_splitk<T, B_NC>(d, splits, per * 64, stream);
+      if (rc != KORE_EUNSUPPORTED) return rc;
+    }
     // few tiles and a long K: the latency-bound case, on the deep direct-to-LDS ring
     if (b_kc && small && buf_ok && d.K >= 512) return launch_ring<T>(d, stream);
     if (!b_kc && small && buf_nc_ok && d.K >= 512) return launch_deep<T, 32, 128, 1, 4, 7, B_NC>(d, stream);

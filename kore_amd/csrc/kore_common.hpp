@@ -150,7 +150,9 @@ int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 // Compute units of the current device (cached per device; 256 on MI355X).
 int device_cus();
-void* scratch_alloc(size_t bytes, hipStream_t stream);  // nullptr when unavailable
+// Per-(device, stream) scratch, valid until the next scratch_alloc on that stream;
+// nullptr when unavailable (the caller falls back).
+void* scratch_alloc(size_t bytes, hipStream_t stream);
 void scratch_free(void* p, hipStream_t stream);
 
 // Top-1 grouped fp8 a8w8 GEMM over an expert-sorted token order (tiles of

@@ -685,6 +685,11 @@ struct RingEngine {
 
   // K must be a positive multiple of 64.
   __device__ __forceinline__ void mainloop(uint16_t* lds, int K, f32x16_t (&acc)[MI][NI]) {
+    mainloop_range(lds, 0, K, acc);
+  }
+
+  // Multiply K elements [k_begin, k_end) (multiples of 64, k_end > k_begin).
+  __device__ __forceinline__ void mainloop_range(uint16_t* lds, int k_begin, int k_end, f32x16_t (&acc)[MI][NI]) {
     using Op = MfmaOp<T>;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
@@ -704,9 +709,9 @@ struct RingEngine {
       }
     }
     if constexpr (NC) nc_frag_offsets<BN, NI>(lane, rowB0, offNC);
-    const int nk = K / kBK;
-    auto soff_of = [&](int stage) { return (uint32_t)min(stage, nk - 1) * (kBK * 2); };
-    auto soffb_of = [&](int stage) { return NC ? (uint32_t)min(stage, nk - 1) * b_kstep : soff_of(stage); };
+    const int nk = (k_end - k_begin) / kBK, kb0 = k_begin / kBK;
+    auto soff_of = [&](int stage) { return (uint32_t)(kb0 + min(stage, nk - 1)) * (kBK * 2); };
+    auto soffb_of = [&](int stage) { return NC ? (uint32_t)(kb0 + min(stage, nk - 1)) * b_kstep : soff_of(stage); };
 #pragma unroll
     for (int s = 0; s < NSLOT - 1; ++s) issue(lds, s, soff_of(s), soffb_of(s), wave);
     int slot = 0;

@@ -172,6 +172,35 @@ def test_gemm_packed_path(gpu, M, N, K, dtype, op, layout):
     assert torch.equal(out, again)
 
 
+@pytest.mark.parametrize("M,N,K,dtype,op,layout", [(1, 4096, 4096, torch.bfloat16, "gemm", "kn"),
+                                                    (16, 11008, 4096, torch.float16, "gemm_bias_gelu", "kn"),
+                                                    (7, 1002, 2048, torch.bfloat16, "gemm_bias_relu", "nk"),
+                                                    (33, 3000, 1024, torch.float16, "gemm_sigmoid", "nk"),
+                                                    (64, 4096, 4096, torch.bfloat16, "gemm_bias_silu", "kn")])
+def test_gemm_splitk(gpu, M, N, K, dtype, op, layout):
+    """Decode-sized M with a long K splits K over the CUs (32x128 ring per slice, fp32
+    partials, fixed-order reduce with the epilogue): ragged N (not a multiple of 4 on the
+    W.t() layout), several slice counts, and bit-identical repeated calls."""
+    has_bias, act = kore_amd.GEMM_FUSION_OPS.get(op, (False, "none"))
+    g = torch.Generator().manual_seed(M + N + K + 1)
+    sc = 1.0 / K ** 0.5
+    a = (torch.randn((M, K), generator=g) * sc).to(dtype)
+    if layout == "kn":
+        b = (torch.randn((K, N), generator=g) * sc).to(dtype)
+        bd = b.to(gpu)
+    else:
+        w = (torch.randn((N, K), generator=g) * sc).to(dtype)
+        b, bd = w.t(), w.to(gpu).t()
+    bias = torch.randn((N,), generator=g).to(dtype) if has_bias else None
+    args = (a.to(gpu), bd, bias.to(gpu) if has_bias else None, act)
+    out = kore_amd.gemm_fused(*args)
+    ref = gemm_fusion_ref(a, b, bias, act)
+    dt = "bf16" if dtype == torch.bfloat16 else "fp16"
+    verdict(out, ref, "gemm_fusion", dt, f"splitk {op} {M}x{N}x{K} {layout}")
+    pair_only(out, ref, dt, f"splitk {op} {M}x{N}x{K} {layout}")
+    assert torch.equal(out, kore_amd.gemm_fused(*args))
+
+
 def test_batched_packed_path(gpu):
     """A batched problem with an odd K runs the packed path per batch."""
     from oracle.gemm import batched_gemm_ref
