@@ -2,9 +2,14 @@
  * kore_amd.h -- C ABI of the MI355X (gfx950) GEMM-family library (libkore_amd.so).
  *
  * Every entry point takes plain device pointers, element strides and sizes, and a
- * HIP stream (hipStream_t passed as void*; NULL = the legacy default stream).  No
- * entry point allocates device memory: outputs and workspaces are owned by the
- * caller.  Calls are asynchronous on `stream`.  Return value: KORE_OK, or an error
+ * HIP stream (hipStream_t passed as void*; NULL = the legacy default stream).
+ * Outputs and workspaces are owned by the caller.  One exception to "no entry point
+ * allocates device memory": kore_gemm and kore_batched_gemm keep one grow-only scratch
+ * buffer per (device, stream) for the packed-operand path (layouts the engines cannot
+ * read in place, e.g. K = 4095) and the split-K path (decode-sized M), allocated on
+ * first need outside graph capture and kept until the process exits; under capture a
+ * buffer that is too small makes them take a path that needs none.  Calls are
+ * asynchronous on `stream`.  Return value: KORE_OK, or an error
  * code with a message available from kore_last_error() (per host thread).
  *
  * Each entry replaces the body of one KORE task-suite candidate entry callable
@@ -90,9 +95,9 @@ int kore_batched_gemm(int dtype,
 /*
  * GEMM backward of the linear layer Y = X @ W^T (X [M,K], W [N,K], dY [M,N]):
  *   dX [M,K] = dY @ W,   dW [N,K] = dY^T @ X,   fp32 accumulate, `dtype` out (bf16/fp16).
- *   Row strides ldx, ldw, lddy, lddx, lddw (unit stride along rows).  W^T, X^T and
- *   dY^T are formed in `workspace` (so both GEMMs read K-contiguous operands), which
- *   must hold kore_gemm_backward_workspace_bytes(M, N, K) bytes.
+ *   Row strides ldx, ldw, lddy, lddx, lddw (unit stride along rows).  dY^T is formed
+ *   in `workspace` (the A operand of dW must be K-contiguous), which must hold
+ *   kore_gemm_backward_workspace_bytes(M, N, K) bytes; W and X are read in place.
  * Replaces: gemm_backward(x, w, dy) -> (dx, dw)
  *           kore/tasks/gemm_backward_bf16/seed_triton.py:74-86 (ENTRY reference.py:22,
  *           oracle reference.py:64-72)

@@ -1212,7 +1212,7 @@ inline size_t bwd_part(int64_t rows, int64_t cols) { return (size_t)(rows * bwd_
 extern "C" size_t kore_gemm_backward_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   using namespace kore;
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  return bwd_part(K, N) + bwd_part(K, M) + bwd_part(N, M) + 256;
+  return bwd_part(N, M) + 256;
 }
 
 extern "C" int kore_gemm_backward(int dtype, const void* x, int64_t ldx, const void* w, int64_t ldw, const void* dy,
@@ -1231,24 +1231,19 @@ extern "C" int kore_gemm_backward(int dtype, const void* x, int64_t ldx, const v
     return set_error(KORE_EINVAL, "gemm_backward: workspace smaller than kore_gemm_backward_workspace_bytes(M, N, K)");
   hipStream_t st = (hipStream_t)stream;
   uint8_t* base = (uint8_t*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
-  uint16_t* wt = (uint16_t*)base;                                         // W^T  [K, N]
-  uint16_t* xt = (uint16_t*)(base + bwd_part(K, N));                      // X^T  [K, M]
-  uint16_t* dyt = (uint16_t*)(base + bwd_part(K, N) + bwd_part(K, M));    // dY^T [N, M]
-  const int64_t ldn = bwd_ld(N), ldm = bwd_ld(M);
-  auto transpose = [&](const void* in, int64_t ldi, uint16_t* out, int64_t ldo, int64_t R, int64_t C) {
-    hipLaunchKernelGGL(transpose16_kernel, dim3((unsigned)((C + 63) / 64), (unsigned)((R + 63) / 64)), dim3(256), 0,
-                       st, (const uint16_t*)in, ldi, out, ldo, (int)R, (int)C);
-    return check_launch("transpose16_kernel");
-  };
-  int rc = transpose(w, ldw, wt, ldn, N, K);
-  if (rc == KORE_OK) rc = transpose(x, ldx, xt, ldm, M, K);
-  if (rc == KORE_OK) rc = transpose(dy, lddy, dyt, ldm, M, N);
+  uint16_t* dyt = (uint16_t*)base;  // dY^T [N, M]
+  const int64_t ldm = bwd_ld(M);
+  // dX[M,K] = dY[M,N] @ W[N,K]: W read in place as an N-contiguous B (element (n, k) at
+  // w[n*ldw + k]); the engines stage it through LDS transpose reads
+  GemmDesc gx{dtype, KORE_ACT_NONE, dy, w, nullptr, dx, M, K, N, 1, lddy, 1, ldw, 1, lddx, 0, 0, 0};
+  int rc = run_gemm(gx, st);
   if (rc != KORE_OK) return rc;
-  // dX[M,K] = dY[M,N] @ W[N,K]: B element (n, k) at wt[k*ldn + n] (K-contiguous)
-  GemmDesc gx{dtype, KORE_ACT_NONE, dy, wt, nullptr, dx, M, K, N, 1, lddy, 1, 1, ldn, lddx, 0, 0, 0};
-  rc = run_gemm(gx, st);
+  // dW[N,K] = dY^T[N,M] @ X[M,K]: A must be K-contiguous, so dY is transposed once into the
+  // workspace; X is read in place as an N-contiguous B (element (m, k) at x[m*ldx + k])
+  hipLaunchKernelGGL(transpose16_kernel, dim3((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64)), dim3(256), 0, st,
+                     (const uint16_t*)dy, lddy, dyt, ldm, (int)M, (int)N);
+  rc = check_launch("transpose16_kernel");
   if (rc != KORE_OK) return rc;
-  // dW[N,K] = dY^T[N,M] @ X[M,K]: B element (m, k) at xt[k*ldm + m] (K-contiguous)
-  GemmDesc gw{dtype, KORE_ACT_NONE, dyt, xt, nullptr, dw, N, K, M, 1, ldm, 1, 1, ldm, lddw, 0, 0, 0};
+  GemmDesc gw{dtype, KORE_ACT_NONE, dyt, x, nullptr, dw, N, K, M, 1, ldm, 1, ldx, 1, lddw, 0, 0, 0};
   return run_gemm(gw, st);
 }

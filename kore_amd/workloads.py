@@ -288,6 +288,25 @@ def bench_workloads():
             return (lambda: kore_amd.gemm_bias(a, b, bias)), "gemm", {"M": M, "N": N, "K": K}, "fp32"
         return build
 
+    def task_kn(M, N, K, dtype, op):
+        # a gemm_bf16 / gen_gemm_* task's own operands: a, b[K,N] ~ N(0,1)/sqrt(K) with
+        # b contiguous (kore/tasks/_genops.py:434-443), bias ~ N(0,1)
+        def build(dev):
+            g = _gen(dev, 0)
+            has_bias, act = kore_amd.GEMM_FUSION_OPS.get(op, (False, "none"))
+            a = (torch.randn((M, K), generator=g, device=dev) / K ** 0.5).to(dtype)
+            b = (torch.randn((K, N), generator=g, device=dev) / K ** 0.5).to(dtype)
+            bias = torch.randn((N,), generator=g, device=dev).to(dtype) if has_bias else None
+            return (lambda: kore_amd.gemm_fused(a, b, bias, act)), "gemm", {"M": M, "N": N, "K": K}, \
+                "bf16" if dtype == torch.bfloat16 else "fp16"
+        return build
+
+    # the gen_gemm_* primary (deep ring), its K-tail validation shape (packed path) and
+    # gemm_bf16's decode validation shape (split-K), all with the tasks' [K,N] B
+    w["fp16_gemm_bias_gelu_512x4096x4096_kn"] = task_kn(512, 4096, 4096, torch.float16, "gemm_bias_gelu")
+    w["bf16_gemm_bias_gelu_512x4096x4095_kn"] = task_kn(512, 4096, 4095, torch.bfloat16, "gemm_bias_gelu")
+    w["bf16_gemm_1x4096x4096_kn"] = task_kn(1, 4096, 4096, torch.bfloat16, "gemm")
+
     # fp32 epilogue GEMM on the fp32 matrix cores (gen_gemm_bias_fp32 primary)
     w["fp32_gemm_bias_512x4096x4096"] = fp32_bias(512, 4096, 4096)
     for M in (512, 128, 16):
