@@ -240,33 +240,39 @@ __global__ void __launch_bounds__(256) gemm_deep_kernel(const TileParams p) {
 // writes its fp32 partial tile to part[s]; splitk_reduce_kernel then sums the slices in
 // a fixed order (deterministic), applies bias and activation and stores C.
 // ---------------------------------------------------------------------------------
-template <typename T, int BL>
+template <typename T, int BL, int BM, int BN, int WM, int WN, int NSLOT>
 __global__ void __launch_bounds__(256) gemm_splitk_kernel(const TileParams p, float* part, int splits, int kper) {
-  using E = RingEngine<T, 32, 128, 1, 4, 7, BL>;
+  using E = RingEngine<T, BM, BN, WM, WN, NSLOT, BL>;
   __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int s = (int)blockIdx.x % splits, t = (int)blockIdx.x / splits;
-  const int m0 = (t % p.tiles_m) * 32, n0 = (t / p.tiles_m) * 128;
+  const int m0 = (t % p.tiles_m) * BM, n0 = (t / p.tiles_m) * BN;
   const int k_begin = s * kper, k_end = min(p.K, k_begin + kper);
   E eng;
-  setup_operands<E, 32, 128, BL>(eng, p, 0, m0, n0, wave, lane);
-  f32x16_t acc[1][1];
+  setup_operands<E, BM, BN, BL>(eng, p, 0, m0, n0, wave, lane);
+  f32x16_t acc[E::MI][E::NI];
   E::zero(acc);
   eng.mainloop_range(lds, k_begin, k_end, acc);
   float* dst = part + (int64_t)s * p.M * p.N;
-  const int m = m0 + out_row(0, lane);
-  if (m >= p.M) return;
+  const int mw = m0 + (wave / WN) * E::WROWS, nw = n0 + (wave % WN) * E::WCOLS;
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const int n = n0 + wave * 32 + out_col(0, g, lane);
-    float* q = dst + (int64_t)m * p.N + n;
-    if ((p.N & 3) == 0 && n + 4 <= p.N) {
-      *(f32x4_t*)q = f32x4_t{acc[0][0][4 * g], acc[0][0][4 * g + 1], acc[0][0][4 * g + 2], acc[0][0][4 * g + 3]};
-    } else {
+  for (int i = 0; i < E::MI; ++i) {
+    const int m = mw + out_row(i, lane);
+    if (m >= p.M) continue;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (n + e < p.N) q[e] = acc[0][0][4 * g + e];
-    }
+    for (int j = 0; j < E::NI; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = nw + out_col(j, g, lane);
+        float* q = dst + (int64_t)m * p.N + n;
+        if ((p.N & 3) == 0 && n + 4 <= p.N) {
+          *(f32x4_t*)q = f32x4_t{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < p.N) q[e] = acc[i][j][4 * g + e];
+        }
+      }
   }
 }
 
@@ -983,8 +989,9 @@ int launch_generic(const GemmDesc& d, hipStream_t stream) {
   return check_launch("gemm_generic_kernel");
 }
 
-// Split-K launch (batch 1): `splits` slices of `kper` (a multiple of 64) K elements.
-template <typename T, int BL>
+// Split-K launch (batch 1): `splits` slices of `kper` (a multiple of 64) K elements on
+// BM x BN ring tiles.
+template <typename T, int BL, int BM, int BN, int WM, int WN, int NSLOT>
 int launch_splitk(const GemmDesc& d, int splits, int kper, hipStream_t stream) {
   TileParams p = {};
   p.a = (const uint16_t*)d.a;
@@ -998,16 +1005,16 @@ int launch_splitk(const GemmDesc& d, int splits, int kper, hipStream_t stream) {
   p.lda = d.sam;
   p.ldb = (BL == B_KC) ? d.sbn : d.sbk;
   p.ldc = d.scm;
-  p.tiles_m = (int)((d.M + 31) / 32);
-  p.tiles_n = (int)((d.N + 127) / 128);
+  p.tiles_m = (int)((d.M + BM - 1) / BM);
+  p.tiles_n = (int)((d.N + BN - 1) / BN);
   p.tiles_per_batch = p.tiles_m * p.tiles_n;
   p.batch = 1;
   p.act = d.act;
   const size_t bytes = (size_t)splits * d.M * d.N * sizeof(float);
   float* part = (float*)scratch_alloc(bytes, stream);
   if (part == nullptr) return KORE_EUNSUPPORTED;
-  hipLaunchKernelGGL((gemm_splitk_kernel<T, BL>), dim3((unsigned)(p.tiles_per_batch * splits)), dim3(256), 0, stream, p,
-                     part, splits, kper);
+  hipLaunchKernelGGL((gemm_splitk_kernel<T, BL, BM, BN, WM, WN, NSLOT>), dim3((unsigned)(p.tiles_per_batch * splits)),
+                     dim3(256), 0, stream, p, part, splits, kper);
   int rc = check_launch("gemm_splitk_kernel");
   if (rc == KORE_OK) {
     const int vec = (d.scm % 8 == 0) && aligned16(d.c);
@@ -1021,18 +1028,51 @@ int launch_splitk(const GemmDesc& d, int splits, int kper, hipStream_t stream) {
   return rc;
 }
 
+// Tile shape for the direct-to-LDS engines.  Every CU runs one tile at a time, so a
+// launch costs about (rounds of tiles over the CUs) x (time of one tile); a tile's time
+// is its area over its engine's efficiency (the 256x256 pipelined engine is best;
+// narrower ring tiles move more bytes per MFMA).  Small problems that fill less
+// than half the chip even with 64x128 tiles take 32x128 tiles.
+enum TileShape { TILE_256x256, TILE_256x128, TILE_128x128, TILE_64x128, TILE_32x128 };
+
+inline TileShape pick_tile(const GemmDesc& d) {
+  const int64_t cus = device_cus();
+  struct Opt {
+    TileShape t;
+    int bm, bn;
+    double cost_per_round;  // tile area / efficiency, in 64x128 units
+  } opts[] = {// efficiencies from one full round at K = 4096 each: 4096^3 (256x256,
+              // 111 us), 1536x4096 (256x128, 71 us), 2048^2 x 4096-equivalent (128x128),
+              // 512x4096 (64x128, 32 us), relative to the 256x256 engine
+              {TILE_256x256, 256, 256, 8.0 / 1.0},
+              {TILE_256x128, 256, 128, 4.0 / 0.79},
+              {TILE_128x128, 128, 128, 2.0 / 0.55},
+              {TILE_64x128, 64, 128, 1.0 / 0.43}};
+  TileShape best = TILE_32x128;
+  double best_cost = 1e300;
+  for (const Opt& o : opts) {
+    const int64_t tiles = ((d.M + o.bm - 1) / o.bm) * ((d.N + o.bn - 1) / o.bn) * d.batch;
+    if (tiles * 2 < cus) continue;  // leaves most of the chip idle
+    const double cost = (double)((tiles + cus - 1) / cus) * o.cost_per_round;
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = o.t;
+    }
+  }
+  return best;
+}
+
 // Direct-to-LDS engine for an already conforming problem (A and B K-contiguous or B
 // N-contiguous, 16-byte rows, K % 64 == 0, buffer ranges checked by the caller).
 template <typename T, int BL>
 int launch_engine(const GemmDesc& d, hipStream_t stream) {
-  const int64_t big_tiles = ((d.M + 255) / 256) * ((d.N + 255) / 256) * d.batch;
-  const int64_t mid_tiles = ((d.M + 127) / 128) * ((d.N + 127) / 128) * d.batch;
-  const int64_t half_tiles = ((d.M + 63) / 64) * ((d.N + 127) / 128) * d.batch;
-  const int64_t fill = (int64_t)device_cus() * 7 / 8;
-  if (big_tiles >= 192) return launch_buf<T, 256, 256, BL>(d, stream);
-  if (mid_tiles >= fill) return launch_deep<T, 128, 128, 2, 2, 4, BL>(d, stream);
-  if (half_tiles >= fill) return launch_deep<T, 64, 128, 2, 2, 6, BL>(d, stream);
-  return launch_deep<T, 32, 128, 1, 4, 7, BL>(d, stream);
+  switch (pick_tile(d)) {
+    case TILE_256x256: return launch_buf<T, 256, 256, BL>(d, stream);
+    case TILE_256x128: return launch_deep<T, 256, 128, 2, 2, 3, BL>(d, stream);
+    case TILE_128x128: return launch_deep<T, 128, 128, 2, 2, 4, BL>(d, stream);
+    case TILE_64x128: return launch_deep<T, 64, 128, 2, 2, 6, BL>(d, stream);
+    default: return launch_deep<T, 32, 128, 1, 4, 7, BL>(d, stream);
+  }
 }
 
 // Layouts the engines cannot read in place (rows not 16-byte aligned, e.g. K = 4095;
@@ -1109,21 +1149,15 @@ int dispatch_typed(const GemmDesc& d, hipStream_t stream) {
     const int64_t mid_tiles = ((d.M + 127) / 128) * ((d.N + 127) / 128) * d.batch;
     const bool short_k = d.K <= 256;
     const bool small = mid_tiles < 128;
-    if (b_kc && big && buf_ok && !short_k) return launch_buf<T, 256, 256, B_KC>(d, stream);
     // N-contiguous B on the direct-to-LDS engines: B bytes from the tile's first column
     // through the last K-row must fit the 32-bit buffer offsets.
     const bool buf_nc_ok = d.K % 64 == 0 && d.sam * 2 * 256 + d.K * 2 < (1ll << 31) &&
                            d.sbk * 2 * d.K + d.N * 2 < (1ll << 31);
-    if (!b_kc && b_nc && big && buf_nc_ok && !short_k) return launch_buf<T, 256, 256, B_NC>(d, stream);
-    // Mid-size with a long K: the deep ring, 128x128 tiles when they fill the chip,
-    // else 64x128 when those do.
     const bool deep_ok = (b_kc ? buf_ok : buf_nc_ok) && d.K >= 256;
-    const int64_t fill = (int64_t)device_cus() * 7 / 8;
-    const int64_t half_tiles = ((d.M + 63) / 64) * ((d.N + 127) / 128) * d.batch;
-    if (deep_ok && !big && mid_tiles >= fill)
-      return b_kc ? launch_deep<T, 128, 128, 2, 2, 4, B_KC>(d, stream) : launch_deep<T, 128, 128, 2, 2, 4, B_NC>(d, stream);
-    if (deep_ok && !big && half_tiles >= fill)
-      return b_kc ? launch_deep<T, 64, 128, 2, 2, 6, B_KC>(d, stream) : launch_deep<T, 64, 128, 2, 2, 6, B_NC>(d, stream);
+    // Long K and enough tiles to fill half the chip: the direct-to-LDS engines at the
+    // tile shape with the fewest weighted rounds.
+    if (deep_ok && pick_tile(d) != TILE_32x128)
+      return b_kc ? launch_engine<T, B_KC>(d, stream) : launch_engine<T, B_NC>(d, stream);
     // K of one or two 64-wide steps, no epilogue, enough 128x128 tiles to give every
     // CU several: the persistent short-K kernel (16-byte buffer stores need N % 8 == 0
     // and 16-byte aligned C rows; per-tile byte offsets must stay below 2^31).
@@ -1138,8 +1172,8 @@ int dispatch_typed(const GemmDesc& d, hipStream_t stream) {
       const int nk = (int)(d.K / 64);
       const int want = (int)std::min<int64_t>(device_cus() / t32, nk / 4);
       const int per = (nk + want - 1) / want, splits = (nk + per - 1) / per;
-      const int rc = b_kc ? launch_splitk<T, B_KC>(d, splits, per * 64, stream)
-                          : launch_splitk<T, B_NC>(d, splits, per * 64, stream);
+      const int rc = b_kc ? launch_splitk<T, B_KC, 32, 128, 1, 4, 7>(d, splits, per * 64, stream)
+                          : launch_splitk<T, B_NC, 32, 128, 1, 4, 7>(d, splits, per * 64, stream);
       if (rc != KORE_EUNSUPPORTED) return rc;
     }
     // few tiles and a long K: the latency-bound case, on the deep direct-to-LDS ring

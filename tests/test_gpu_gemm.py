@@ -102,12 +102,15 @@ def test_gemm_nc_buffer_engine(gpu, M, N, K, dtype, op, strided):
                                              (1024, 2048, 2048, torch.float16, "gemm_sigmoid"),
                                              (500, 4000, 1024, torch.bfloat16, "gemm_bias"),
                                              (1000, 1000, 1024, torch.bfloat16, "gemm_tanh"),
-                                             (1, 4096, 4096, torch.bfloat16, "gemm")])
+                                             (1, 4096, 4096, torch.bfloat16, "gemm"),
+                                             (1536, 4096, 4096, torch.bfloat16, "gemm"),
+                                             (1500, 4000, 1024, torch.float16, "gemm_bias_gelu"),
+                                             (768, 4096, 4096, torch.bfloat16, "gemm_bias_relu")])
 @pytest.mark.parametrize("layout", ["kn", "nk"])
 def test_gemm_deep_ring(gpu, M, N, K, dtype, op, layout):
-    """Mid-size and small problems with a long K on the deep-ring kernel (128x128 tiles
-    when they fill the chip, else 64x128; 32x128 for small N-contiguous problems), both
-    B layouts ([K,N] and the W.t() view), ragged M and N, fused epilogues."""
+    """Mid-size and small problems with a long K on the deep-ring kernel (256x128,
+    128x128, 64x128 or 32x128 tiles by weighted rounds over the CUs), both B layouts
+    ([K,N] and the W.t() view), ragged M and N, fused epilogues."""
     has_bias, act = kore_amd.GEMM_FUSION_OPS.get(op, (False, "none"))
     g = torch.Generator().manual_seed(M * 7 + N + K)
     sc = 1.0 / K ** 0.5
