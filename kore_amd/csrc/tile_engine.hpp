@@ -722,9 +722,7 @@ struct RingEngine {
       issue(lds, nslot, soff_of(s + NSLOT - 1), soffb_of(s + NSLOT - 1), wave);
       const uint16_t* sA = lds + slot * STAGE + rowA0 * kBK;
       const uint16_t* sB = lds + slot * STAGE + B_OFF;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        u32x4_t af[MI], bf[NI];
+      auto read = [&](int ks, u32x4_t (&af)[MI], u32x4_t (&bf)[NI]) {
 #pragma unroll
         for (int i = 0; i < MI; ++i) af[i] = *(const u32x4_t*)(sA + i * 32 * kBK + offA[i & 1][ks]);
 #pragma unroll
@@ -737,10 +735,20 @@ struct RingEngine {
             bf[j] = *(const u32x4_t*)(sB + rowB0 * kBK + j * 32 * kBK + offB[j & 1][ks]);
           }
         }
+      };
+      // sub-step ks + 1's fragments are read before sub-step ks's MFMAs go out, so LDS
+      // latency hides under them (one wave per SIMD has nothing else to switch to)
+      u32x4_t fa[2][MI], fb[2][NI];
+      read(0, fa[0], fb[0]);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        if (ks + 1 < 4) read(ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
-          for (int j = 0; j < NI; ++j) acc[i][j] = Op::mma32(bf[j], af[i], acc[i][j]);
+          for (int j = 0; j < NI; ++j) acc[i][j] = Op::mma32(fb[ks & 1][j], fa[ks & 1][i], acc[i][j]);
+        __builtin_amdgcn_sched_barrier(0);
       }
       slot = slot + 1 == NSLOT ? 0 : slot + 1;
     }
