@@ -7,8 +7,8 @@
  * allocates device memory": kore_gemm and kore_batched_gemm keep one grow-only scratch
  * buffer per (device, stream) for the packed-operand path (layouts the engines cannot
  * read in place, e.g. K = 4095) and the split-K path (decode-sized M), allocated on
- * first need outside graph capture and kept until the process exits; under capture a
- * buffer that is too small makes them take a path that needs none.  Calls are
+ * first need and kept until the process exits; a stream being captured into a graph
+ * without such a buffer gets a stream-ordered allocation recorded in the graph.  Calls are
  * asynchronous on `stream`.  Return value: KORE_OK, or an error
  * code with a message available from kore_last_error() (per host thread).
  *

@@ -42,9 +42,9 @@ int device_cus() {
 // Scratch for the packed and split-K paths: one grow-only device buffer per (device,
 // stream), kept until the process ends.  Work on one stream runs in order, so the next
 // call on that stream may reuse the buffer as soon as it is enqueued; different streams
-// get different buffers.  Growing synchronises the stream before freeing the old buffer;
-// under graph capture (where allocation is not allowed) a buffer that is too small
-// makes the caller take its fallback path instead.
+// get different buffers.  Growing synchronises the stream before freeing the old buffer.
+// A capturing stream without a large enough buffer gets a stream-ordered allocation
+// that becomes part of the graph (allocated and freed at each replay).
 namespace {
 struct ScratchSlot {
   hipStream_t stream;
@@ -68,9 +68,19 @@ void* scratch_alloc(size_t bytes, hipStream_t stream) {
   if (slot == nullptr) return nullptr;  // more streams than slots: fallback path
   if (slot->ptr != nullptr && slot->bytes >= bytes) return slot->ptr;
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess) {
     (void)hipGetLastError();
     return nullptr;
+  }
+  if (cap != hipStreamCaptureStatusNone) {
+    // under capture: a stream-ordered allocation (a graph memory node), released by
+    // scratch_free in the same graph
+    void* p = nullptr;
+    if (hipMallocAsync(&p, bytes, stream) != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    return p;
   }
   if (slot->ptr != nullptr) {
     if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
@@ -90,7 +100,17 @@ void* scratch_alloc(size_t bytes, hipStream_t stream) {
   return p;
 }
 
-void scratch_free(void*, hipStream_t) {}  // the buffer stays with its stream
+// A cached buffer stays with its stream; a capture-time allocation is freed stream-ordered.
+void scratch_free(void* p, hipStream_t stream) {
+  if (p == nullptr) return;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    for (auto& dev : g_scratch)
+      for (auto& slot : dev)
+        if (slot.ptr == p) return;
+  }
+  (void)hipFreeAsync(p, stream);
+}
 
 }  // namespace kore
 

@@ -396,3 +396,29 @@ def test_gemm_backward_errors(gpu):
     with pytest.raises(ValueError):
         kore_amd.gemm_backward(x, torch.zeros((4, 16), dtype=torch.float16, device=gpu),
                                torch.zeros((8, 4), dtype=torch.bfloat16, device=gpu))
+
+
+def test_scratch_paths_under_graph_capture(gpu):
+    """The packed path (K = 4095) and split-K (M = 1) captured into a HIP graph on a fresh
+    stream take a stream-ordered scratch allocation recorded in the graph.  Every replay,
+    with eager work and synchronisations between replays, matches the eager result bit
+    for bit."""
+    g = torch.Generator().manual_seed(11)
+    a = (torch.randn((512, 4095), generator=g) / 64).bfloat16().to(gpu)
+    b = (torch.randn((4095, 1024), generator=g) / 64).bfloat16().to(gpu)
+    a1 = (torch.randn((1, 4096), generator=g) / 64).bfloat16().to(gpu)
+    b1 = (torch.randn((4096, 2048), generator=g) / 64).bfloat16().to(gpu)
+    e_packed, e_split = kore_amd.gemm(a, b), kore_amd.gemm(a1, b1)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y_packed = kore_amd.gemm(a, b)
+        y_split = kore_amd.gemm(a1, b1)
+    for r in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_packed, e_packed), f"packed replay {r}"
+        assert torch.equal(y_split, e_split), f"split-K replay {r}"
+        other = kore_amd.gemm(a1, b1)  # eager work on the default stream between replays
+        torch.cuda.synchronize()
+        assert torch.equal(other, e_split)
