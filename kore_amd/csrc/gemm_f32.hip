@@ -293,6 +293,33 @@ __global__ void __launch_bounds__(256) gemm_f32_generic_kernel(const F32GenericP
 
 inline bool al16(const void* q) { return ((uintptr_t)q & 15u) == 0; }
 
+// Operands the MFMA kernel cannot read (K % 64 != 0, e.g. the tasks' K = 4095; unaligned
+// rows; transposed or strided operands): out[r][k] = in[r * sr + k * sk] for k < K, 0 for
+// K <= k < Kp (a multiple of 64), rows of Kp floats.  64 x 64 tiles through LDS, loads
+// along whichever index is unit-stride, 16-byte row stores.
+__global__ void __launch_bounds__(256) pack32_kernel(const float* in, int64_t sr, int64_t sk, float* out, int R, int K,
+                                                     int Kp) {
+  __shared__ float t[64][65];  // [r][k]
+  const int tid = threadIdx.x;
+  const int r0 = (int)blockIdx.y * 64, k0 = (int)blockIdx.x * 64;
+  const bool r_unit = sr == 1 && sk != 1;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int u = tid & 63, v = 4 * i + (tid >> 6);
+    const int r = r_unit ? u : v, k = r_unit ? v : u;
+    const int gr = r0 + r, gk = k0 + k;
+    t[r][k] = (gr < R && gk < K) ? in[(int64_t)gr * sr + (int64_t)gk * sk] : 0.0f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int idx = tid + 256 * q, r = idx >> 4, ch = idx & 15;
+    if (r0 + r >= R) continue;
+    *(f32x4v*)(out + (int64_t)(r0 + r) * Kp + k0 + 4 * ch) =
+        f32x4v{t[r][4 * ch], t[r][4 * ch + 1], t[r][4 * ch + 2], t[r][4 * ch + 3]};
+  }
+}
+
 constexpr bool kF32M16 = false;
 
 template <int BM, int BN, bool BNC>
@@ -339,6 +366,44 @@ int launch_gemm_f32(const GemmF32Args& d, hipStream_t st) {
     return b_kc ? pick_f32<false>(p, st) : pick_f32<true>(p, st);
   }
   if (!fits) return set_error(KORE_EUNSUPPORTED, "gemm fp32: dimension >= 2^31");
+  // Large problems in other layouts: pack A to [M, Kp] and B to [N, Kp] (K-contiguous,
+  // zero K tail) in the stream's scratch, then the MFMA kernel.
+  const int64_t Kp = (d.K + kF32BK - 1) / kF32BK * kF32BK;
+  if (d.M * d.N * d.K >= (1ll << 26) && d.K >= kF32BK) {
+    const size_t a_bytes = (size_t)(d.M * Kp * 4 + 255) / 256 * 256;
+    float* ws = (float*)scratch_alloc(a_bytes + (size_t)d.N * Kp * 4, st);
+    if (ws != nullptr) {
+      float* ap = ws;
+      float* bp = (float*)((char*)ws + a_bytes);
+      hipLaunchKernelGGL(pack32_kernel, dim3((unsigned)(Kp / 64), (unsigned)((d.M + 63) / 64)), dim3(256), 0, st,
+                         (const float*)d.a, d.sam, d.sak, ap, (int)d.M, (int)d.K, (int)Kp);
+      int rc = check_launch("pack32_kernel");
+      if (rc == KORE_OK) {
+        // rows of B^T: element (n, k) at b[k * sbk + n * sbn]
+        hipLaunchKernelGGL(pack32_kernel, dim3((unsigned)(Kp / 64), (unsigned)((d.N + 63) / 64)), dim3(256), 0, st,
+                           (const float*)d.b, d.sbn, d.sbk, bp, (int)d.N, (int)d.K, (int)Kp);
+        rc = check_launch("pack32_kernel");
+      }
+      if (rc == KORE_OK) {
+        F32Params p{};
+        p.a = ap;
+        p.b = bp;
+        p.bias = (const float*)d.bias;
+        p.c = (float*)d.c;
+        p.M = (int)d.M;
+        p.N = (int)d.N;
+        p.K = (int)Kp;
+        p.lda = Kp;
+        p.ldb = Kp;
+        p.ldc = d.scm;
+        p.act = d.act;
+        p.vec_store = d.scm % 4 == 0 && al16(d.c);
+        rc = pick_f32<false>(p, st);
+      }
+      scratch_free(ws, st);
+      return rc;
+    }
+  }
   F32GenericParams g{};
   g.a = (const float*)d.a;
   g.b = (const float*)d.b;

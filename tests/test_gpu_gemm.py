@@ -349,7 +349,8 @@ def test_gemm_fusion_fp32_ops(gpu, op):
 @pytest.mark.parametrize("bt", [False, True])
 def test_gemm_fp32_task_shapes(gpu, M, N, K, bt):
     """The fp32 task shapes, with b N-contiguous (the task's layout) or a W.t() view;
-    K = 4095 takes the generic kernel.  Rows are sampled for the oracle."""
+    K = 4095 packs A and B (zero K tail) into scratch for the MFMA kernel.  Rows are
+    sampled for the oracle."""
     g = torch.Generator(device=gpu).manual_seed(K)
     sc = 1.0 / K ** 0.5
     a = torch.randn((M, K), generator=g, device=gpu) * sc
