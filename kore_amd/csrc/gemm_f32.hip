@@ -22,6 +22,7 @@
 // Any other layout, K % 64 != 0 or unaligned rows: a 64x64 FMA tile (generic).
 #include "../../include/kore_amd.h"
 #include "kore_common.hpp"
+#include "tile_engine.hpp"
 
 #include <type_traits>
 
@@ -320,6 +321,173 @@ __global__ void __launch_bounds__(256) pack32_kernel(const float* in, int64_t sr
   }
 }
 
+// ---------------------------------------------------------------------------------
+// Deep-ring fp32 kernel.  The register-staged kernel above stalls once per K step on
+// its LDS stores and the barrier, with one step of loads in flight.  Here an NSLOT-deep
+// ring of 32-float K stages is filled by direct-to-LDS buffer loads NSLOT - 1 stages
+// ahead of the MFMAs (one barrier per stage).  A and K-contiguous B use 128-byte rows
+// with the swz8 chunk swizzle (source side); N-contiguous B is staged as 32 K-rows of
+// BN floats and a lane reads the 4 K values of its column with 4 ds_read_b32.  Wave
+// tile (BM/2) x (BN/2) as 32x32 blocks; within a stage, K group q+1's fragments are
+// read under group q's MFMAs.
+// ---------------------------------------------------------------------------------
+constexpr int kF32RK = 32;  // K floats per ring stage
+
+template <int BM, int BN, int NSLOT, bool BNC>
+__global__ void __launch_bounds__(256) gemm_f32_ring_kernel(const F32Params p) {
+  constexpr int WM = BM / 2, WN = BN / 2, MI = WM / 32, NI = WN / 32;
+  static_assert(MI >= 1 && NI >= 1, "wave tile");
+  constexpr int A_FL = BM * kF32RK, STAGE = (BM + BN) * kF32RK;  // floats
+  constexpr int AJ = BM / 32, BJ = BN / 32;                       // 1 KiB loads per wave per stage
+  constexpr int LPS = AJ + BJ;
+  constexpr int NCR = 256 / BN, NCH = BN / 4;  // N-contiguous B: K-rows and chunks per load
+  static_assert((NSLOT - 2) * LPS <= 63, "vmcnt range");
+  static_assert(NSLOT * STAGE * 4 <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(16))) float lds[NSLOT * STAGE];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lr = lane & 31, hh = lane >> 5;
+  const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int m0 = (bid % p.tiles_m) * BM, n0 = (bid / p.tiles_m) * BN;
+  const int rows_a = min(BM, p.M - m0), rows_b = min(BN, p.N - n0);
+  const int nk = p.K / kF32RK;
+
+  // buffer resources and per-lane byte offsets (rows past the tile re-read its last row,
+  // chunks past N re-read the last chunk: they only feed outputs that are never stored)
+  const __amdgpu_buffer_rsrc_t ra =
+      make_rsrc(p.a + (int64_t)m0 * p.lda, (uint32_t)(((int64_t)(rows_a - 1) * p.lda + p.K) * 4));
+  const __amdgpu_buffer_rsrc_t rb =
+      BNC ? make_rsrc(p.b + n0, (uint32_t)(((int64_t)(p.K - 1) * p.ldb + rows_b) * 4))
+          : make_rsrc(p.b + (int64_t)n0 * p.ldb, (uint32_t)(((int64_t)(rows_b - 1) * p.ldb + p.K) * 4));
+  uint32_t a_voff[AJ], b_voff[BJ];
+#pragma unroll
+  for (int j = 0; j < AJ; ++j) {
+    const int r = (wave + 4 * j) * 8 + (lane >> 3);
+    a_voff[j] = (uint32_t)(((int64_t)min(r, rows_a - 1) * p.lda + 4 * ((lane & 7) ^ swz8(r))) * 4);
+  }
+#pragma unroll
+  for (int j = 0; j < BJ; ++j) {
+    if constexpr (BNC) {
+      const int kr = (wave + 4 * j) * NCR + lane / NCH;
+      b_voff[j] = (uint32_t)(((int64_t)kr * p.ldb + min(4 * (lane % NCH), rows_b - 4)) * 4);
+    } else {
+      const int r = (wave + 4 * j) * 8 + (lane >> 3);
+      b_voff[j] = (uint32_t)(((int64_t)min(r, rows_b - 1) * p.ldb + 4 * ((lane & 7) ^ swz8(r))) * 4);
+    }
+  }
+  const uint32_t b_kstep = BNC ? (uint32_t)(kF32RK * p.ldb * 4) : (uint32_t)(kF32RK * 4);
+  auto issue = [&](int slot, int stage) {
+    const int st = min(stage, nk - 1);  // past the end: re-load the last stage into a free slot
+    float* base = lds + slot * STAGE;
+#pragma unroll
+    for (int j = 0; j < AJ; ++j)
+      buf_lds16(ra, a_voff[j], (uint32_t)st * (kF32RK * 4), (uint16_t*)(base + (wave + 4 * j) * 256));
+#pragma unroll
+    for (int j = 0; j < BJ; ++j)
+      buf_lds16(rb, b_voff[j], (uint32_t)st * b_kstep, (uint16_t*)(base + A_FL + (wave + 4 * j) * 256));
+  };
+
+  // fragment offsets: row R + lr of a 32-row block (R % 32 == 0) has
+  // swz8(R + lr) = (lr & 7) ^ (lr >> 3) ^ (4 * ((R / 32) & 1))
+  const int rowA0 = wm * WM, rowB0 = wn * WN;
+  int offA[2][4], offB[2][4];
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int swa = ((lr & 7) ^ (lr >> 3) ^ (4 * ((wm * MI + par) & 1))) & 7;
+    const int swb = ((lr & 7) ^ (lr >> 3) ^ (4 * ((wn * NI + par) & 1))) & 7;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      offA[par][q] = lr * kF32RK + 4 * ((2 * q + hh) ^ swa);
+      offB[par][q] = lr * kF32RK + 4 * ((2 * q + hh) ^ swb);
+    }
+  }
+
+  f32x16_t acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+#pragma unroll
+  for (int st = 0; st < NSLOT - 1; ++st) issue(st, st);
+  int slot = 0;
+  for (int s = 0; s < nk; ++s) {
+    wait_vmcnt<(NSLOT - 2) * LPS>();
+    exec_barrier();
+    issue(slot == 0 ? NSLOT - 1 : slot - 1, s + NSLOT - 1);
+    const float* sa = lds + slot * STAGE + rowA0 * kF32RK;
+    const float* sb = lds + slot * STAGE + A_FL;
+    // K group q (8 K values): lane half hh holds k = 8q + 4hh + e for e = 0..3
+    auto frags = [&](int q, f32x4v (&fa)[MI], f32x4v (&fb)[NI]) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i) fa[i] = *(const f32x4v*)(sa + i * 32 * kF32RK + offA[i & 1][q]);
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        if constexpr (BNC) {
+          const float* col = sb + (8 * q + 4 * hh) * BN + rowB0 + 32 * j + lr;
+          fb[j] = f32x4v{col[0], col[BN], col[2 * BN], col[3 * BN]};
+        } else {
+          fb[j] = *(const f32x4v*)(sb + (rowB0 + 32 * j) * kF32RK + offB[j & 1][q]);
+        }
+      }
+    };
+    f32x4v af[2][MI], bf[2][NI];
+    frags(0, af[0], bf[0]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (q + 1 < 4) frags(q + 1, af[(q + 1) & 1], bf[(q + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < NI; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[q & 1][j][e], af[q & 1][i][e], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    slot = slot + 1 == NSLOT ? 0 : slot + 1;
+  }
+  wait_vmcnt<0>();  // the clamped trailing loads must land before the kernel ends
+
+  auto epi = [&](auto act_tag) {
+    constexpr int ACT = decltype(act_tag)::value;
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int m = m0 + rowA0 + 32 * i + lr;
+      if (m >= p.M) continue;
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float v[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+          f32_store<ACT>(p, v, m, n0 + rowB0 + 32 * j + 8 * g + 4 * hh);
+        }
+    }
+  };
+  switch (p.act) {
+    case ACT_RELU: epi(std::integral_constant<int, ACT_RELU>{}); break;
+    case ACT_GELU: epi(std::integral_constant<int, ACT_GELU>{}); break;
+    case ACT_SILU: epi(std::integral_constant<int, ACT_SILU>{}); break;
+    case ACT_TANH: epi(std::integral_constant<int, ACT_TANH>{}); break;
+    case ACT_SIGMOID: epi(std::integral_constant<int, ACT_SIGMOID>{}); break;
+    default: epi(std::integral_constant<int, ACT_NONE>{}); break;
+  }
+}
+
+template <int BM, int BN, int NSLOT, bool BNC>
+int launch_f32_ring(F32Params p, hipStream_t st) {
+  p.tiles_m = (p.M + BM - 1) / BM;
+  p.tiles_n = (p.N + BN - 1) / BN;
+  const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n;
+  if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "gemm fp32: grid too large");
+  hipLaunchKernelGGL((gemm_f32_ring_kernel<BM, BN, NSLOT, BNC>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+  return check_launch("gemm_f32_ring_kernel");
+}
+
 constexpr bool kF32M16 = false;
 
 template <int BM, int BN, bool BNC>
@@ -334,9 +502,18 @@ int launch_f32(F32Params p, hipStream_t st) {
 
 template <bool BNC>
 int pick_f32(const F32Params& p, hipStream_t st) {
-  // the largest tile that still gives every CU a tile
+  // the largest tile that still gives every CU a tile; the deep ring whenever its
+  // 32-float stages tile K and the buffer offsets fit 32 bits
   const int64_t t128 = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128);
   const int64_t t12864 = (int64_t)((p.M + 127) / 128) * ((p.N + 63) / 64);
+  const bool ring = p.K % kF32RK == 0 && (int64_t)p.lda * 4 * 128 + (int64_t)p.K * 4 < (1ll << 31) &&
+                    (BNC ? (int64_t)p.ldb * 4 * p.K + (int64_t)p.N * 4 < (1ll << 31)
+                         : (int64_t)p.ldb * 4 * 128 + (int64_t)p.K * 4 < (1ll << 31));
+  if (ring) {
+    if (t128 >= 240) return launch_f32_ring<128, 128, 4, BNC>(p, st);
+    if (t12864 >= 200) return launch_f32_ring<128, 64, 6, BNC>(p, st);
+    return launch_f32_ring<64, 64, 8, BNC>(p, st);
+  }
   if (t128 >= 240) return launch_f32<128, 128, BNC>(p, st);
   if (t12864 >= 200) return launch_f32<128, 64, BNC>(p, st);
   return launch_f32<64, 64, BNC>(p, st);
