@@ -510,8 +510,10 @@ int pick_f32(const F32Params& p, hipStream_t st) {
                     (BNC ? (int64_t)p.ldb * 4 * p.K + (int64_t)p.N * 4 < (1ll << 31)
                          : (int64_t)p.ldb * 4 * 128 + (int64_t)p.K * 4 < (1ll << 31));
   if (ring) {
-    if (t128 >= 240) return launch_f32_ring<128, 128, 4, BNC>(p, st);
-    if (t12864 >= 200) return launch_f32_ring<128, 64, 6, BNC>(p, st);
+    // 64x64 tiles on a 3-stage ring (48 KiB): up to three workgroups share a CU, so
+    // one's LDS reads and barriers overlap another's MFMAs (as fast as 128x128 tiles
+    // at 4096^3 and faster below); few tiles: one deeper ring per CU
+    if (t12864 >= 200) return launch_f32_ring<64, 64, 3, BNC>(p, st);
     return launch_f32_ring<64, 64, 8, BNC>(p, st);
   }
   if (t128 >= 240) return launch_f32<128, 128, BNC>(p, st);
