@@ -41,6 +41,7 @@ struct F32Params {
   int tiles_m, tiles_n;
   int act;
   int vec_store;
+  int kb;  // ring kernel, N-contiguous B: K-rows that exist (rows from kb on read as 0)
 };
 
 constexpr int kF32BK = 64;          // K values per stage
@@ -358,7 +359,7 @@ __global__ void __launch_bounds__(256) gemm_f32_ring_kernel(const F32Params p) {
   const __amdgpu_buffer_rsrc_t ra =
       make_rsrc(p.a + (int64_t)m0 * p.lda, (uint32_t)(((int64_t)(rows_a - 1) * p.lda + p.K) * 4));
   const __amdgpu_buffer_rsrc_t rb =
-      BNC ? make_rsrc(p.b + n0, (uint32_t)(((int64_t)(p.K - 1) * p.ldb + rows_b) * 4))
+      BNC ? make_rsrc(p.b + n0, (uint32_t)(((int64_t)(p.kb - 1) * p.ldb + rows_b) * 4))
           : make_rsrc(p.b + (int64_t)n0 * p.ldb, (uint32_t)(((int64_t)(rows_b - 1) * p.ldb + p.K) * 4));
   uint32_t a_voff[AJ], b_voff[BJ];
 #pragma unroll
@@ -542,6 +543,7 @@ int launch_gemm_f32(const GemmF32Args& d, hipStream_t st) {
     p.ldc = d.scm;
     p.act = d.act;
     p.vec_store = d.scm % 4 == 0 && al16(d.c);
+    p.kb = p.K;
     return b_kc ? pick_f32<false>(p, st) : pick_f32<true>(p, st);
   }
   if (!fits) return set_error(KORE_EUNSUPPORTED, "gemm fp32: dimension >= 2^31");
@@ -549,14 +551,37 @@ int launch_gemm_f32(const GemmF32Args& d, hipStream_t st) {
   // zero K tail) in the stream's scratch, then the MFMA kernel.
   const int64_t Kp = (d.K + kF32BK - 1) / kF32BK * kF32BK;
   if (d.M * d.N * d.K >= (1ll << 26) && d.K >= kF32BK) {
+    // an N-contiguous B with aligned K-rows is read in place by the ring kernel, its
+    // buffer resource ending at the last real K-row (the padded rows read as zero)
+    const bool b_inplace = b_nc && Kp * 4 * 128 + Kp * 4 < (1ll << 31) && d.sbk * 4 * Kp + d.N * 4 < (1ll << 31);
     const size_t a_bytes = (size_t)(d.M * Kp * 4 + 255) / 256 * 256;
-    float* ws = (float*)scratch_alloc(a_bytes + (size_t)d.N * Kp * 4, st);
+    float* ws = (float*)scratch_alloc(a_bytes + (b_inplace ? 0 : (size_t)d.N * Kp * 4), st);
     if (ws != nullptr) {
       float* ap = ws;
       float* bp = (float*)((char*)ws + a_bytes);
       hipLaunchKernelGGL(pack32_kernel, dim3((unsigned)(Kp / 64), (unsigned)((d.M + 63) / 64)), dim3(256), 0, st,
                          (const float*)d.a, d.sam, d.sak, ap, (int)d.M, (int)d.K, (int)Kp);
       int rc = check_launch("pack32_kernel");
+      if (rc == KORE_OK && b_inplace) {
+        F32Params p{};
+        p.a = ap;
+        p.b = (const float*)d.b;
+        p.bias = (const float*)d.bias;
+        p.c = (float*)d.c;
+        p.M = (int)d.M;
+        p.N = (int)d.N;
+        p.K = (int)Kp;
+        p.kb = (int)d.K;
+        p.lda = Kp;
+        p.ldb = d.sbk;
+        p.ldc = d.scm;
+        p.act = d.act;
+        p.vec_store = d.scm % 4 == 0 && al16(d.c);
+        const int64_t t12864 = (d.M + 127) / 128 * ((d.N + 63) / 64);
+        rc = t12864 >= 200 ? launch_f32_ring<64, 64, 3, true>(p, st) : launch_f32_ring<64, 64, 8, true>(p, st);
+        scratch_free(ws, st);
+        return rc;
+      }
       if (rc == KORE_OK) {
         // rows of B^T: element (n, k) at b[k * sbk + n * sbn]
         hipLaunchKernelGGL(pack32_kernel, dim3((unsigned)(Kp / 64), (unsigned)((d.N + 63) / 64)), dim3(256), 0, st,
@@ -577,6 +602,7 @@ int launch_gemm_f32(const GemmF32Args& d, hipStream_t st) {
         p.ldc = d.scm;
         p.act = d.act;
         p.vec_store = d.scm % 4 == 0 && al16(d.c);
+        p.kb = p.K;
         rc = pick_f32<false>(p, st);
       }
       scratch_free(ws, st);
