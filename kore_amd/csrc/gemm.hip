@@ -1155,8 +1155,9 @@ int dispatch_typed(const GemmDesc& d, hipStream_t stream) {
                            d.sbk * 2 * d.K + d.N * 2 < (1ll << 31);
     const bool deep_ok = (b_kc ? buf_ok : buf_nc_ok) && d.K >= 256;
     // Long K and enough tiles to fill half the chip: the direct-to-LDS engines at the
-    // tile shape with the fewest weighted rounds.
-    if (deep_ok && pick_tile(d) != TILE_32x128)
+    // tile shape with the fewest weighted rounds (small problems, under 128 tiles of
+    // 128x128, keep their latency-bound paths below: split-K, the 32x128 rings).
+    if (deep_ok && !small && pick_tile(d) != TILE_32x128)
       return b_kc ? launch_engine<T, B_KC>(d, stream) : launch_engine<T, B_NC>(d, stream);
     // K of one or two 64-wide steps, no epilogue, enough 128x128 tiles to give every
     // CU several: the persistent short-K kernel (16-byte buffer stores need N % 8 == 0
