@@ -8,7 +8,7 @@
  * buffer per (device, stream) for the packed-operand path (layouts the engines cannot
  * read in place, e.g. K = 4095) and the split-K path (decode-sized M), allocated on
  * first need and kept until the process exits; a stream being captured into a graph
- * without such a buffer gets a stream-ordered allocation recorded in the graph.  Calls are
+ * gets a stream-ordered allocation recorded in the graph instead.  Calls are
  * asynchronous on `stream`.  Return value: KORE_OK, or an error
  * code with a message available from kore_last_error() (per host thread).
  *

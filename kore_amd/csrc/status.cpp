@@ -43,8 +43,8 @@ int device_cus() {
 // stream), kept until the process ends.  Work on one stream runs in order, so the next
 // call on that stream may reuse the buffer as soon as it is enqueued; different streams
 // get different buffers.  Growing synchronises the stream before freeing the old buffer.
-// A capturing stream without a large enough buffer gets a stream-ordered allocation
-// that becomes part of the graph (allocated and freed at each replay).
+// A capturing stream always gets a stream-ordered allocation that becomes part of the
+// graph (allocated and freed at each replay).
 namespace {
 struct ScratchSlot {
   hipStream_t stream;
@@ -57,6 +57,22 @@ std::mutex g_scratch_mu;  // host threads may call on different streams at once
 }  // namespace
 
 void* scratch_alloc(size_t bytes, hipStream_t stream) {
+  // Under graph capture: a stream-ordered allocation that becomes part of the graph, so
+  // a replay never shares memory with eager calls or other graphs (a graph may be
+  // replayed on any stream, concurrently with work on the stream it was captured on).
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (cap != hipStreamCaptureStatusNone) {
+    void* p = nullptr;
+    if (hipMallocAsync(&p, bytes, stream) != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    return p;
+  }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
@@ -67,21 +83,6 @@ void* scratch_alloc(size_t bytes, hipStream_t stream) {
     if (g_scratch[dev][i].ptr == nullptr) slot = &g_scratch[dev][i];
   if (slot == nullptr) return nullptr;  // more streams than slots: fallback path
   if (slot->ptr != nullptr && slot->bytes >= bytes) return slot->ptr;
-  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &cap) != hipSuccess) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  if (cap != hipStreamCaptureStatusNone) {
-    // under capture: a stream-ordered allocation (a graph memory node), released by
-    // scratch_free in the same graph
-    void* p = nullptr;
-    if (hipMallocAsync(&p, bytes, stream) != hipSuccess || p == nullptr) {
-      (void)hipGetLastError();
-      return nullptr;
-    }
-    return p;
-  }
   if (slot->ptr != nullptr) {
     if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
     (void)hipFree(slot->ptr);

@@ -411,15 +411,24 @@ def test_scratch_paths_under_graph_capture(gpu):
     b1 = (torch.randn((4096, 2048), generator=g) / 64).bfloat16().to(gpu)
     e_packed, e_split = kore_amd.gemm(a, b), kore_amd.gemm(a1, b1)
     torch.cuda.synchronize()
+    cap = torch.cuda.Stream()
+    with torch.cuda.stream(cap):  # the capture stream owns a cached buffer before capture
+        assert torch.equal(kore_amd.gemm(a, b), e_packed)
+    torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=cap):
         y_packed = kore_amd.gemm(a, b)
         y_split = kore_amd.gemm(a1, b1)
+    other_stream = torch.cuda.Stream()
     for r in range(4):
-        graph.replay()
+        with torch.cuda.stream(other_stream):
+            graph.replay()  # replayed on another stream while the capture stream works
+        with torch.cuda.stream(cap):
+            eager = kore_amd.gemm(a, b)
         torch.cuda.synchronize()
         assert torch.equal(y_packed, e_packed), f"packed replay {r}"
         assert torch.equal(y_split, e_split), f"split-K replay {r}"
+        assert torch.equal(eager, e_packed), f"eager on the capture stream {r}"
         other = kore_amd.gemm(a1, b1)  # eager work on the default stream between replays
         torch.cuda.synchronize()
         assert torch.equal(other, e_split)
