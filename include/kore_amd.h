@@ -7,8 +7,8 @@
  * allocates device memory": kore_gemm and kore_batched_gemm keep one grow-only scratch
  * buffer per (device, stream) for the packed-operand path (layouts the engines cannot
  * read in place, e.g. K = 4095) and the split-K path (decode-sized M), allocated on
- * first need and kept until the process exits; a stream being captured into a graph
- * gets a stream-ordered allocation recorded in the graph instead.  Calls are
+ * first need and kept until the process exits.  Under graph capture they take paths
+ * that need no scratch (the generic kernel, the non-split kernels).  Calls are
  * asynchronous on `stream`.  Return value: KORE_OK, or an error
  * code with a message available from kore_last_error() (per host thread).
  *

@@ -150,9 +150,9 @@ int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 // Compute units of the current device (cached per device; 256 on MI355X).
 int device_cus();
-// Per-(device, stream) scratch, valid until the next scratch_alloc on that stream (a
-// capture-time allocation until its scratch_free); nullptr when unavailable (the caller
-// falls back).  Every scratch_alloc is paired with a scratch_free on the same stream.
+// Per-(device, stream) scratch, valid until the next scratch_alloc on that stream;
+// nullptr under graph capture or when unavailable (the caller falls back).  Every
+// scratch_alloc is paired with a scratch_free on the same stream.
 void* scratch_alloc(size_t bytes, hipStream_t stream);
 void scratch_free(void* p, hipStream_t stream);
 

@@ -43,8 +43,7 @@ int device_cus() {
 // stream), kept until the process ends.  Work on one stream runs in order, so the next
 // call on that stream may reuse the buffer as soon as it is enqueued; different streams
 // get different buffers.  Growing synchronises the stream before freeing the old buffer.
-// A capturing stream always gets a stream-ordered allocation that becomes part of the
-// graph (allocated and freed at each replay).
+// A capturing stream gets none (see scratch_alloc).
 namespace {
 struct ScratchSlot {
   hipStream_t stream;
@@ -57,21 +56,14 @@ std::mutex g_scratch_mu;  // host threads may call on different streams at once
 }  // namespace
 
 void* scratch_alloc(size_t bytes, hipStream_t stream) {
-  // Under graph capture: a stream-ordered allocation that becomes part of the graph, so
-  // a replay never shares memory with eager calls or other graphs (a graph may be
-  // replayed on any stream, concurrently with work on the stream it was captured on).
+  // Under graph capture: no scratch, so the caller takes a path that needs none.  A
+  // captured graph may be replayed on any stream, concurrently with eager work on the
+  // stream it was captured on, so it must not hold the cached buffer; graphs holding
+  // stream-ordered allocation nodes instead faulted on replay on this platform.
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &cap) != hipSuccess) {
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
     (void)hipGetLastError();
     return nullptr;
-  }
-  if (cap != hipStreamCaptureStatusNone) {
-    void* p = nullptr;
-    if (hipMallocAsync(&p, bytes, stream) != hipSuccess || p == nullptr) {
-      (void)hipGetLastError();
-      return nullptr;
-    }
-    return p;
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   int dev = 0;
@@ -101,17 +93,7 @@ void* scratch_alloc(size_t bytes, hipStream_t stream) {
   return p;
 }
 
-// A cached buffer stays with its stream; a capture-time allocation is freed stream-ordered.
-void scratch_free(void* p, hipStream_t stream) {
-  if (p == nullptr) return;
-  {
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    for (auto& dev : g_scratch)
-      for (auto& slot : dev)
-        if (slot.ptr == p) return;
-  }
-  (void)hipFreeAsync(p, stream);
-}
+void scratch_free(void*, hipStream_t) {}  // the buffer stays with its stream
 
 }  // namespace kore
 
