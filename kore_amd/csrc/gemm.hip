@@ -123,7 +123,6 @@ template <typename T, int BL, int BM, int BN>
 __global__ void __launch_bounds__(kEngineThreads)
     gemm_tile_kernel(const TileParams p) {
   using E = TileEngine<T, BM, BN, 2, 2, BL>;
-  using Op = MfmaOp<T>;
   constexpr int MI = E::MI, NI = E::NI;
   __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
 
@@ -388,19 +387,6 @@ __global__ void __launch_bounds__(256) gemm_ring_kernel(const TileParams p) {
 // past the last row block (when SEG does not divide it) load the last block again and
 // store nothing.
 // ---------------------------------------------------------------------------------
-// Wait until at most n (>= 0) vector-memory ops are outstanding, n rounded down to a
-// multiple of 4 and capped at 60: waiting for fewer is always safe, and with in-order
-// retirement a cap below the number of ops issued after the awaited one still implies it.
-__device__ __forceinline__ void wait_vmcnt_le(int n) {
-  if (n >= 60) wait_vmcnt<60>();
-  else if (n >= 48) { if (n >= 56) wait_vmcnt<56>(); else if (n >= 52) wait_vmcnt<52>(); else wait_vmcnt<48>(); }
-  else if (n >= 32) { if (n >= 44) wait_vmcnt<44>(); else if (n >= 40) wait_vmcnt<40>(); else if (n >= 36) wait_vmcnt<36>(); else wait_vmcnt<32>(); }
-  else if (n >= 16) { if (n >= 28) wait_vmcnt<28>(); else if (n >= 24) wait_vmcnt<24>(); else if (n >= 20) wait_vmcnt<20>(); else wait_vmcnt<16>(); }
-  else if (n >= 12) wait_vmcnt<12>();
-  else if (n >= 8) wait_vmcnt<8>();
-  else if (n >= 4) wait_vmcnt<4>();
-  else wait_vmcnt<0>();
-}
 
 template <typename T, int NKS, int BL>
 __global__ void __launch_bounds__(512) gemm_shortk_kernel(const TileParams p, const int seg) {

@@ -300,7 +300,6 @@ template <int MODE, int BM, int BN, int WM, int WN>
 __global__ void __launch_bounds__(kEngineThreads)
     moe_gemm_kernel(const MoeGemmParams p) {
   using E = TileEngine<BF16, BM, BN, WM, WN, B_KC, MODE == MOE_DOWN ? 2 : 1>;
-  using Op = MfmaOp<BF16>;
   constexpr int MI = E::MI, NI = E::NI;
   __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -366,7 +365,6 @@ __global__ void __launch_bounds__(256)
     moe_buf_kernel(const MoeGemmParams p) {
   constexpr int AP = (MODE == MOE_DOWN) ? 2 : 1;
   using E = BufPipeEngine<BF16, BM, BN, 2, 2, AP>;
-  using Op = MfmaOp<BF16>;
   constexpr int MI = E::MI, NI = E::NI;
   __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
