@@ -632,59 +632,117 @@ struct GenericParams {
   int act;
 };
 
+// ---------------------------------------------------------------------------------
+// Generic MFMA kernel: any strides, any K (the fallback for layouts the engines cannot
+// read and for K tails under graph capture, where no scratch is taken).  128x128 tiles,
+// 4 waves of 64x64, K steps of 32.  Operands are read element by element, 16 per thread
+// per operand and step, along whichever index is unit-stride (so a wave reads 128
+// contiguous bytes), every read bounds-checked (zero outside); the next step is loaded
+// into registers while the current one is multiplied.  LDS rows of 32 values with a
+// stride of 40 (80 bytes): a 16-byte fragment read by 8 consecutive rows covers all 32
+// banks once.
+// ---------------------------------------------------------------------------------
+constexpr int kGenBK = 32, kGenLd = 40;
+
 template <typename T>
-__global__ void __launch_bounds__(256) gemm_generic_kernel(const GenericParams p) {
+__global__ void __launch_bounds__(256) gemm_generic_mfma_kernel(const GenericParams p) {
   using Op = MfmaOp<T>;
-  __shared__ float sA[16][64 + 1];
-  __shared__ float sB[16][64 + 1];
-  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64, z = blockIdx.z;
-  const uint16_t* A = p.a + z * p.sa;
-  const uint16_t* B = p.b + z * p.sb;
-  uint16_t* C = p.c + z * p.sc;
-  float acc[4][4] = {};
-  for (int k0 = 0; k0 < p.K; k0 += 16) {
-    for (int q = tid; q < 16 * 64; q += 256) {
-      const int kk = q / 64, mm = q % 64;
-      const int gm = m0 + mm, gk = k0 + kk;
-      sA[kk][mm] = (gm < p.M && gk < p.K) ? Op::to_f32(A[gm * p.sam + gk * p.sak]) : 0.0f;
-      const int gn = n0 + mm;
-      sB[kk][mm] = (gn < p.N && gk < p.K) ? Op::to_f32(B[gk * p.sbk + gn * p.sbn]) : 0.0f;
+  __shared__ __attribute__((aligned(16))) uint16_t sA[128 * kGenLd];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[128 * kGenLd];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = (int)blockIdx.y * 128, n0 = (int)blockIdx.x * 128, z = (int)blockIdx.z;
+  const uint16_t* A = p.a + (int64_t)z * p.sa;
+  const uint16_t* B = p.b + (int64_t)z * p.sb;
+  uint16_t* C = p.c + (int64_t)z * p.sc;
+  // element e (0..15) of a thread: tile row and K index; the unit-stride index runs
+  // fastest across the lanes
+  const bool a_rows = p.sak != 1 && p.sam == 1;  // A's M index is the unit-stride one
+  const bool b_rows = p.sbk != 1 && p.sbn == 1;  // B's N index is the unit-stride one
+  auto a_idx = [&](int e, int& r, int& k) {
+    const int q = e * 256 + tid;  // 0 .. 4095
+    if (a_rows) { r = q & 127; k = q >> 7; } else { k = q & 31; r = q >> 5; }
+  };
+  auto b_idx = [&](int e, int& r, int& k) {
+    const int q = e * 256 + tid;
+    if (b_rows) { r = q & 127; k = q >> 7; } else { k = q & 31; r = q >> 5; }
+  };
+  uint16_t ra[16], rb[16];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      int r, k;
+      a_idx(e, r, k);
+      const int gm = m0 + r, gk = k0 + k;
+      ra[e] = (gm < p.M && gk < p.K) ? A[(int64_t)gm * p.sam + (int64_t)gk * p.sak] : (uint16_t)0;
+      b_idx(e, r, k);
+      const int gn = n0 + r, gkb = k0 + k;
+      rb[e] = (gn < p.N && gkb < p.K) ? B[(int64_t)gkb * p.sbk + (int64_t)gn * p.sbn] : (uint16_t)0;
     }
-    __syncthreads();
+  };
+  auto store = [&]() {
 #pragma unroll
-    for (int kk = 0; kk < 16; ++kk) {
-      float av[4], bv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = sA[kk][ty * 4 + i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = sB[kk][tx * 4 + j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+    for (int e = 0; e < 16; ++e) {
+      int r, k;
+      a_idx(e, r, k);
+      sA[r * kGenLd + k] = ra[e];
+      b_idx(e, r, k);
+      sB[r * kGenLd + k] = rb[e];
     }
+  };
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  const int lr = lane & 31, hh = lane >> 5;
+  load(0);
+  for (int k0 = 0; k0 < p.K; k0 += kGenBK) {
+    __syncthreads();  // the previous step's fragment reads are done
+    store();
     __syncthreads();
+    if (k0 + kGenBK < p.K) load(k0 + kGenBK);
+#pragma unroll
+    for (int ks = 0; ks < kGenBK / 16; ++ks) {
+      u32x4_t af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = *(const u32x4_t*)(sA + (wm * 64 + 32 * i + lr) * kGenLd + 16 * ks + 8 * hh);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bf[j] = *(const u32x4_t*)(sB + (wn * 64 + 32 * j + lr) * kGenLd + 16 * ks + 8 * hh);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = Op::mma32(bf[j], af[i], acc[i][j]);
+    }
   }
+  auto epi = [&](auto act_tag) {
+    constexpr int ACT = decltype(act_tag)::value;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int gm = m0 + ty * 4 + i;
-    if (gm >= p.M) continue;
+    for (int i = 0; i < 2; ++i) {
+      const int gm = m0 + wm * 64 + out_row(i, lane);
+      if (gm >= p.M) continue;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int gn = n0 + tx * 4 + j;
-      if (gn >= p.N) continue;
-      float v = acc[i][j] + (p.bias ? Op::to_f32(p.bias[gn]) : 0.0f);
-      switch (p.act) {
-        case ACT_RELU: v = apply_act<ACT_RELU>(v); break;
-        case ACT_GELU: v = apply_act<ACT_GELU>(v); break;
-        case ACT_SILU: v = apply_act<ACT_SILU>(v); break;
-        case ACT_TANH: v = apply_act<ACT_TANH>(v); break;
-        case ACT_SIGMOID: v = apply_act<ACT_SIGMOID>(v); break;
-        default: break;
-      }
-      C[gm * p.scm + gn] = (uint16_t)(Op::pack2(v, 0.0f) & 0xffffu);
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int gn = n0 + wn * 64 + out_col(j, g, lane) + e;
+            if (gn >= p.N) continue;
+            const float v = apply_act<ACT>(acc[i][j][4 * g + e] + (p.bias ? Op::to_f32(p.bias[gn]) : 0.0f));
+            C[(int64_t)gm * p.scm + gn] = (uint16_t)(Op::pack2(v, 0.0f) & 0xffffu);
+          }
     }
+  };
+  switch (p.act) {
+    case ACT_RELU: epi(std::integral_constant<int, ACT_RELU>{}); break;
+    case ACT_GELU: epi(std::integral_constant<int, ACT_GELU>{}); break;
+    case ACT_SILU: epi(std::integral_constant<int, ACT_SILU>{}); break;
+    case ACT_TANH: epi(std::integral_constant<int, ACT_TANH>{}); break;
+    case ACT_SIGMOID: epi(std::integral_constant<int, ACT_SIGMOID>{}); break;
+    default: epi(std::integral_constant<int, ACT_NONE>{}); break;
   }
 }
 
@@ -970,9 +1028,9 @@ int launch_generic(const GemmDesc& d, hipStream_t stream) {
   p.sc = d.sc;
   p.act = d.act;
   if (d.batch > 65535) return set_error(KORE_EUNSUPPORTED, "gemm: batch > 65535 on the generic path");
-  dim3 grid((unsigned)((d.N + 63) / 64), (unsigned)((d.M + 63) / 64), (unsigned)d.batch);
-  hipLaunchKernelGGL(gemm_generic_kernel<T>, grid, dim3(256), 0, stream, p);
-  return check_launch("gemm_generic_kernel");
+  dim3 grid((unsigned)((d.N + 127) / 128), (unsigned)((d.M + 127) / 128), (unsigned)d.batch);
+  hipLaunchKernelGGL(gemm_generic_mfma_kernel<T>, grid, dim3(256), 0, stream, p);
+  return check_launch("gemm_generic_mfma_kernel");
 }
 
 // Split-K launch (batch 1): `splits` slices of `kper` (a multiple of 64) K elements on

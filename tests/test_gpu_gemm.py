@@ -204,6 +204,36 @@ def test_gemm_splitk(gpu, M, N, K, dtype, op, layout):
     assert torch.equal(out, kore_amd.gemm_fused(*args))
 
 
+@pytest.mark.parametrize("M,N,K,dtype,op,a_t,b_layout", [(512, 512, 511, torch.bfloat16, "gemm_bias_gelu", False, "kn"),
+                                                           (200, 300, 1001, torch.float16, "gemm_relu", True, "nk"),
+                                                           (130, 129, 77, torch.bfloat16, "gemm", True, "odd"),
+                                                           (1, 257, 33, torch.float16, "gemm_bias_silu", False, "odd")])
+def test_gemm_generic_mfma(gpu, M, N, K, dtype, op, a_t, b_layout):
+    """Problems too small for a pack pass in layouts the engines cannot read (odd K,
+    transposed A, B rows with an odd stride) run the generic MFMA kernel: element reads
+    along the unit-stride index, every read bounds-checked, ragged tiles on every edge."""
+    has_bias, act = kore_amd.GEMM_FUSION_OPS.get(op, (False, "none"))
+    g = torch.Generator().manual_seed(M + N + K + 7)
+    sc = 1.0 / K ** 0.5
+    a = (torch.randn((M, K), generator=g) * sc).to(dtype)
+    ad = a.t().contiguous().to(gpu).t() if a_t else a.to(gpu)
+    if b_layout == "kn":
+        b = (torch.randn((K, N), generator=g) * sc).to(dtype)
+        bd = b.to(gpu)
+    elif b_layout == "nk":
+        w = (torch.randn((N, K), generator=g) * sc).to(dtype)
+        b, bd = w.t(), w.to(gpu).t()
+    else:
+        full = (torch.randn((K, N + 5), generator=g) * sc).to(dtype)
+        b, bd = full[:, 2:2 + N], full.to(gpu)[:, 2:2 + N]
+    bias = torch.randn((N,), generator=g).to(dtype) if has_bias else None
+    out = kore_amd.gemm_fused(ad, bd, bias.to(gpu) if has_bias else None, act)
+    ref = gemm_fusion_ref(a, b, bias, act)
+    dt = "bf16" if dtype == torch.bfloat16 else "fp16"
+    verdict(out, ref, "gemm_fusion", dt, f"generic {op} {M}x{N}x{K} a_t={a_t} {b_layout}")
+    pair_only(out, ref, dt, f"generic {op} {M}x{N}x{K}")
+
+
 def test_batched_packed_path(gpu):
     """A batched problem with an odd K runs the packed path per batch."""
     from oracle.gemm import batched_gemm_ref
