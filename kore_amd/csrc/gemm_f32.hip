@@ -243,53 +243,106 @@ struct F32GenericParams {
   int act;
 };
 
+// Generic fp32 kernel on the fp32 matrix cores: any strides, any K (layouts the MFMA
+// kernels cannot read when the problem is too small for a pack pass, and K tails under
+// graph capture, where no scratch is taken).  128x128 tiles, 4 waves of 64x64, K steps of
+// 16; operands read element by element along whichever index is unit-stride (a wave
+// reads 256 contiguous bytes), every read bounds-checked, the next step prefetched into
+// registers.  LDS rows of 16 floats at a stride of 20: a 16-byte fragment read by 8
+// consecutive rows covers all 32 banks once.  K group q: lane half hh holds
+// k = 8q + 4hh + e, which MFMA e consumes (the same map for A and B).
+constexpr int kF32GK = 16, kF32GLd = 20;
+
 __global__ void __launch_bounds__(256) gemm_f32_generic_kernel(const F32GenericParams p) {
-  __shared__ float sA[16][64 + 1];
-  __shared__ float sB[16][64 + 1];
-  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
-  float acc[4][4] = {};
-  for (int k0 = 0; k0 < p.K; k0 += 16) {
-    for (int q = tid; q < 16 * 64; q += 256) {
-      const int kk = q / 64, mm = q % 64;
-      const int gm = m0 + mm, gk = k0 + kk, gn = n0 + mm;
-      sA[kk][mm] = (gm < p.M && gk < p.K) ? p.a[(int64_t)gm * p.sam + (int64_t)gk * p.sak] : 0.0f;
-      sB[kk][mm] = (gn < p.N && gk < p.K) ? p.b[(int64_t)gk * p.sbk + (int64_t)gn * p.sbn] : 0.0f;
+  __shared__ __attribute__((aligned(16))) float sA[128 * kF32GLd];
+  __shared__ __attribute__((aligned(16))) float sB[128 * kF32GLd];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lr = lane & 31, hh = lane >> 5;
+  const int m0 = (int)blockIdx.y * 128, n0 = (int)blockIdx.x * 128;
+  const bool a_rows = p.sak != 1 && p.sam == 1;  // A's M index is the unit-stride one
+  const bool b_rows = p.sbk != 1 && p.sbn == 1;  // B's N index is the unit-stride one
+  auto idx = [&](bool rows, int e, int& r, int& k) {
+    const int q = e * 256 + tid;  // 0 .. 2047
+    if (rows) { r = q & 127; k = q >> 7; } else { k = q & 15; r = q >> 4; }
+  };
+  float ra[8], rb[8];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      int r, k;
+      idx(a_rows, e, r, k);
+      const int gm = m0 + r, gka = k0 + k;
+      ra[e] = (gm < p.M && gka < p.K) ? p.a[(int64_t)gm * p.sam + (int64_t)gka * p.sak] : 0.0f;
+      idx(b_rows, e, r, k);
+      const int gn = n0 + r, gkb = k0 + k;
+      rb[e] = (gn < p.N && gkb < p.K) ? p.b[(int64_t)gkb * p.sbk + (int64_t)gn * p.sbn] : 0.0f;
     }
-    __syncthreads();
+  };
+  auto store = [&]() {
 #pragma unroll
-    for (int kk = 0; kk < 16; ++kk) {
-      float av[4], bv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = sA[kk][ty * 4 + i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = sB[kk][tx * 4 + j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+    for (int e = 0; e < 8; ++e) {
+      int r, k;
+      idx(a_rows, e, r, k);
+      sA[r * kF32GLd + k] = ra[e];
+      idx(b_rows, e, r, k);
+      sB[r * kF32GLd + k] = rb[e];
     }
+  };
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  load(0);
+  for (int k0 = 0; k0 < p.K; k0 += kF32GK) {
+    __syncthreads();  // the previous step's fragment reads are done
+    store();
     __syncthreads();
+    if (k0 + kF32GK < p.K) load(k0 + kF32GK);
+#pragma unroll
+    for (int q = 0; q < kF32GK / 8; ++q) {
+      f32x4v af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = *(const f32x4v*)(sA + (wm * 64 + 32 * i + lr) * kF32GLd + 8 * q + 4 * hh);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bf[j] = *(const f32x4v*)(sB + (wn * 64 + 32 * j + lr) * kF32GLd + 8 * q + 4 * hh);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[j][e], af[i][e], acc[i][j], 0, 0, 0);
+    }
   }
+  auto epi = [&](auto act_tag) {
+    constexpr int ACT = decltype(act_tag)::value;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int gm = m0 + ty * 4 + i;
-    if (gm >= p.M) continue;
+    for (int i = 0; i < 2; ++i) {
+      const int gm = m0 + wm * 64 + 32 * i + lr;
+      if (gm >= p.M) continue;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int gn = n0 + tx * 4 + j;
-      if (gn >= p.N) continue;
-      float v = acc[i][j] + (p.bias ? p.bias[gn] : 0.0f);
-      switch (p.act) {
-        case ACT_RELU: v = apply_act<ACT_RELU>(v); break;
-        case ACT_GELU: v = apply_act<ACT_GELU>(v); break;
-        case ACT_SILU: v = apply_act<ACT_SILU>(v); break;
-        case ACT_TANH: v = apply_act<ACT_TANH>(v); break;
-        case ACT_SIGMOID: v = apply_act<ACT_SIGMOID>(v); break;
-        default: break;
-      }
-      p.c[(int64_t)gm * p.scm + gn] = v;
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int gn = n0 + wn * 64 + 32 * j + 8 * g + 4 * hh + e;
+            if (gn >= p.N) continue;
+            p.c[(int64_t)gm * p.scm + gn] = apply_act<ACT>(acc[i][j][4 * g + e] + (p.bias ? p.bias[gn] : 0.0f));
+          }
     }
+  };
+  switch (p.act) {
+    case ACT_RELU: epi(std::integral_constant<int, ACT_RELU>{}); break;
+    case ACT_GELU: epi(std::integral_constant<int, ACT_GELU>{}); break;
+    case ACT_SILU: epi(std::integral_constant<int, ACT_SILU>{}); break;
+    case ACT_TANH: epi(std::integral_constant<int, ACT_TANH>{}); break;
+    case ACT_SIGMOID: epi(std::integral_constant<int, ACT_SIGMOID>{}); break;
+    default: epi(std::integral_constant<int, ACT_NONE>{}); break;
   }
 }
 
@@ -623,7 +676,7 @@ int launch_gemm_f32(const GemmF32Args& d, hipStream_t st) {
   g.sbn = d.sbn;
   g.scm = d.scm;
   g.act = d.act;
-  dim3 grid((unsigned)((d.N + 63) / 64), (unsigned)((d.M + 63) / 64));
+  dim3 grid((unsigned)((d.N + 127) / 128), (unsigned)((d.M + 127) / 128));
   hipLaunchKernelGGL(gemm_f32_generic_kernel, grid, dim3(256), 0, st, g);
   return check_launch("gemm_f32_generic_kernel");
 }

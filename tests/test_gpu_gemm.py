@@ -234,6 +234,34 @@ def test_gemm_generic_mfma(gpu, M, N, K, dtype, op, a_t, b_layout):
     pair_only(out, ref, dt, f"generic {op} {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("M,N,K,op,a_t,b_layout", [(300, 200, 77, "gemm_bias_gelu", True, "kn"),
+                                                    (257, 130, 1001, "gemm_sigmoid", False, "odd"),
+                                                    (1, 300, 64, "gemm_bias", False, "nk"),
+                                                    (129, 257, 130, "gemm_relu", True, "odd")])
+def test_gemm_fp32_generic_mfma(gpu, M, N, K, op, a_t, b_layout):
+    """fp32 problems the ring kernel cannot read and too small for a pack pass run the
+    generic fp32 MFMA kernel (element reads along the unit-stride index, bounds-checked,
+    ragged tiles on every edge) at the fp32 gate."""
+    has_bias, act = kore_amd.GEMM_FUSION_OPS.get(op, (False, "none"))
+    g = torch.Generator().manual_seed(M * 3 + N + K)
+    sc = 1.0 / K ** 0.5
+    a = torch.randn((M, K), generator=g) * sc
+    ad = a.t().contiguous().to(gpu).t() if a_t else a.to(gpu)
+    if b_layout == "kn":
+        b = torch.randn((K, N), generator=g) * sc
+        bd = b.to(gpu)
+    elif b_layout == "nk":
+        w = torch.randn((N, K), generator=g) * sc
+        b, bd = w.t(), w.to(gpu).t()
+    else:
+        full = torch.randn((K, N + 3), generator=g) * sc
+        b, bd = full[:, 1:1 + N], full.to(gpu)[:, 1:1 + N]
+    bias = torch.randn((N,), generator=g) if has_bias else None
+    out = kore_amd.gemm_fused(ad, bd, bias.to(gpu) if has_bias else None, act)
+    ref = gemm_fusion_ref(a, b, bias, act)
+    verdict(out, ref, "gemm_fusion_fp32", "fp32", f"fp32 generic {op} {M}x{N}x{K} a_t={a_t} {b_layout}")
+
+
 def test_batched_packed_path(gpu):
     """A batched problem with an odd K runs the packed path per batch."""
     from oracle.gemm import batched_gemm_ref
