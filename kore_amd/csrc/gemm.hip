@@ -345,7 +345,7 @@ __global__ void __launch_bounds__(256) gemm_ring_kernel(const TileParams p) {
   eng.ra = make_rsrc(A, (uint32_t)(((int64_t)(rows_a - 1) * p.lda + p.K) * 2));
   eng.rb = make_rsrc(B, (uint32_t)(((int64_t)(rows_b - 1) * p.ldb + p.K) * 2));
   const int ar = E::a_row(wave, lane);
-  eng.a_voff = (uint32_t)(((int64_t)min(ar, rows_a - 1) * p.lda + 8 * E::chunk(ar, lane)) * 2);
+  eng.a_voff[0] = (uint32_t)(((int64_t)min(ar, rows_a - 1) * p.lda + 8 * E::chunk(ar, lane)) * 2);
 #pragma unroll
   for (int j = 0; j < E::BJ; ++j) {
     const int r = E::b_row(wave, lane, j);

@@ -445,17 +445,17 @@ __global__ void __launch_bounds__(256)
 }
 
 // Decode path (32-row blocks): weight streaming on the skinny ring engine.  Grid =
-// ksplit x ntiles x max_mblocks; a workgroup multiplies one 32-slot block by BN rows
+// ksplit x ntiles x max_mblocks; a workgroup multiplies one BM-slot block (32 or 64) by BN rows
 // of its expert's weights over K / ksplit, so w1/w2 are streamed once per block with
 // NSLOT-1 stages in flight per CU.  The down projection splits K so its grid (32
 // column tiles per block) covers the CUs; split k writes its own Yw slab, summed in
 // fixed order by the combine.
-template <int MODE, int BN, int NSLOT>
+template <int MODE, int BN, int NSLOT, int BM>
 __global__ void __launch_bounds__(256)
     moe_decode_kernel(const MoeGemmParams p) {
   constexpr int AP = (MODE == MOE_DOWN) ? 2 : 1;
-  using E = SkinnyRingEngine<BF16, BN, AP, NSLOT>;
-  constexpr int NI = E::NI;
+  using E = SkinnyRingEngine<BF16, BN, AP, NSLOT, BM>;
+  constexpr int MI = E::MI, NI = E::NI;
   __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
@@ -468,18 +468,25 @@ __global__ void __launch_bounds__(256)
   const int pos0 = mb * E::BM;
 
   E eng;
-  const int ar = E::a_row(wave, lane);
   // A: gathered token rows (gate_up, plain) or the H planes of this block (down)
   if constexpr (MODE != MOE_DOWN) {
     eng.ra = make_rsrc(p.x, (uint32_t)((int64_t)p.T * p.ldx * 2));
-    const int sl = p.sorted[pos0 + ar];
-    const int64_t row = (sl < p.S) ? sl / p.topk : 0;  // padding rows read token 0; never stored
-    eng.a_voff = (uint32_t)((row * p.ldx + 8 * E::chunk(ar, lane)) * 2);
+#pragma unroll
+    for (int j = 0; j < E::AJ; ++j) {
+      const int ar = E::a_row(wave, lane, j);
+      const int sl = p.sorted[pos0 + ar];
+      const int64_t row = (sl < p.S) ? sl / p.topk : 0;  // padding rows read token 0; never stored
+      eng.a_voff[j] = (uint32_t)((row * p.ldx + 8 * E::chunk(ar, lane)) * 2);
+    }
   } else {
     const uint32_t tile_bytes = (uint32_t)((int64_t)E::BM * p.ldx * 2);
     eng.ra = make_rsrc(p.x + (int64_t)pos0 * p.ldx, tile_bytes);
     eng.ra2 = make_rsrc(p.h_lo + (int64_t)pos0 * p.ldx, tile_bytes);
-    eng.a_voff = (uint32_t)(((int64_t)ar * p.ldx + 8 * E::chunk(ar, lane)) * 2);
+#pragma unroll
+    for (int j = 0; j < E::AJ; ++j) {
+      const int ar = E::a_row(wave, lane, j);
+      eng.a_voff[j] = (uint32_t)(((int64_t)ar * p.ldx + 8 * E::chunk(ar, lane)) * 2);
+    }
   }
   // B: interleaved gate/up rows of w1[e] (gate_up) or consecutive rows of w[e]
   int n0;
@@ -508,12 +515,12 @@ __global__ void __launch_bounds__(256)
     }
   }
   const int kper = p.K / p.ksplit;
-  f32x16_t acc[1][NI];
+  f32x16_t acc[MI][NI];
   E::zero(acc);
   eng.mainloop(lds, ks * kper, (ks + 1) * kper, acc);
   MoeGemmParams q = p;
   q.yw = p.yw + (int64_t)ks * p.S * p.Nout;
-  moe_epilogue<MODE, 1, NI, E::BM, E::WCOLS>(acc, lds, q, pos0, n0, 0, wave, wave, lane);
+  moe_epilogue<MODE, MI, NI, E::BM, E::WCOLS>(acc, lds, q, pos0, n0, 0, wave, wave, lane);
 }
 
 // ------------------------------------------------------------------------------
@@ -556,10 +563,12 @@ inline int64_t align_capacity(int64_t S, int64_t E, int64_t block) {
 }
 
 // Block size of the grouped GEMMs: skinny blocks when experts see few rows.
-inline int moe_block_rows(int64_t S, int64_t E) { return (S <= 32 * E * 2) ? 32 : 256; }
+// Up to 32 rows per expert on average: 32-row blocks; up to 128: 64-row blocks (each
+// expert's weights streamed once or twice rather than two to four times); beyond: 256.
+inline int moe_block_rows(int64_t S, int64_t E) { return S <= 32 * E ? 32 : S <= 128 * E ? 64 : 256; }
 
 // K splits of the down projection: 2 on the decode path (32-row blocks).
-inline int moe_down_ksplit(int64_t S, int64_t E) { return moe_block_rows(S, E) == 32 ? 2 : 1; }
+inline int moe_down_ksplit(int64_t S, int64_t E) { return moe_block_rows(S, E) <= 64 ? 2 : 1; }
 
 struct MoeWorkspace {
   int32_t* offsets;
@@ -610,13 +619,13 @@ int launch_moe_gemm(MoeGemmParams p, int64_t cap, hipStream_t st) {
 }
 
 
-template <int MODE, int BN, int NSLOT>
+template <int MODE, int BN, int NSLOT, int BM = 32>
 int launch_moe_decode(MoeGemmParams p, int64_t cap, hipStream_t st) {
   p.ntiles = (MODE == MOE_GATEUP) ? p.Nout / (BN / 2) : p.Nout / BN;
-  p.max_mblocks = (int)(cap / 32);
+  p.max_mblocks = (int)(cap / BM);
   const int64_t blocks = (int64_t)p.max_mblocks * p.ntiles * p.ksplit;
   if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "fused_moe: grid too large");
-  hipLaunchKernelGGL((moe_decode_kernel<MODE, BN, NSLOT>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((moe_decode_kernel<MODE, BN, NSLOT, BM>), dim3((unsigned)blocks), dim3(256), 0, st, p);
   return check_launch(MODE == MOE_GATEUP ? "moe_gateup_decode_kernel" : "moe_down_decode_kernel");
 }
 
@@ -711,8 +720,10 @@ extern "C" int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, c
   p.w_rstride = D;
   // buffer-load engine needs operand byte ranges below 4 GiB and K % 64 == 0
   const bool buf_ok = T * ldh * 2 < (1ll << 32) && 2 * I * D * 2 < (1ll << 32) && D % 64 == 0 && I % 64 == 0;
+  // 64-row blocks without the buffer engine run 32-row tiles (two per aligned block)
   rc = (BM == 32 && buf_ok) ? launch_moe_decode<MOE_GATEUP, 128, 7>(p, cap, st)
-       : (BM == 32) ? launch_moe_gemm<MOE_GATEUP, 32, 256, 1, 4>(p, cap, st)
+       : (BM == 64 && buf_ok) ? launch_moe_decode<MOE_GATEUP, 128, 6, 64>(p, cap, st)
+       : (BM <= 64) ? launch_moe_gemm<MOE_GATEUP, 32, 256, 1, 4>(p, cap, st)
        : buf_ok   ? launch_moe_buf<MOE_GATEUP, 256, 256>(p, cap, st)
                   : launch_moe_gemm<MOE_GATEUP, 256, 256, 2, 2>(p, cap, st);
   if (rc) return rc;
@@ -730,7 +741,10 @@ extern "C" int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, c
   if (BM == 32 && buf_ok) {
     p.ksplit = ksplit;  // I % 128 == 0, so every split is a multiple of 64
     rc = launch_moe_decode<MOE_DOWN, 128, 6>(p, cap, st);
-  } else if (BM == 32) {
+  } else if (BM == 64 && buf_ok) {
+    p.ksplit = ksplit;
+    rc = launch_moe_decode<MOE_DOWN, 128, 4, 64>(p, cap, st);
+  } else if (BM <= 64) {
     rc = launch_moe_gemm<MOE_DOWN, 32, 128, 1, 4>(p, cap, st);
   } else if (buf_ok && D % 256 == 0) {
     rc = launch_moe_buf<MOE_DOWN, 128, 256>(p, cap, st);
@@ -829,7 +843,7 @@ extern "C" int kore_moe_grouped_gemm(const void* x, int64_t ldx, const void* w, 
       ((uintptr_t)out & 15u))
     return set_error(KORE_EINVAL, "moe_grouped_gemm: rows must be 16-byte aligned (ldx, ldo %% 8 == 0)");
   if (M >= (1ll << 30) || N * K >= (1ll << 40)) return set_error(KORE_EUNSUPPORTED, "moe_grouped_gemm: too large");
-  const int BM = moe_block_rows(M, E);
+  const int BM = M <= 64 * E ? 32 : 256;  // the 32-row ring or 256-row tiles
   const GroupedWorkspace ws = carve_grouped(workspace, M, E, BM);
   if (workspace_bytes < kore_moe_grouped_gemm_workspace_bytes(M, E))
     return set_error(KORE_EWORKSPACE, "moe_grouped_gemm: workspace %zu bytes < required %zu", workspace_bytes,

@@ -531,57 +531,64 @@ namespace kore {
 // vmcnt arithmetic is uniform.  AP == 2 multiplies two A planes by the same B
 // fragments (the bf16 high/low split of an fp32 activation).
 // ---------------------------------------------------------------------------------
-template <typename T, int BN, int AP, int NSLOT>
+template <typename T, int BN, int AP, int NSLOT, int BM_ = 32>
 struct SkinnyRingEngine {
-  static constexpr int NW = 4, BM = 32;
+  static constexpr int NW = 4, BM = BM_, MI = BM / 32;
+  static_assert(BM == 32 || BM == 64, "32 or 64 rows");
   static constexpr int WCOLS = BN / NW, NI = WCOLS / 32;
-  static_assert(WCOLS % 32 == 0 && NI >= 1, "wave tile is 32 x (multiple of 32)");
+  static_assert(WCOLS % 32 == 0 && NI >= 1, "wave tile is BM x (multiple of 32)");
   static constexpr int A_ELEMS = BM * kBK, B_ELEMS = BN * kBK;
   static constexpr int B_OFF = AP * A_ELEMS;
   static constexpr int STAGE = AP * A_ELEMS + B_ELEMS;
   static constexpr int LDS_ELEMS = NSLOT * STAGE;
-  static constexpr int BJ = BN / 8 / NW;  // 8-row B loads per wave per stage (A: one per plane)
+  static constexpr int AJ = BM / 32;      // 8-row A loads per wave per plane
+  static constexpr int BJ = BN / 8 / NW;  // 8-row B loads per wave per stage
   static_assert(BJ * 8 * NW == BN, "8-row wave loads must cover the B tile");
-  static constexpr int LPS = AP + BJ;
+  static constexpr int LPS = AP * AJ + BJ;
   static_assert(NSLOT >= 2 && (NSLOT - 2) * LPS <= 63, "vmcnt range");
 
-  static __device__ __forceinline__ int a_row(int wave, int lane) { return wave * 8 + (lane >> 3); }
+  static __device__ __forceinline__ int a_row(int wave, int lane, int j = 0) { return (wave + NW * j) * 8 + (lane >> 3); }
   static __device__ __forceinline__ int b_row(int wave, int lane, int j) { return (wave + NW * j) * 8 + (lane >> 3); }
   static __device__ __forceinline__ int chunk(int row, int lane) { return (lane & 7) ^ swz8(row); }
 
   __amdgpu_buffer_rsrc_t ra, ra2, rb;
-  uint32_t a_voff, b_voff[BJ];
+  uint32_t a_voff[AJ], b_voff[BJ];
 
   __device__ __forceinline__ void issue(uint16_t* lds, int slot, uint32_t soff, int wave) const {
     uint16_t* st = lds + slot * STAGE;
-    buf_lds16(ra, a_voff, soff, st + wave * 8 * kBK);
-    if constexpr (AP == 2) buf_lds16(ra2, a_voff, soff, st + A_ELEMS + wave * 8 * kBK);
+#pragma unroll
+    for (int j = 0; j < AJ; ++j) {
+      buf_lds16(ra, a_voff[j], soff, st + (wave + NW * j) * 8 * kBK);
+      if constexpr (AP == 2) buf_lds16(ra2, a_voff[j], soff, st + A_ELEMS + (wave + NW * j) * 8 * kBK);
+    }
 #pragma unroll
     for (int j = 0; j < BJ; ++j) buf_lds16(rb, b_voff[j], soff, st + B_OFF + (wave + NW * j) * 8 * kBK);
   }
 
-  static __device__ __forceinline__ void zero(f32x16_t (&acc)[1][NI]) {
+  static __device__ __forceinline__ void zero(f32x16_t (&acc)[MI][NI]) {
 #pragma unroll
-    for (int j = 0; j < NI; ++j)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[0][j][r] = 0.0f;
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
   }
 
   // Multiply K elements [k_begin, k_end) (multiples of 64; k_end > k_begin).
-  __device__ __forceinline__ void mainloop(uint16_t* lds, int k_begin, int k_end, f32x16_t (&acc)[1][NI]) {
+  __device__ __forceinline__ void mainloop(uint16_t* lds, int k_begin, int k_end, f32x16_t (&acc)[MI][NI]) {
     using Op = MfmaOp<T>;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 31, hh = lane >> 5;
     // fragment row R + lr (R % 32 == 0): swz8(R + lr) = (lr & 7) ^ (lr >> 3) ^ (4 * ((R / 32) & 1))
-    int offA[4], offB[2][4];
-    const int swa = ((lr & 7) ^ (lr >> 3)) & 7;
+    int offA[2][4], offB[2][4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      offA[ks] = lr * kBK + (((2 * ks + hh) ^ swa) << 3);
+    for (int par = 0; par < 2; ++par) {
+      const int swa = ((lr & 7) ^ (lr >> 3) ^ (4 * par)) & 7;
 #pragma unroll
-      for (int par = 0; par < 2; ++par) {
+      for (int ks = 0; ks < 4; ++ks) {
+        offA[par][ks] = lr * kBK + (((2 * ks + hh) ^ swa) << 3);
         const int qb = (wave * NI + par) & 1;
-        offB[par][ks] = lr * kBK + (((2 * ks + hh) ^ (swa ^ (4 * qb))) << 3);
+        offB[par][ks] = lr * kBK + (((2 * ks + hh) ^ ((((lr & 7) ^ (lr >> 3)) & 7) ^ (4 * qb))) << 3);
       }
     }
     const int nk = (k_end - k_begin) / kBK;
@@ -599,15 +606,19 @@ struct SkinnyRingEngine {
       const uint16_t* sB = sA + B_OFF + wave * WCOLS * kBK;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        u32x4_t af[AP], bf[NI];
+        u32x4_t af[AP][MI], bf[NI];
 #pragma unroll
-        for (int pl = 0; pl < AP; ++pl) af[pl] = *(const u32x4_t*)(sA + pl * A_ELEMS + offA[ks]);
+        for (int pl = 0; pl < AP; ++pl)
+#pragma unroll
+          for (int i = 0; i < MI; ++i) af[pl][i] = *(const u32x4_t*)(sA + pl * A_ELEMS + i * 32 * kBK + offA[i & 1][ks]);
 #pragma unroll
         for (int j = 0; j < NI; ++j) bf[j] = *(const u32x4_t*)(sB + j * 32 * kBK + offB[j & 1][ks]);
 #pragma unroll
         for (int pl = 0; pl < AP; ++pl)
 #pragma unroll
-          for (int j = 0; j < NI; ++j) acc[0][j] = Op::mma32(bf[j], af[pl], acc[0][j]);
+          for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NI; ++j) acc[i][j] = Op::mma32(bf[j], af[pl][i], acc[i][j]);
       }
       slot = slot + 1 == NSLOT ? 0 : slot + 1;
     }

@@ -52,7 +52,7 @@ def test_fused_moe_task_shapes(gpu, T, E, topk, D, I, seed):
 
 @pytest.mark.parametrize("T,E,topk,D,I", [(640, 4, 2, 512, 384), (700, 4, 3, 384, 256), (520, 2, 1, 256, 640)])
 def test_fused_moe_prefill_tiles(gpu, T, E, topk, D, I):
-    """Slot counts above 64 per expert select the 256-row prefill tiles (buffer-load
+    """Slot counts above 128 per expert select the 256-row prefill tiles (buffer-load
     pipeline for gate_up; two-plane down on 128x256 tiles when D % 256 == 0, else the
     128x128 register-staged tiles); ragged per-expert counts leave padding rows."""
     hidden, w1, w2, tw, ti = W.moe_inputs(T, E, topk, D, I, seed=T, wscale=0.05)
@@ -60,6 +60,17 @@ def test_fused_moe_prefill_tiles(gpu, T, E, topk, D, I):
     ref = moe_ref(hidden, w1, w2, tw, ti)
     verdict(out, ref, "fused_moe", "bf16", f"prefill tiles T{T} E{E} k{topk} D{D} I{I}")
     verdict(out, ref, "north_star", "bf16", f"prefill tiles T{T} (1e-2)")
+
+
+@pytest.mark.parametrize("T,E,topk,D,I", [(300, 4, 1, 256, 384), (500, 8, 2, 512, 256), (200, 4, 2, 384, 640)])
+def test_fused_moe_64row_blocks(gpu, T, E, topk, D, I):
+    """Slot counts of 33-128 per expert select 64-row blocks on the skinny ring engine
+    (each expert's weights streamed once per 64 slots); ragged counts leave padding rows."""
+    hidden, w1, w2, tw, ti = W.moe_inputs(T, E, topk, D, I, seed=T + 1, wscale=0.05)
+    out = kore_amd.fused_moe(*[t.to(gpu) for t in (hidden, w1, w2, tw, ti)])
+    ref = moe_ref(hidden, w1, w2, tw, ti)
+    verdict(out, ref, "fused_moe", "bf16", f"64-row blocks T{T} E{E} k{topk} D{D} I{I}")
+    verdict(out, ref, "north_star", "bf16", f"64-row blocks T{T} (1e-2)")
 
 
 def test_fused_moe_decode_config(gpu):
