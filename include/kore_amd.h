@@ -3,12 +3,12 @@
  *
  * Every entry point takes plain device pointers, element strides and sizes, and a
  * HIP stream (hipStream_t passed as void*; NULL = the legacy default stream).
- * Outputs and workspaces are owned by the caller.  One exception to "no entry point
- * allocates device memory": kore_gemm and kore_batched_gemm keep one grow-only scratch
- * buffer per (device, stream) for the packed-operand path (layouts the engines cannot
- * read in place, e.g. K = 4095) and the split-K path (decode-sized M), allocated on
- * first need and kept until the process exits.  Under graph capture they take paths
- * that need no scratch (the generic kernel, the non-split kernels).  Calls are
+ * Outputs and workspaces are owned by the caller: no entry point allocates device
+ * memory.  Entry points whose paths need device scratch take a `workspace` pointer and
+ * its size in bytes, and a matching *_workspace_bytes query (same arguments, no
+ * workspace, no stream) returns how many bytes those exact arguments need (0: none,
+ * and `workspace` may be NULL).  A workspace smaller than that fails with
+ * KORE_EWORKSPACE; the library never switches path because of it.  Calls are
  * asynchronous on `stream`.  Return value: KORE_OK, or an error
  * code with a message available from kore_last_error() (per host thread).
  *
@@ -65,44 +65,64 @@ int kore_abi_version(void);
  *   A element (m,k) at a[m*lda_m + k*lda_k]; B element (k,n) at b[k*ldb_k + n*ldb_n];
  *   C element (m,n) at c[m*ldc_m + n]; bias may be NULL (no bias), else [N] contiguous.
  * Any strides are accepted; the MFMA fast path needs unit stride along K for A and
- * along K or N for B, 16-byte aligned rows and K % 8 == 0 -- other layouts run a
- * slower generic kernel.  M, N >= 1, K >= 0 (K == 0 gives act(bias); a and b may then
- * be NULL).
+ * along K or N for B, 16-byte aligned rows and K % 8 == 0.  Other layouts (e.g. the
+ * K = 4095 tails) are packed into `workspace` first when the problem is large, or run
+ * a slower generic kernel when it is small; decode-sized M splits K and sums fp32
+ * partials held in `workspace`.  M, N >= 1, K >= 0 (K == 0 gives act(bias); a and b
+ * may then be NULL).  `workspace` must hold kore_gemm_workspace_bytes(<same args>).
  * Replaces: gemm(a, b)            kore/tasks/gemm_bf16/seed_triton.py:64-86
  *           <op>(a, b[, bias])    kore/tasks/_genops.py:715-731 (_GEMM_TMPL entry,
  *                                 gemm_fusion ops listed at _genops.py:274-290;
  *                                 dtypes bf16/fp16/fp32 at _genops.py:41-45)
  */
+size_t kore_gemm_workspace_bytes(int dtype, int act,
+                                 const void* a, int64_t lda_m, int64_t lda_k,
+                                 const void* b, int64_t ldb_k, int64_t ldb_n,
+                                 const void* bias, void* c, int64_t ldc_m,
+                                 int64_t M, int64_t N, int64_t K);
 int kore_gemm(int dtype, int act,
               const void* a, int64_t lda_m, int64_t lda_k,
               const void* b, int64_t ldb_k, int64_t ldb_n,
               const void* bias, void* c, int64_t ldc_m,
-              int64_t M, int64_t N, int64_t K, void* stream);
+              int64_t M, int64_t N, int64_t K,
+              void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Batched GEMM:  C[i] = A[i] @ B[i]^T  for i < batch, A[i] is [M,K], B[i] is [N,K].
  *   A (i,m,k) at a[i*sa_b + m*sa_m + k*sa_k]; B (i,n,k) at b[i*sb_b + n*sb_n + k*sb_k];
- *   C (i,m,n) at c[i*sc_b + m*sc_m + n].  fp32 accumulate, `dtype` out.
+ *   C (i,m,n) at c[i*sc_b + m*sc_m + n].  fp32 accumulate, `dtype` out.  `workspace`
+ *   must hold kore_batched_gemm_workspace_bytes(<same args>) bytes (layouts the
+ *   engines cannot read are packed there).
  * Replaces: batched_gemm(a, b)    kore/tasks/vendor_ops.py:914-920 (_BATCHED_GEMM_SEED)
  *           batched_gemm(a, b)    kore/tasks/moe_batched_gemm_bf16/reference.py:22
  */
+size_t kore_batched_gemm_workspace_bytes(int dtype,
+                                         const void* a, int64_t sa_b, int64_t sa_m, int64_t sa_k,
+                                         const void* b, int64_t sb_b, int64_t sb_n, int64_t sb_k,
+                                         void* c, int64_t sc_b, int64_t sc_m,
+                                         int64_t batch, int64_t M, int64_t N, int64_t K);
 int kore_batched_gemm(int dtype,
                       const void* a, int64_t sa_b, int64_t sa_m, int64_t sa_k,
                       const void* b, int64_t sb_b, int64_t sb_n, int64_t sb_k,
                       void* c, int64_t sc_b, int64_t sc_m,
-                      int64_t batch, int64_t M, int64_t N, int64_t K, void* stream);
+                      int64_t batch, int64_t M, int64_t N, int64_t K,
+                      void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * GEMM backward of the linear layer Y = X @ W^T (X [M,K], W [N,K], dY [M,N]):
  *   dX [M,K] = dY @ W,   dW [N,K] = dY^T @ X,   fp32 accumulate, `dtype` out (bf16/fp16).
  *   Row strides ldx, ldw, lddy, lddx, lddw (unit stride along rows).  dY^T is formed
- *   in `workspace` (the A operand of dW must be K-contiguous), which must hold
- *   kore_gemm_backward_workspace_bytes(M, N, K) bytes; W and X are read in place.
+ *   in `workspace` (the A operand of dW must be K-contiguous), followed by the two
+ *   GEMMs' own scratch; it must hold kore_gemm_backward_workspace_bytes(<same args>)
+ *   bytes.  W and X are read in place.
  * Replaces: gemm_backward(x, w, dy) -> (dx, dw)
  *           kore/tasks/gemm_backward_bf16/seed_triton.py:74-86 (ENTRY reference.py:22,
  *           oracle reference.py:64-72)
  */
-size_t kore_gemm_backward_workspace_bytes(int64_t M, int64_t N, int64_t K);
+size_t kore_gemm_backward_workspace_bytes(int dtype, const void* x, int64_t ldx, const void* w,
+                                          int64_t ldw, const void* dy, int64_t lddy, const void* dx,
+                                          int64_t lddx, const void* dw, int64_t lddw,
+                                          int64_t M, int64_t N, int64_t K);
 int kore_gemm_backward(int dtype, const void* x, int64_t ldx, const void* w, int64_t ldw,
                        const void* dy, int64_t lddy, void* dx, int64_t lddx, void* dw,
                        int64_t lddw, int64_t M, int64_t N, int64_t K,

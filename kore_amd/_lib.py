@@ -21,11 +21,16 @@ _vp, _i64, _i32, _sz = C.c_void_p, C.c_int64, C.c_int, C.c_size_t
 SIGNATURES = {
     "kore_last_error": (C.c_char_p, []),
     "kore_abi_version": (_i32, []),
+    "kore_gemm_workspace_bytes": (_sz, [_i32, _i32, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64,
+                                        _i64, _i64, _i64]),
     "kore_gemm": (_i32, [_i32, _i32, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64,
-                         _i64, _i64, _i64, _vp]),
+                         _i64, _i64, _i64, _vp, _sz, _vp]),
+    "kore_batched_gemm_workspace_bytes": (_sz, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
+                                                _vp, _i64, _i64, _i64, _i64, _i64, _i64]),
     "kore_batched_gemm": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
-                                 _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
-    "kore_gemm_backward_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+                                 _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _sz, _vp]),
+    "kore_gemm_backward_workspace_bytes": (_sz, [_i32, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64,
+                                                 _i64, _i64, _i64]),
     "kore_gemm_backward": (_i32, [_i32, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64,
                                   _vp, _sz, _vp]),
     "kore_gemm_a8w8_blockscale": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _vp, _i64,

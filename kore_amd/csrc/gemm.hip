@@ -16,7 +16,8 @@
 // activation in fp32, packs, stages the wave's tile in LDS and writes C with
 // 16-byte row-contiguous stores.
 //
-// Generic path: any strides and any K, fp32 FMA on 64x64 tiles staged through LDS.
+// Generic path: any strides and any K, 128x128 MFMA tiles fed by bounds-checked element
+// reads along the unit-stride index (gemm_generic_mfma_kernel).
 #include "../../include/kore_amd.h"
 #include "kore_common.hpp"
 #include "tile_engine.hpp"
@@ -618,9 +619,7 @@ __global__ void __launch_bounds__(512) gemm_shortk_kernel(const TileParams p, co
   if (storer) store_tile(count - 1, slot == 0 ? NA - 1 : slot - 1);
 }
 
-// ---------------------------------------------------------------------------------
-// Generic-stride kernel: 64x64 tile, BK 16, fp32 FMA, any strides / K / alignment.
-// ---------------------------------------------------------------------------------
+// Arguments of the generic MFMA kernel below (any strides / K / alignment).
 struct GenericParams {
   const uint16_t* a;
   const uint16_t* b;
@@ -633,8 +632,8 @@ struct GenericParams {
 };
 
 // ---------------------------------------------------------------------------------
-// Generic MFMA kernel: any strides, any K (the fallback for layouts the engines cannot
-// read and for K tails under graph capture, where no scratch is taken).  128x128 tiles,
+// Generic MFMA kernel: any strides, any K (layouts the engines cannot read, when the
+// problem is too small for a pack pass).  128x128 tiles,
 // 4 waves of 64x64, K steps of 32.  Operands are read element by element, 16 per thread
 // per operand and step, along whichever index is unit-stride (so a wave reads 128
 // contiguous bytes), every read bounds-checked (zero outside); the next step is loaded
@@ -1036,7 +1035,12 @@ int launch_generic(const GemmDesc& d, hipStream_t stream) {
 // Split-K launch (batch 1): `splits` slices of `kper` (a multiple of 64) K elements on
 // BM x BN ring tiles.
 template <typename T, int BL, int BM, int BN, int WM, int WN, int NSLOT>
-int launch_splitk(const GemmDesc& d, int splits, int kper, hipStream_t stream) {
+int launch_splitk(const GemmDesc& d, int splits, int kper, Ws& ws, hipStream_t stream) {
+  const size_t bytes = (size_t)splits * d.M * d.N * sizeof(float);
+  float* part = (float*)ws.take(bytes);
+  if (ws.plan) return KORE_OK;
+  if (part == nullptr)
+    return set_error(KORE_EWORKSPACE, "gemm: split-K needs %zu workspace bytes (got %zu)", ws_bytes(bytes), ws.bytes);
   TileParams p = {};
   p.a = (const uint16_t*)d.a;
   p.b = (const uint16_t*)d.b;
@@ -1054,9 +1058,6 @@ int launch_splitk(const GemmDesc& d, int splits, int kper, hipStream_t stream) {
   p.tiles_per_batch = p.tiles_m * p.tiles_n;
   p.batch = 1;
   p.act = d.act;
-  const size_t bytes = (size_t)splits * d.M * d.N * sizeof(float);
-  float* part = (float*)scratch_alloc(bytes, stream);
-  if (part == nullptr) return KORE_EUNSUPPORTED;
   hipLaunchKernelGGL((gemm_splitk_kernel<T, BL, BM, BN, WM, WN, NSLOT>), dim3((unsigned)(p.tiles_per_batch * splits)),
                      dim3(256), 0, stream, p, part, splits, kper);
   int rc = check_launch("gemm_splitk_kernel");
@@ -1068,7 +1069,6 @@ int launch_splitk(const GemmDesc& d, int splits, int kper, hipStream_t stream) {
                        d.scm, vec);
     rc = check_launch("splitk_reduce_kernel");
   }
-  scratch_free(part, stream);
   return rc;
 }
 
@@ -1122,23 +1122,30 @@ int launch_engine(const GemmDesc& d, hipStream_t stream) {
 // Layouts the engines cannot read in place (rows not 16-byte aligned, e.g. K = 4095;
 // transposed or strided operands): A, and B unless it is N-contiguous with aligned
 // K-rows, are packed K-contiguous with the K tail zero-padded to a multiple of 64
-// into the caller stream's scratch buffer (scratch_alloc).
+// into the caller's workspace.
 // An N-contiguous B is read in place: its buffer resource ends at the last real
-// K-row, so the padded rows read as zero.  Returns KORE_EUNSUPPORTED when the packed
-// problem does not fit the engines' 32-bit buffer offsets or scratch is unavailable.
-template <typename T>
-int launch_padded(const GemmDesc& d, hipStream_t stream) {
+// K-row, so the padded rows read as zero.  The caller checks padded_fits first.
+inline bool padded_b_inplace(const GemmDesc& d) {
+  return d.sbn == 1 && d.sbk % 8 == 0 && aligned16(d.b) && d.sb % 8 == 0 && d.N % 8 == 0 &&
+         d.sbk * 2 * d.K + d.N * 2 < (1ll << 31);
+}
+inline bool padded_fits(const GemmDesc& d) {
   const int64_t Kp = (d.K + 63) / 64 * 64;
-  const bool b_nc = d.sbn == 1 && d.sbk % 8 == 0 && aligned16(d.b) && d.sb % 8 == 0 && d.N % 8 == 0 &&
-                    d.sbk * 2 * d.K + d.N * 2 < (1ll << 31);
-  if (d.M >= (1ll << 31) || d.N >= (1ll << 31) || Kp * 2 * 256 + Kp * 2 >= (1ll << 31) || d.batch > 65535)
-    return KORE_EUNSUPPORTED;
+  return d.M < (1ll << 31) && d.N < (1ll << 31) && Kp * 2 * 256 + Kp * 2 < (1ll << 31) && d.batch <= 65535;
+}
+template <typename T>
+int launch_padded(const GemmDesc& d, Ws& ws, hipStream_t stream) {
+  const int64_t Kp = (d.K + 63) / 64 * 64;
+  const bool b_nc = padded_b_inplace(d);
   const size_t a_bytes = (size_t)(d.batch * d.M * Kp * 2 + 255) / 256 * 256;
   const size_t b_bytes = b_nc ? 0 : (size_t)(d.batch * d.N * Kp * 2);
-  void* ws = scratch_alloc(a_bytes + b_bytes, stream);
-  if (ws == nullptr) return KORE_EUNSUPPORTED;
-  uint16_t* ap = (uint16_t*)ws;
-  uint16_t* bp = (uint16_t*)((char*)ws + a_bytes);
+  void* buf = ws.take(a_bytes + b_bytes);
+  if (ws.plan) return KORE_OK;
+  if (buf == nullptr)
+    return set_error(KORE_EWORKSPACE, "gemm: packing the operands needs %zu workspace bytes (got %zu)",
+                     ws_bytes(a_bytes + b_bytes), ws.bytes);
+  uint16_t* ap = (uint16_t*)buf;
+  uint16_t* bp = (uint16_t*)((char*)buf + a_bytes);
   hipLaunchKernelGGL(pack16_kernel, dim3((unsigned)(Kp / 64), (unsigned)((d.M + 63) / 64), (unsigned)d.batch), dim3(256),
                      0, stream, (const uint16_t*)d.a, d.sam, d.sak, d.sa, ap, d.M * Kp, (int)d.M, (int)d.K, (int)Kp);
   int rc = check_launch("pack16_kernel");
@@ -1167,12 +1174,13 @@ int launch_padded(const GemmDesc& d, hipStream_t stream) {
       rc = launch_engine<T, B_KC>(q, stream);
     }
   }
-  scratch_free(ws, stream);
   return rc;
 }
 
+// Picks the kernel path for d and launches it; in plan mode (ws.plan) it launches
+// nothing and only records the workspace that path needs.
 template <typename T>
-int dispatch_typed(const GemmDesc& d, hipStream_t stream) {
+int dispatch_typed(const GemmDesc& d, Ws& ws, hipStream_t stream) {
   // Fast-path preconditions: A K-contiguous with 16-byte aligned rows, K % 8 == 0,
   // B K- or N-contiguous with 16-byte aligned rows, C N-contiguous.
   const bool a_ok = d.sak == 1 && d.sam % 8 == 0 && aligned16(d.a) && d.sa % 8 == 0 && d.K % 8 == 0;
@@ -1201,8 +1209,10 @@ int dispatch_typed(const GemmDesc& d, hipStream_t stream) {
     // Long K and enough tiles to fill half the chip: the direct-to-LDS engines at the
     // tile shape with the fewest weighted rounds (small problems, under 128 tiles of
     // 128x128, keep their latency-bound paths below: split-K, the 32x128 rings).
-    if (deep_ok && !small && pick_tile(d) != TILE_32x128)
+    if (deep_ok && !small && pick_tile(d) != TILE_32x128) {
+      if (ws.plan) return KORE_OK;
       return b_kc ? launch_engine<T, B_KC>(d, stream) : launch_engine<T, B_NC>(d, stream);
+    }
     // K of one or two 64-wide steps, no epilogue, enough 128x128 tiles to give every
     // CU several: the persistent short-K kernel (16-byte buffer stores need N % 8 == 0
     // and 16-byte aligned C rows; per-tile byte offsets must stay below 2^31).
@@ -1210,17 +1220,20 @@ int dispatch_typed(const GemmDesc& d, hipStream_t stream) {
                         d.N % 8 == 0 && d.scm % 8 == 0 && d.sc % 8 == 0 && aligned16(d.c) &&
                         d.sam * 2 * 128 + d.K * 2 < (1ll << 31) && (b_nc || d.sbn * 2 * 128 + d.K * 2 < (1ll << 31)) &&
                         d.scm * 2 * 128 < (1ll << 31) && mid_tiles >= 4 * (int64_t)device_cus();
-    if (shortk) return b_kc ? launch_shortk<T, B_KC>(d, stream) : launch_shortk<T, B_NC>(d, stream);
+    if (shortk) {
+      if (ws.plan) return KORE_OK;
+      return b_kc ? launch_shortk<T, B_KC>(d, stream) : launch_shortk<T, B_NC>(d, stream);
+    }
     // Few 32x128 tiles for the CUs and a long K (decode-sized M): split K.
     const int64_t t32 = ((d.M + 31) / 32) * ((d.N + 127) / 128);
     if (d.batch == 1 && (b_kc ? buf_ok : buf_nc_ok) && d.K >= 1024 && t32 * 2 <= device_cus()) {
       const int nk = (int)(d.K / 64);
       const int want = (int)std::min<int64_t>(device_cus() / t32, nk / 4);
       const int per = (nk + want - 1) / want, splits = (nk + per - 1) / per;
-      const int rc = b_kc ? launch_splitk<T, B_KC, 32, 128, 1, 4, 7>(d, splits, per * 64, stream)
-                          : launch_splitk<T, B_NC, 32, 128, 1, 4, 7>(d, splits, per * 64, stream);
-      if (rc != KORE_EUNSUPPORTED) return rc;
+      return b_kc ? launch_splitk<T, B_KC, 32, 128, 1, 4, 7>(d, splits, per * 64, ws, stream)
+                  : launch_splitk<T, B_NC, 32, 128, 1, 4, 7>(d, splits, per * 64, ws, stream);
     }
+    if (ws.plan) return KORE_OK;
     // few tiles and a long K: the latency-bound case, on the deep direct-to-LDS ring
     if (b_kc && small && buf_ok && d.K >= 512) return launch_ring<T>(d, stream);
     if (!b_kc && small && buf_nc_ok && d.K >= 512) return launch_deep<T, 32, 128, 1, 4, 7, B_NC>(d, stream);
@@ -1233,14 +1246,12 @@ int dispatch_typed(const GemmDesc& d, hipStream_t stream) {
   }
   // Large problems in other layouts: pack, then the engines (small ones are cheaper on
   // the generic kernel than a pack pass).
-  if (d.M * d.N * d.K >= (1ll << 27) && d.K >= 64) {
-    const int rc = launch_padded<T>(d, stream);
-    if (rc != KORE_EUNSUPPORTED) return rc;
-  }
+  if (d.M * d.N * d.K >= (1ll << 27) && d.K >= 64 && padded_fits(d)) return launch_padded<T>(d, ws, stream);
+  if (ws.plan) return KORE_OK;
   return launch_generic<T>(d, stream);
 }
 
-int run_gemm(const GemmDesc& d, void* stream) {
+int run_gemm(const GemmDesc& d, Ws& ws, void* stream) {
   if (d.c == nullptr || (d.K > 0 && (d.a == nullptr || d.b == nullptr)))
     return set_error(KORE_EINVAL, "gemm: null pointer");
   if (d.M <= 0 || d.N <= 0 || d.K < 0 || d.batch <= 0)
@@ -1249,12 +1260,12 @@ int run_gemm(const GemmDesc& d, void* stream) {
   if (d.act < KORE_ACT_NONE || d.act > KORE_ACT_SIGMOID) return set_error(KORE_EINVAL, "gemm: unknown act %d", d.act);
   if (d.scm < d.N) return set_error(KORE_EINVAL, "gemm: ldc_m (%lld) < N (%lld)", (long long)d.scm, (long long)d.N);
   hipStream_t s = (hipStream_t)stream;
-  if (d.dtype == KORE_DT_BF16) return dispatch_typed<BF16>(d, s);
-  if (d.dtype == KORE_DT_FP16) return dispatch_typed<F16>(d, s);
+  if (d.dtype == KORE_DT_BF16) return dispatch_typed<BF16>(d, ws, s);
+  if (d.dtype == KORE_DT_FP16) return dispatch_typed<F16>(d, ws, s);
   if (d.dtype == KORE_DT_FP32) {
     if (d.batch != 1) return set_error(KORE_EUNSUPPORTED, "gemm: fp32 is not batched");
     GemmF32Args f{d.a, d.b, d.bias, d.c, d.M, d.N, d.K, d.sam, d.sak, d.sbk, d.sbn, d.scm, d.act};
-    return launch_gemm_f32(f, s);
+    return launch_gemm_f32(f, ws, s);
   }
   return set_error(KORE_EINVAL, "gemm: unsupported dtype code %d", d.dtype);
 }
@@ -1262,42 +1273,77 @@ int run_gemm(const GemmDesc& d, void* stream) {
 }  // namespace
 }  // namespace kore
 
+extern "C" size_t kore_gemm_workspace_bytes(int dtype, int act, const void* a, int64_t lda_m, int64_t lda_k,
+                                            const void* b, int64_t ldb_k, int64_t ldb_n, const void* bias, void* c,
+                                            int64_t ldc_m, int64_t M, int64_t N, int64_t K) {
+  kore::GemmDesc d{dtype, act, a, b, bias, c, M, N, K, 1, lda_m, lda_k, ldb_k, ldb_n, ldc_m, 0, 0, 0};
+  kore::Ws ws;
+  ws.plan = true;
+  if (kore::run_gemm(d, ws, nullptr) != KORE_OK) return 0;  // the call itself reports the error
+  return kore::ws_bytes(ws.need);
+}
+
 extern "C" int kore_gemm(int dtype, int act, const void* a, int64_t lda_m, int64_t lda_k, const void* b,
                          int64_t ldb_k, int64_t ldb_n, const void* bias, void* c, int64_t ldc_m, int64_t M,
-                         int64_t N, int64_t K, void* stream) {
+                         int64_t N, int64_t K, void* workspace, size_t workspace_bytes, void* stream) {
   kore::GemmDesc d{dtype, act, a, b, bias, c, M, N, K, 1, lda_m, lda_k, ldb_k, ldb_n, ldc_m, 0, 0, 0};
-  return kore::run_gemm(d, stream);
+  kore::Ws ws;
+  ws.ptr = workspace;
+  ws.bytes = workspace ? workspace_bytes : 0;
+  return kore::run_gemm(d, ws, stream);
+}
+
+extern "C" size_t kore_batched_gemm_workspace_bytes(int dtype, const void* a, int64_t sa_b, int64_t sa_m,
+                                                    int64_t sa_k, const void* b, int64_t sb_b, int64_t sb_n,
+                                                    int64_t sb_k, void* c, int64_t sc_b, int64_t sc_m, int64_t batch,
+                                                    int64_t M, int64_t N, int64_t K) {
+  kore::GemmDesc d{dtype, KORE_ACT_NONE, a, b, nullptr, c, M, N, K, batch, sa_m, sa_k, sb_k, sb_n, sc_m,
+                   sa_b, sb_b, sc_b};
+  kore::Ws ws;
+  ws.plan = true;
+  if (kore::run_gemm(d, ws, nullptr) != KORE_OK) return 0;
+  return kore::ws_bytes(ws.need);
 }
 
 extern "C" int kore_batched_gemm(int dtype, const void* a, int64_t sa_b, int64_t sa_m, int64_t sa_k, const void* b,
                                  int64_t sb_b, int64_t sb_n, int64_t sb_k, void* c, int64_t sc_b, int64_t sc_m,
-                                 int64_t batch, int64_t M, int64_t N, int64_t K, void* stream) {
+                                 int64_t batch, int64_t M, int64_t N, int64_t K, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
   // C[i] = A[i] @ B[i]^T: B[i] is [N,K], i.e. the (k, n) strides are (sb_k, sb_n).
   kore::GemmDesc d{dtype, KORE_ACT_NONE, a, b, nullptr, c, M, N, K, batch, sa_m, sa_k, sb_k, sb_n, sc_m,
                    sa_b, sb_b, sc_b};
-  return kore::run_gemm(d, stream);
+  kore::Ws ws;
+  ws.ptr = workspace;
+  ws.bytes = workspace ? workspace_bytes : 0;
+  return kore::run_gemm(d, ws, stream);
 }
 
-// Linear-layer backward for Y = X @ W^T: dX = dY @ W and dW = dY^T @ X.  Both GEMMs
-// run on the K-contiguous fast path: W^T [K,N], X^T [K,M] and dY^T [N,M] are formed in
-// the caller's workspace first (three HBM-bound transposes, about a tenth of the GEMM
-// time at 8192x4096x4096), since dW reduces over the row index of both of its operands
-// and dX reads W along its rows.
+// Linear-layer backward for Y = X @ W^T: dX = dY @ W and dW = dY^T @ X.  W and X are
+// read in place as N-contiguous B operands (LDS transpose reads); the A operand of dW
+// must be K-contiguous, so dY^T [N,M] is formed in the caller's workspace by one
+// HBM-bound transpose.
 namespace kore {
 inline int64_t bwd_ld(int64_t n) { return (n + 7) / 8 * 8; }  // 16-byte transposed rows
 inline size_t bwd_part(int64_t rows, int64_t cols) { return (size_t)(rows * bwd_ld(cols) * 2 + 255) / 256 * 256; }
 }  // namespace kore
 
-extern "C" size_t kore_gemm_backward_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  using namespace kore;
-  if (M <= 0 || N <= 0 || K <= 0) return 0;
-  return bwd_part(N, M) + 256;
+namespace kore {
+namespace {
+// The two GEMMs of the backward; dyt is the dY^T copy in the workspace.
+GemmDesc bwd_dx(int dtype, const void* w, int64_t ldw, const void* dy, int64_t lddy, void* dx, int64_t lddx,
+                int64_t M, int64_t N, int64_t K) {
+  // dX[M,K] = dY[M,N] @ W[N,K]: W read in place as an N-contiguous B (element (n, k) at
+  // w[n*ldw + k]); the engines stage it through LDS transpose reads
+  return GemmDesc{dtype, KORE_ACT_NONE, dy, w, nullptr, dx, M, K, N, 1, lddy, 1, ldw, 1, lddx, 0, 0, 0};
 }
-
-extern "C" int kore_gemm_backward(int dtype, const void* x, int64_t ldx, const void* w, int64_t ldw, const void* dy,
-                                  int64_t lddy, void* dx, int64_t lddx, void* dw, int64_t lddw, int64_t M, int64_t N,
-                                  int64_t K, void* workspace, size_t workspace_bytes, void* stream) {
-  using namespace kore;
+GemmDesc bwd_dw(int dtype, const void* x, int64_t ldx, const void* dyt, void* dw, int64_t lddw, int64_t M,
+                int64_t N, int64_t K) {
+  // dW[N,K] = dY^T[N,M] @ X[M,K]: X read in place as an N-contiguous B (element (m, k)
+  // at x[m*ldx + k])
+  return GemmDesc{dtype, KORE_ACT_NONE, dyt, x, nullptr, dw, N, K, M, 1, bwd_ld(M), 1, ldx, 1, lddw, 0, 0, 0};
+}
+int bwd_check(int dtype, const void* x, int64_t ldx, const void* w, int64_t ldw, const void* dy, int64_t lddy,
+              const void* dx, int64_t lddx, const void* dw, int64_t lddw, int64_t M, int64_t N, int64_t K) {
   if (dtype != KORE_DT_BF16 && dtype != KORE_DT_FP16)
     return set_error(KORE_EINVAL, "gemm_backward: dtype must be bf16 or fp16 (got %d)", dtype);
   if (!x || !w || !dy || !dx || !dw) return set_error(KORE_EINVAL, "gemm_backward: null pointer");
@@ -1306,23 +1352,51 @@ extern "C" int kore_gemm_backward(int dtype, const void* x, int64_t ldx, const v
     return set_error(KORE_EINVAL, "gemm_backward: row stride smaller than row");
   if (M >= (1ll << 31) || N >= (1ll << 31) || K >= (1ll << 31))
     return set_error(KORE_EUNSUPPORTED, "gemm_backward: dimension >= 2^31");
-  if (!workspace || workspace_bytes < kore_gemm_backward_workspace_bytes(M, N, K))
-    return set_error(KORE_EINVAL, "gemm_backward: workspace smaller than kore_gemm_backward_workspace_bytes(M, N, K)");
+  return KORE_OK;
+}
+}  // namespace
+}  // namespace kore
+
+// Workspace: dY^T [N, bwd_ld(M)] at a 256-byte aligned start, then the scratch of the
+// two GEMMs (they run one after the other, so they share it).
+extern "C" size_t kore_gemm_backward_workspace_bytes(int dtype, const void* x, int64_t ldx, const void* w,
+                                                     int64_t ldw, const void* dy, int64_t lddy, const void* dx,
+                                                     int64_t lddx, const void* dw, int64_t lddw, int64_t M,
+                                                     int64_t N, int64_t K) {
+  using namespace kore;
+  if (bwd_check(dtype, x, ldx, w, ldw, dy, lddy, dx, lddx, dw, lddw, M, N, K) != KORE_OK) return 0;
+  Ws ws;
+  ws.plan = true;
+  GemmDesc gx = bwd_dx(dtype, w, ldw, dy, lddy, (void*)dx, lddx, M, N, K);
+  GemmDesc gw = bwd_dw(dtype, x, ldx, (const void*)(uintptr_t)256, (void*)dw, lddw, M, N, K);
+  if (run_gemm(gx, ws, nullptr) != KORE_OK || run_gemm(gw, ws, nullptr) != KORE_OK) return 0;
+  return 256 + bwd_part(N, M) + ws_bytes(ws.need);
+}
+
+extern "C" int kore_gemm_backward(int dtype, const void* x, int64_t ldx, const void* w, int64_t ldw, const void* dy,
+                                  int64_t lddy, void* dx, int64_t lddx, void* dw, int64_t lddw, int64_t M, int64_t N,
+                                  int64_t K, void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace kore;
+  int rc = bwd_check(dtype, x, ldx, w, ldw, dy, lddy, dx, lddx, dw, lddw, M, N, K);
+  if (rc != KORE_OK) return rc;
+  const size_t need = kore_gemm_backward_workspace_bytes(dtype, x, ldx, w, ldw, dy, lddy, dx, lddx, dw, lddw, M, N, K);
+  if (!workspace || workspace_bytes < need)
+    return set_error(KORE_EWORKSPACE, "gemm_backward: needs %zu workspace bytes (got %zu)", need,
+                     workspace ? workspace_bytes : (size_t)0);
   hipStream_t st = (hipStream_t)stream;
   uint8_t* base = (uint8_t*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
   uint16_t* dyt = (uint16_t*)base;  // dY^T [N, M]
-  const int64_t ldm = bwd_ld(M);
-  // dX[M,K] = dY[M,N] @ W[N,K]: W read in place as an N-contiguous B (element (n, k) at
-  // w[n*ldw + k]); the engines stage it through LDS transpose reads
-  GemmDesc gx{dtype, KORE_ACT_NONE, dy, w, nullptr, dx, M, K, N, 1, lddy, 1, ldw, 1, lddx, 0, 0, 0};
-  int rc = run_gemm(gx, st);
+  Ws ws;  // the GEMMs' scratch follows dY^T
+  ws.ptr = base + bwd_part(N, M);
+  ws.bytes = workspace_bytes - (size_t)(base - (uint8_t*)workspace) - bwd_part(N, M);
+  GemmDesc gx = bwd_dx(dtype, w, ldw, dy, lddy, dx, lddx, M, N, K);
+  rc = run_gemm(gx, ws, st);
   if (rc != KORE_OK) return rc;
-  // dW[N,K] = dY^T[N,M] @ X[M,K]: A must be K-contiguous, so dY is transposed once into the
-  // workspace; X is read in place as an N-contiguous B (element (m, k) at x[m*ldx + k])
+  // dY^T: A of dW must be K-contiguous
   hipLaunchKernelGGL(transpose16_kernel, dim3((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64)), dim3(256), 0, st,
-                     (const uint16_t*)dy, lddy, dyt, ldm, (int)M, (int)N);
+                     (const uint16_t*)dy, lddy, dyt, bwd_ld(M), (int)M, (int)N);
   rc = check_launch("transpose16_kernel");
   if (rc != KORE_OK) return rc;
-  GemmDesc gw{dtype, KORE_ACT_NONE, dyt, x, nullptr, dw, N, K, M, 1, ldm, 1, ldx, 1, lddw, 0, 0, 0};
-  return run_gemm(gw, st);
+  GemmDesc gw = bwd_dw(dtype, x, ldx, dyt, dw, lddw, M, N, K);
+  return run_gemm(gw, ws, st);
 }

@@ -19,7 +19,8 @@
 // The B fragment is the first MFMA operand, so lane l owns output row l % 32 and four
 // N-consecutive columns per register group: 16-byte stores straight from registers.
 //
-// Any other layout, K % 64 != 0 or unaligned rows: a 64x64 FMA tile (generic).
+// Any other layout, K % 32 != 0 or unaligned rows: large problems are packed into the
+// caller's workspace first; small ones run a bounds-checked generic MFMA kernel.
 #include "../../include/kore_amd.h"
 #include "kore_common.hpp"
 #include "tile_engine.hpp"
@@ -244,8 +245,7 @@ struct F32GenericParams {
 };
 
 // Generic fp32 kernel on the fp32 matrix cores: any strides, any K (layouts the MFMA
-// kernels cannot read when the problem is too small for a pack pass, and K tails under
-// graph capture, where no scratch is taken).  128x128 tiles, 4 waves of 64x64, K steps of
+// kernels cannot read when the problem is too small for a pack pass).  128x128 tiles, 4 waves of 64x64, K steps of
 // 16; operands read element by element along whichever index is unit-stride (a wave
 // reads 256 contiguous bytes), every read bounds-checked, the next step prefetched into
 // registers.  LDS rows of 16 floats at a stride of 20: a 16-byte fragment read by 8
@@ -577,7 +577,7 @@ int pick_f32(const F32Params& p, hipStream_t st) {
 
 }  // namespace
 
-int launch_gemm_f32(const GemmF32Args& d, hipStream_t st) {
+int launch_gemm_f32(const GemmF32Args& d, Ws& ws, hipStream_t st) {
   const bool fits = d.M < (1ll << 31) && d.N < (1ll << 31) && d.K < (1ll << 31);
   const bool a_ok = d.sak == 1 && d.sam % 4 == 0 && al16(d.a) && d.sam >= d.K;
   const bool b_kc = d.sbk == 1 && d.sbn % 4 == 0 && al16(d.b) && d.sbn >= d.K;
@@ -597,21 +597,27 @@ int launch_gemm_f32(const GemmF32Args& d, hipStream_t st) {
     p.act = d.act;
     p.vec_store = d.scm % 4 == 0 && al16(d.c);
     p.kb = p.K;
+    if (ws.plan) return KORE_OK;
     return b_kc ? pick_f32<false>(p, st) : pick_f32<true>(p, st);
   }
   if (!fits) return set_error(KORE_EUNSUPPORTED, "gemm fp32: dimension >= 2^31");
   // Large problems in other layouts: pack A to [M, Kp] and B to [N, Kp] (K-contiguous,
-  // zero K tail) in the stream's scratch, then the MFMA kernel.
+  // zero K tail) in the caller's workspace, then the MFMA kernel.
   const int64_t Kp = (d.K + kF32BK - 1) / kF32BK * kF32BK;
   if (d.M * d.N * d.K >= (1ll << 26) && d.K >= kF32BK) {
     // an N-contiguous B with aligned K-rows is read in place by the ring kernel, its
     // buffer resource ending at the last real K-row (the padded rows read as zero)
     const bool b_inplace = b_nc && Kp * 4 * 128 + Kp * 4 < (1ll << 31) && d.sbk * 4 * Kp + d.N * 4 < (1ll << 31);
     const size_t a_bytes = (size_t)(d.M * Kp * 4 + 255) / 256 * 256;
-    float* ws = (float*)scratch_alloc(a_bytes + (b_inplace ? 0 : (size_t)d.N * Kp * 4), st);
-    if (ws != nullptr) {
-      float* ap = ws;
-      float* bp = (float*)((char*)ws + a_bytes);
+    const size_t total = a_bytes + (b_inplace ? 0 : (size_t)d.N * Kp * 4);
+    float* buf = (float*)ws.take(total);
+    if (ws.plan) return KORE_OK;
+    if (buf == nullptr)
+      return set_error(KORE_EWORKSPACE, "gemm fp32: packing the operands needs %zu workspace bytes (got %zu)",
+                       ws_bytes(total), ws.bytes);
+    {
+      float* ap = buf;
+      float* bp = (float*)((char*)buf + a_bytes);
       hipLaunchKernelGGL(pack32_kernel, dim3((unsigned)(Kp / 64), (unsigned)((d.M + 63) / 64)), dim3(256), 0, st,
                          (const float*)d.a, d.sam, d.sak, ap, (int)d.M, (int)d.K, (int)Kp);
       int rc = check_launch("pack32_kernel");
@@ -632,7 +638,6 @@ int launch_gemm_f32(const GemmF32Args& d, hipStream_t st) {
         p.vec_store = d.scm % 4 == 0 && al16(d.c);
         const int64_t t12864 = (d.M + 127) / 128 * ((d.N + 63) / 64);
         rc = t12864 >= 200 ? launch_f32_ring<64, 64, 3, true>(p, st) : launch_f32_ring<64, 64, 8, true>(p, st);
-        scratch_free(ws, st);
         return rc;
       }
       if (rc == KORE_OK) {
@@ -658,10 +663,10 @@ int launch_gemm_f32(const GemmF32Args& d, hipStream_t st) {
         p.kb = p.K;
         rc = pick_f32<false>(p, st);
       }
-      scratch_free(ws, st);
       return rc;
     }
   }
+  if (ws.plan) return KORE_OK;
   F32GenericParams g{};
   g.a = (const float*)d.a;
   g.b = (const float*)d.b;

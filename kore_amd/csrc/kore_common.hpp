@@ -150,11 +150,29 @@ int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 // Compute units of the current device (cached per device; 256 on MI355X).
 int device_cus();
-// Per-(device, stream) scratch, valid until the next scratch_alloc on that stream;
-// nullptr under graph capture or when unavailable (the caller falls back).  Every
-// scratch_alloc is paired with a scratch_free on the same stream.
-void* scratch_alloc(size_t bytes, hipStream_t stream);
-void scratch_free(void* p, hipStream_t stream);
+
+// Device scratch of one call: the caller's workspace (the library allocates none).
+// In plan mode nothing is launched: the dispatch only records in `need` the bytes
+// the path it picks would take, which is what the *_workspace_bytes queries return.
+struct Ws {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  bool plan = false;
+  size_t need = 0;
+  // Scratch of `n` bytes (256-byte aligned start) for the chosen path: nullptr in
+  // plan mode (after recording the need) or when the workspace is too small.
+  void* take(size_t n) {
+    if (plan) {
+      if (n > need) need = n;
+      return nullptr;
+    }
+    const uintptr_t base = ((uintptr_t)ptr + 255) & ~(uintptr_t)255;
+    if (ptr == nullptr || base - (uintptr_t)ptr + n > bytes) return nullptr;
+    return (void*)base;
+  }
+};
+// Bytes a workspace must hold so that take(n) succeeds whatever its alignment.
+inline size_t ws_bytes(size_t need) { return need == 0 ? 0 : need + 256; }
 
 // Top-1 grouped fp8 a8w8 GEMM over an expert-sorted token order (tiles of
 // gemm_fp8_blockscale.hip, called by the grouped entry in moe.hip): xq[M,K] (row
@@ -187,5 +205,5 @@ struct GemmF32Args {
   int64_t sam, sak, sbk, sbn, scm;
   int act;
 };
-int launch_gemm_f32(const GemmF32Args& d, hipStream_t st);
+int launch_gemm_f32(const GemmF32Args& d, Ws& ws, hipStream_t st);
 }  // namespace kore

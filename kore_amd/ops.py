@@ -42,6 +42,19 @@ def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+def _workspace(nbytes: int, device: torch.device):
+    """Device scratch of one call (a uint8 tensor, or None when the path needs none),
+    owned by torch's caching allocator -- under graph capture by the graph's private
+    pool.  The caller keeps it alive until the launch is enqueued."""
+    if nbytes == 0:
+        return None
+    return torch.empty((nbytes,), dtype=torch.uint8, device=device)
+
+
+def _ws_args(ws):
+    return (None, 0) if ws is None else (ws.data_ptr(), ws.numel())
+
+
 def _require_cuda(*ts: torch.Tensor) -> None:
     dev = None
     for t in ts:
@@ -85,11 +98,11 @@ def gemm_fused(a: torch.Tensor, b: torch.Tensor, bias: torch.Tensor | None = Non
     if M == 0 or N == 0:
         return c
     lib = _lib.load()
-    rc = lib.kore_gemm(DT_CODE[a.dtype], ACT_CODE[act], a.data_ptr(), a.stride(0), a.stride(1),
-                       b.data_ptr(), b.stride(0), b.stride(1),
-                       bias.data_ptr() if bias is not None else None,
-                       c.data_ptr(), c.stride(0), M, N, K, _stream(a))
-    _lib.check(rc)
+    args = (DT_CODE[a.dtype], ACT_CODE[act], a.data_ptr(), a.stride(0), a.stride(1),
+            b.data_ptr(), b.stride(0), b.stride(1), bias.data_ptr() if bias is not None else None,
+            c.data_ptr(), c.stride(0), M, N, K)
+    ws = _workspace(lib.kore_gemm_workspace_bytes(*args), a.device)
+    _lib.check(lib.kore_gemm(*args, *_ws_args(ws), _stream(a)))
     return c
 
 
@@ -149,10 +162,11 @@ def batched_gemm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     if Bn == 0 or M == 0 or N == 0:
         return c
     lib = _lib.load()
-    rc = lib.kore_batched_gemm(DT_CODE[a.dtype], a.data_ptr(), a.stride(0), a.stride(1), a.stride(2),
-                               b.data_ptr(), b.stride(0), b.stride(1), b.stride(2),
-                               c.data_ptr(), c.stride(0), c.stride(1), Bn, M, N, K, _stream(a))
-    _lib.check(rc)
+    args = (DT_CODE[a.dtype], a.data_ptr(), a.stride(0), a.stride(1), a.stride(2),
+            b.data_ptr(), b.stride(0), b.stride(1), b.stride(2),
+            c.data_ptr(), c.stride(0), c.stride(1), Bn, M, N, K)
+    ws = _workspace(lib.kore_batched_gemm_workspace_bytes(*args), a.device)
+    _lib.check(lib.kore_batched_gemm(*args, *_ws_args(ws), _stream(a)))
     return c
 
 
@@ -180,12 +194,10 @@ def gemm_backward(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor):
     if M == 0 or N == 0 or K == 0:
         return dx.zero_(), dw.zero_()
     lib = _lib.load()
-    nbytes = lib.kore_gemm_backward_workspace_bytes(M, N, K)
-    ws = torch.empty((nbytes,), dtype=torch.uint8, device=x.device)
-    rc = lib.kore_gemm_backward(DT_CODE[x.dtype], x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0),
-                                dy.data_ptr(), dy.stride(0), dx.data_ptr(), dx.stride(0), dw.data_ptr(),
-                                dw.stride(0), M, N, K, ws.data_ptr(), nbytes, _stream(x))
-    _lib.check(rc)
+    args = (DT_CODE[x.dtype], x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0),
+            dy.data_ptr(), dy.stride(0), dx.data_ptr(), dx.stride(0), dw.data_ptr(), dw.stride(0), M, N, K)
+    ws = _workspace(lib.kore_gemm_backward_workspace_bytes(*args), x.device)
+    _lib.check(lib.kore_gemm_backward(*args, *_ws_args(ws), _stream(x)))
     return dx, dw
 
 

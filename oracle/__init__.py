@@ -14,7 +14,9 @@ quant    OCP e4m3 fp8 codec, 1x128 / 128x128 quantisers, block-scaled GEMM oracl
 moe      router (softmax -> top-k -> renorm), fused-MoE oracle, sort/align oracle
 compare  the drivers' comparators (SNR, non-finite-aware allclose) and the
          four-prong per-pair verdict (rel-err + SNR + strict non-finite)
-inputs   seeded CPU input generators for every configuration the build measures
+
+The seeded input generators live in ``kore_amd/workloads.py`` (product side: the
+bench and the tests draw the same inputs from them).
 
 Parity status of each function (how it is pinned) is listed in its docstring;
 every function here is pinned by at least one check in ``tests/test_oracle_*.py``

@@ -129,11 +129,12 @@ def test_library_exports_every_declared_symbol(lib):
 def test_capi_validation_without_gpu(lib):
     """Argument checks run before any HIP call, so they are testable on the CPU."""
     fake = ctypes.c_void_p(256)
-    assert lib.kore_gemm(0, 0, fake, 8, 1, fake, 1, 8, None, fake, 8, 0, 8, 8, None) == 1   # M = 0
+    assert lib.kore_gemm(0, 0, fake, 8, 1, fake, 1, 8, None, fake, 8, 0, 8, 8, None, 0, None) == 1   # M = 0
     assert b"M, N, batch >= 1" in lib.kore_last_error()
-    assert lib.kore_gemm(0, 9, fake, 8, 1, fake, 1, 8, None, fake, 8, 8, 8, 8, None) == 1   # bad act
-    assert lib.kore_gemm(7, 0, fake, 8, 1, fake, 1, 8, None, fake, 8, 8, 8, 8, None) == 1   # bad dtype
-    assert lib.kore_gemm(0, 0, fake, 8, 1, fake, 1, 8, None, None, 8, 8, 8, 8, None) == 1   # null C
+    assert lib.kore_gemm(0, 9, fake, 8, 1, fake, 1, 8, None, fake, 8, 8, 8, 8, None, 0, None) == 1   # bad act
+    assert lib.kore_gemm(7, 0, fake, 8, 1, fake, 1, 8, None, fake, 8, 8, 8, 8, None, 0, None) == 1   # bad dtype
+    assert lib.kore_gemm(0, 0, fake, 8, 1, fake, 1, 8, None, None, 8, 8, 8, 8, None, 0, None) == 1   # null C
+    assert lib.kore_gemm_workspace_bytes(0, 0, fake, 8, 1, fake, 1, 8, None, fake, 8, 0, 8, 8) == 0
     assert lib.kore_gemm_a8w8_blockscale(fake, 4095, fake, 4095, fake, 32, 1, fake, 32, 1, fake, 128,
                                          16, 128, 4095, None) == 1
     assert b"multiples of 128" in lib.kore_last_error()
@@ -146,6 +147,44 @@ def test_capi_validation_without_gpu(lib):
     assert 0 < ws_small < ws_big
     assert lib.kore_fused_moe(fake, 4096, fake, fake, fake, fake, fake, 64, 4096, 14336, 8, 2, fake,
                               ws_small - 1, None) == 4   # workspace too small
+
+
+def test_gemm_workspace_queries_without_gpu(lib):
+    """The workspace a call needs is planned on the host by the same dispatch that
+    launches it: zero for the in-place engines, the packed operands for a K tail with
+    unaligned rows, the fp32 split-K partials for a decode-sized M.  A workspace smaller
+    than the query fails with KORE_EWORKSPACE before anything is launched."""
+    fake = ctypes.c_void_p(256)
+    # 4096^3, A and B = W.t() K-contiguous: the engines read both in place
+    assert lib.kore_gemm_workspace_bytes(0, 0, fake, 4096, 1, fake, 1, 4096, None, fake, 4096,
+                                         4096, 4096, 4096) == 0
+    # 512x1024x4095 with the task's [K, N] B: A packed to [512, 4096] bf16, B read in place
+    packed = lib.kore_gemm_workspace_bytes(0, 0, fake, 4095, 1, fake, 1024, 1, None, fake, 1024, 512, 1024, 4095)
+    assert 512 * 4096 * 2 <= packed <= 512 * 4096 * 2 + 1024
+    # the same with B = W.t() (rows of 4095 elements, unaligned): B is packed too
+    both = lib.kore_gemm_workspace_bytes(0, 0, fake, 4095, 1, fake, 1, 4095, None, fake, 1024, 512, 1024, 4095)
+    assert both >= packed + 1024 * 4096 * 2
+    # 1x2048x4096: split K, fp32 partials of the [1, 2048] output per slice
+    split = lib.kore_gemm_workspace_bytes(0, 0, fake, 4096, 1, fake, 2048, 1, None, fake, 2048, 1, 2048, 4096)
+    assert split > 0 and (split - 256) % (2048 * 4) == 0
+    rc = lib.kore_gemm(0, 0, fake, 4095, 1, fake, 1024, 1, None, fake, 1024, 512, 1024, 4095, None, 0, None)
+    assert rc == 4 and b"workspace bytes" in lib.kore_last_error()
+    # the query leaves room for a 256-byte alignment step; an aligned workspace one byte
+    # short of the packed operands is rejected
+    rc = lib.kore_gemm(0, 0, fake, 4095, 1, fake, 1024, 1, None, fake, 1024, 512, 1024, 4095, fake, packed - 257, None)
+    assert rc == 4
+    # fp32 K tail: A packed to [M, Kp] fp32
+    f32 = lib.kore_gemm_workspace_bytes(2, 0, fake, 4095, 1, fake, 1024, 1, None, fake, 1024, 512, 1024, 4095)
+    assert f32 >= 512 * 4096 * 4
+    # batched with B[i] = [N, K] K-contiguous: in place
+    assert lib.kore_batched_gemm_workspace_bytes(0, fake, 1024 * 128, 128, 1, fake, 1024 * 128, 128, 1, fake,
+                                                 1024 * 1024, 1024, 64, 1024, 1024, 128) == 0
+    # backward: dY^T [N, M] bf16 plus the GEMMs' own scratch (none at this shape)
+    bwd = lib.kore_gemm_backward_workspace_bytes(0, fake, 4096, fake, 4096, fake, 4096, fake, 4096, fake, 4096,
+                                                 8192, 4096, 4096)
+    assert 4096 * 8192 * 2 <= bwd <= 4096 * 8192 * 2 + 512
+    assert lib.kore_gemm_backward_workspace_bytes(0, fake, 4096, fake, 4096, fake, 4096, fake, 4096, fake, 4096,
+                                                  0, 4096, 4096) == 0
 
 
 # --------------------------------------------------------------------------- #
