@@ -88,6 +88,25 @@ int kore_gemm(int dtype, int act,
               void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * kore_gemm for callers that cannot allocate device memory (code under HIP graph
+ * capture that may not record allocations, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference: KORE's candidates allocate freely.
+ * Same arguments and results as kore_gemm without the workspace: the packed-operand
+ * and split-K scratch is a static device array of kore_gemm_noalloc_scratch_bytes()
+ * (64 MiB) per GPU, held from the library's first use on that GPU until the process
+ * exits.  Calls needing more fail with KORE_EWORKSPACE (use kore_gemm then); nothing
+ * is allocated or freed.  All calls on one GPU share that array, which keeps the last
+ * call's contents: calls that overlap on one GPU (other streams, other host threads)
+ * race -- serialise them.
+ */
+size_t kore_gemm_noalloc_scratch_bytes(void);
+int kore_gemm_noalloc(int dtype, int act,
+                      const void* a, int64_t lda_m, int64_t lda_k,
+                      const void* b, int64_t ldb_k, int64_t ldb_n,
+                      const void* bias, void* c, int64_t ldc_m,
+                      int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
  * Batched GEMM:  C[i] = A[i] @ B[i]^T  for i < batch, A[i] is [M,K], B[i] is [N,K].
  *   A (i,m,k) at a[i*sa_b + m*sa_m + k*sa_k]; B (i,n,k) at b[i*sb_b + n*sb_n + k*sb_k];
  *   C (i,m,n) at c[i*sc_b + m*sc_m + n].  fp32 accumulate, `dtype` out.  `workspace`

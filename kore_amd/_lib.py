@@ -25,6 +25,9 @@ SIGNATURES = {
                                         _i64, _i64, _i64]),
     "kore_gemm": (_i32, [_i32, _i32, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64,
                          _i64, _i64, _i64, _vp, _sz, _vp]),
+    "kore_gemm_noalloc_scratch_bytes": (_sz, []),
+    "kore_gemm_noalloc": (_i32, [_i32, _i32, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64,
+                                 _i64, _i64, _i64, _vp]),
     "kore_batched_gemm_workspace_bytes": (_sz, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
                                                 _vp, _i64, _i64, _i64, _i64, _i64, _i64]),
     "kore_batched_gemm": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,

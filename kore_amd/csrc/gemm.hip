@@ -1400,3 +1400,75 @@ extern "C" int kore_gemm_backward(int dtype, const void* x, int64_t ldx, const v
   GemmDesc gw = bwd_dw(dtype, x, ldx, dyt, dw, lddw, M, N, K);
   return run_gemm(gw, ws, st);
 }
+
+// ---------------------------------------------------------------------------------
+// kore_gemm_noalloc: kore_gemm for callers that cannot allocate device memory.  The
+// scratch of its packed and split-K paths is a file-scope device array: each GPU the
+// library runs on holds one copy (kNoAllocScratchBytes) from the library's first use on
+// it until the process ends.  Host code never passes the array's name to a kernel (on
+// the host it is only a stand-in symbol); the address hipGetSymbolAddress returns for
+// the current device is looked up once per device and used instead.  Every call on a
+// GPU shares that GPU's array: calls that overlap on one GPU (different streams, or
+// host threads) race.  The packed operands and split-K partials are written in full
+// before they are read, so nothing has to start at zero.
+// ---------------------------------------------------------------------------------
+#include <mutex>
+
+namespace kore {
+
+constexpr size_t kNoAllocScratchBytes = 64ull << 20;  // 64 MiB per GPU
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+void* g_scratch_ptr[64] = {};
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device (resolved once per device).
+int noalloc_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return set_error(KORE_EHIP, "gemm_noalloc: no current HIP device (%s)", hipGetErrorString(e));
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      return set_error(KORE_EHIP, "gemm_noalloc: hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                       hipGetErrorString(e));
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return KORE_OK;
+}
+}  // namespace
+}  // namespace kore
+
+extern "C" size_t kore_gemm_noalloc_scratch_bytes(void) { return kore::kNoAllocScratchBytes; }
+
+extern "C" int kore_gemm_noalloc(int dtype, int act, const void* a, int64_t lda_m, int64_t lda_k, const void* b,
+                                 int64_t ldb_k, int64_t ldb_n, const void* bias, void* c, int64_t ldc_m, int64_t M,
+                                 int64_t N, int64_t K, void* stream) {
+  using namespace kore;
+  GemmDesc d{dtype, act, a, b, bias, c, M, N, K, 1, lda_m, lda_k, ldb_k, ldb_n, ldc_m, 0, 0, 0};
+  void* base = nullptr;
+  int rc = noalloc_scratch(&base);
+  if (rc != KORE_OK) return rc;
+  Ws plan;
+  plan.plan = true;
+  rc = run_gemm(d, plan, nullptr);
+  if (rc != KORE_OK) return rc;
+  if (plan.need > kNoAllocScratchBytes)
+    return set_error(KORE_EWORKSPACE,
+                     "gemm_noalloc: this call needs %zu bytes of scratch, more than the %zu-byte static scratch "
+                     "(use kore_gemm with a workspace)",
+                     plan.need, kNoAllocScratchBytes);
+  Ws ws;
+  ws.ptr = base;
+  ws.bytes = kNoAllocScratchBytes;
+  return run_gemm(d, ws, stream);
+}
