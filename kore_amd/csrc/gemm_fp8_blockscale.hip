@@ -571,6 +571,305 @@ int launch_fp8_pipe(Fp8Params p, hipStream_t st) {
   return check_launch("gemm_fp8_pipe_kernel");
 }
 
+// ------------------------------------------------------------------------------
+// Wide block-scale kernel: 256 x 224 tiles, 8 waves.  2048 x 7168 (the BASELINE
+// shape) has exactly 8 x 32 = 256 such tiles, one per CU, where 256 x 256 tiles leave
+// 32 of the 256 CUs idle.  Waves form a 4 (M) x 2 (N) grid: every wave owns 64 rows
+// (two 32-row tiles); waves 0-3 own columns 0..127 of the tile (four 32-column tiles)
+// and waves 4-7 columns 128..223 (three).  Wave w runs on SIMD w % 4 next to wave
+// w + 4, so every SIMD multiplies 2 x (4 + 3) = 14 tiles of 32 x 32 per K block.
+//
+// Per 128-wide K block (= one scale block) a wave walks its tiles column by column:
+// tile (j, i) is two 32x32x64 MFMAs into a zeroed partial, and the partial of the
+// previous tile is promoted acc += partial * xs[m, kb] * ws[n/128, kb] between them
+// (each scale applied once, as in the oracle).  The A fragments of both row tiles stay
+// in registers for the whole block; B fragments are read one column ahead into a
+// double buffer.  The LDS ring (two slots; XOR-swizzled 128-byte rows, filled by
+// direct-to-LDS loads; scales travel in the same DMA stream) and the one barrier per
+// block follow the pipelined kernel above: the barrier sits at the first tile of
+// the last column, after the block's last B read and before the next block's first.
+// Requires M % 256 == 0, N % 224 == 0, K % 512 == 0 and K-contiguous scale rows.
+// ------------------------------------------------------------------------------
+// LDS: the A tiles of both slots, then the B tiles of both slots, then the ws copies
+// of both slots and the xs ring, so that every fragment read is one base register per
+// operand plus an immediate offset below 64 KiB.
+// LDS reads through a 32-bit LDS byte offset held in a VGPR plus a compile-time
+// immediate.  The offset is made opaque to the compiler (an empty asm), so it keeps
+// one register per base and folds the constant into the ds_read offset field instead
+// of materialising a new address register per read.
+// Calls f(std::integral_constant<int, t>) for t = 0 .. N-1 (a compile-time loop).
+template <int T, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (T < N) {
+    f(std::integral_constant<int, T>{});
+    static_for<T + 1, N>(f);
+  }
+}
+
+typedef __attribute__((address_space(3))) const u32x4_t* lds_cv4;
+typedef __attribute__((address_space(3))) const float* lds_cf;
+typedef __attribute__((address_space(3))) uint8_t* lds_u8;
+__device__ __forceinline__ uint32_t lds_offset_of(const void* p) {
+  uint32_t v = (uint32_t)(uintptr_t)(lds_u8)(p);
+  asm volatile("" : "+v"(v));
+  return v;
+}
+__device__ __forceinline__ u32x4_t lds_ld16(uint32_t off) { return *(lds_cv4)(uintptr_t)off; }
+__device__ __forceinline__ float lds_ldf(uint32_t off) { return *(lds_cf)(uintptr_t)off; }
+template <int IMM>
+__device__ __forceinline__ i32x8_t lds_frag32_imm(const uint32_t (&base)[2]) {
+  const u32x4_t lo = lds_ld16(base[0] + IMM);
+  const u32x4_t hi = lds_ld16(base[1] + IMM);
+  return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+
+struct WideCfg {
+  static constexpr int BM = 256, BN = 224, NW = 8, MI = 2;
+  static constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
+  static constexpr int B_BASE = 2 * A_BYTES;            // B tile of slot s at B_BASE + s * B_BYTES
+  static constexpr int NWB = 3;                         // weight-scale blocks a tile can touch
+  static constexpr int W_BASE = B_BASE + 2 * B_BYTES;   // ws copies of slot s (1 KiB per block)
+  static constexpr int RING = W_BASE + 2 * NWB * 1024;  // xs ring (2 x 4 K blocks)
+  static constexpr int LDS = RING + 2 * 4096;
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+  static_assert(NW * 64 * 128 * 2 <= LDS, "epilogue staging fits");
+};
+
+// Main loop and epilogue of one wave with NI column tiles (4: waves 0-3, 3: waves
+// 4-7).  A wave issues 4 A loads, NI B loads and 1 scale load per stage.
+template <int NI>
+__device__ __forceinline__ void fp8_wide_wave(const Fp8Params& p, uint8_t* lds, int wave, int lane, int m0, int n0) {
+  using C = WideCfg;
+  constexpr int MI = C::MI, AQ = 4, BQ = NI, LPS = AQ + BQ + 1;
+  constexpr int NT = MI * NI, TB = 2 * (NI - 1);  // barrier tile: (j = NI-1, i = 0)
+  // The loads of block s+2 (into the slot released at block s's barrier) are spread
+  // over NU = NT - 2 issue tiles: tiles TB .. NT-1 of block s, then tiles 0 .. TB-3 of
+  // block s+1 (they must land by its barrier).  Issue tile u takes loads
+  // [u * LPS / NU, (u + 1) * LPS / NU): bunching them into two tiles filled the TA
+  // queue and stalled the waves at issue.
+  constexpr int NU = NT - 2, U0 = NT - TB;  // U0: issue tiles in the releasing block
+  const int lr = lane & 31, hh = lane >> 5;
+  const int wm = wave & 3;
+  const int rowA0 = 64 * wm, colB0 = wave < 4 ? 0 : 128;
+  const int nk = p.K / 128;
+
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.xq + (int64_t)m0 * p.ldx, (uint32_t)(C::BM * p.ldx));
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.wq + (int64_t)n0 * p.ldw, (uint32_t)(C::BN * p.ldw));
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(p.xs + (int64_t)m0 * p.xs_m, (uint32_t)(((C::BM - 1) * p.xs_m + (nk - 1) + 1) * 4));
+  const int wblk0 = n0 / 128;  // first weight-scale block of the tile
+  const __amdgpu_buffer_rsrc_t rw =
+      make_rsrc(p.ws + (int64_t)wblk0 * p.ws_n,
+                (uint32_t)((((int64_t)p.N / 128 - 1 - wblk0) * p.ws_n + (nk - 1) + 1) * 4));
+  // DMA: load q of a wave covers tile rows 8 * (wave + 8q) + lane / 8, whose row % 32 is
+  // 8 * (wave % 4) + lane / 8 for every q; lane l fetches chunk (l % 8) ^ key(row % 32)
+  const int lrow = lane >> 3;
+  const int dchunk = (lane & 7) ^ f8_key(8 * (wave & 3) + lrow);
+  const uint32_t a_voff = (uint32_t)((lrow + 8 * wave) * p.ldx + 16 * dchunk);
+  const uint32_t b_voff = (uint32_t)((lrow + 8 * wave) * p.ldw + 16 * dchunk);
+  const uint32_t a_rstep = (uint32_t)(64 * p.ldx), b_rstep = (uint32_t)(64 * p.ldw);
+  const uint32_t x_voff = (uint32_t)((64 * (wave & 3) + lane) * p.xs_m * 4);
+  // scale load of this wave: waves 0-3 load the xs of 64 rows (4 K blocks per 16 bytes)
+  // at every fourth block and otherwise a copy of ws block wave % 3; waves 4-7 load
+  // ws block (wave - 4) % 3 (64 copies of 4 K blocks each)
+  const int wblk_ld = wave < 4 ? wave % 3 : (wave - 4) % 3;
+  const uint32_t w_soff = (uint32_t)(wblk_ld * p.ws_n * 4);
+
+  auto issue = [&](int slot, int kb, int q) {
+    if (q < AQ) {
+      buf_lds(ra, a_voff, (uint32_t)kb * 128u + (uint32_t)q * a_rstep,
+              lds + slot * C::A_BYTES + (wave + 8 * q) * 1024, 16);
+    } else if (q < AQ + BQ) {
+      buf_lds(rb, b_voff, (uint32_t)kb * 128u + (uint32_t)(q - AQ) * b_rstep,
+              lds + C::B_BASE + slot * C::B_BYTES + (wave + 8 * (q - AQ)) * 1024, 16);
+    } else {
+      const bool xload = wave < 4 && (kb & 3) == 0;
+      uint8_t* dst = xload ? lds + C::RING + ((kb >> 2) & 1) * 4096 + (wave & 3) * 1024
+                           : lds + C::W_BASE + (slot * C::NWB + wblk_ld) * 1024;
+      buf_lds(xload ? rx : rw, xload ? x_voff : 0u, xload ? (uint32_t)kb * 4u : w_soff + (uint32_t)(kb & ~3) * 4u,
+              dst, 16);
+    }
+  };
+
+  // fragment read offsets: row lr of a 32-row block, K half h, 16-byte half e
+  const int key = f8_key(lr);
+  int off[2][2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) off[h][e] = lr * 128 + (((4 * h + 2 * hh + e) ^ key) << 4);
+  // weight-scale block of each column tile, relative to the tile's first block
+  int wsb[NI];
+#pragma unroll
+  for (int j = 0; j < NI; ++j) wsb[j] = (n0 + colB0 + 32 * j) / 128 - wblk0;
+
+  f32x16_t acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  f32x16_t part[2];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) part[1][r] = 0.0f;
+  const f32x16_t zero = {};
+  float sc_last = 0.0f, xsv_[MI] = {}, wsv_[NI] = {};
+  i32x8_t af[MI][2], bf[2][2];  // af[i][h]; bf[buffer][h]
+
+  // prologue: block 0, and the share of block 1 normally issued at the end of the
+  // block before it; wait for block 0
+  constexpr int P1 = U0 * LPS / NU;
+#pragma unroll
+  for (int q = 0; q < LPS; ++q) issue(0, 0, q);
+#pragma unroll
+  for (int q = 0; q < P1; ++q) issue(1, min(1, nk - 1), q);
+  wait_vmcnt<P1>();
+  exec_barrier();
+  // fragment bases (LDS byte offsets): A row block 0 and B column block 0 of slot 0,
+  // per K half h and 16-byte half e; slot, row and column offsets are immediates
+  uint32_t ab[2][2], bbv[2][2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      ab[h][e] = lds_offset_of(lds + rowA0 * 128 + off[h][e]);
+      bbv[h][e] = lds_offset_of(lds + C::B_BASE + colB0 * 128 + off[h][e]);
+    }
+  // xs of row block 0 (16 bytes per row: 4 K blocks) and the ws copies of slot 0
+  const uint32_t xbase = lds_offset_of(lds + C::RING + (rowA0 + lr) * 16);
+  const uint32_t wbase = lds_offset_of(lds + C::W_BASE);
+  af[0][0] = lds_frag32_imm<0>(ab[0]);
+  af[0][1] = lds_frag32_imm<0>(ab[1]);
+  af[1][0] = lds_frag32_imm<32 * 128>(ab[0]);
+  af[1][1] = lds_frag32_imm<32 * 128>(ab[1]);
+  bf[0][0] = lds_frag32_imm<0>(bbv[0]);
+  bf[0][1] = lds_frag32_imm<0>(bbv[1]);
+
+  // one K block; SL: its slot, PB: the bf buffer of its column 0 (both compile-time)
+  auto stage = [&](int s, auto sl_tag, auto pb_tag) {
+    constexpr int SL = decltype(sl_tag)::value, PB = decltype(pb_tag)::value;
+    constexpr int A_NXT = (SL ^ 1) * C::A_BYTES, B_CUR = SL * C::B_BYTES, B_NXT = (SL ^ 1) * C::B_BYTES;
+    constexpr int W_CUR = SL * C::NWB * 1024;
+    const int kb1 = min(s + 1, nk - 1), kb2 = min(s + 2, nk - 1);
+    static_for<0, NT>([&](auto tt) {
+      constexpr int t = decltype(tt)::value;
+      constexpr int j = t / MI, i = t % MI;
+      constexpr int bb = (PB + j) & 1;
+      if constexpr (t == TB) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        wait_vmcnt<0>();
+        exec_barrier();
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      part[t & 1] = mma32_fp8(bf[bb][0], af[i][0], zero);
+      __builtin_amdgcn_sched_barrier(0);
+      {
+        // promote the previous tile (t == 0: the last tile of the previous block)
+        constexpr int pi = t == 0 ? MI - 1 : (t - 1) % MI, pj = t == 0 ? NI - 1 : (t - 1) / MI;
+        const float f = t == 0 ? sc_last : xsv_[pi] * wsv_[pj];
+        f32x16_t& a = acc[pi][pj];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) a[r] = fmaf(part[(t + 1) & 1][r], f, a[r]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      part[t & 1] = mma32_fp8(bf[bb][1], af[i][1], part[t & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (t == NT - 1) sc_last = xsv_[MI - 1] * wsv_[NI - 1];
+      // LDS reads: this block's scales at t == 0; B column j + 1 at tile (j, 0); after
+      // the barrier B column 0 and the A fragments of the next block
+      if constexpr (t == 0) {
+        const uint32_t xo = xbase + (uint32_t)(((s >> 2) & 1) * 4096 + (s & 3) * 4);
+        const uint32_t wo = wbase + (uint32_t)((s & 3) * 4);
+        xsv_[0] = lds_ldf(xo);
+        xsv_[1] = lds_ldf(xo + 32 * 16);
+        const float w0 = lds_ldf(wo + W_CUR), w1 = lds_ldf(wo + W_CUR + 1024), w2 = lds_ldf(wo + W_CUR + 2048);
+#pragma unroll
+        for (int jj = 0; jj < NI; ++jj) wsv_[jj] = wsb[jj] == 0 ? w0 : (wsb[jj] == 1 ? w1 : w2);
+      }
+      if constexpr (i == 0 && j + 1 < NI) {
+        bf[bb ^ 1][0] = lds_frag32_imm<B_CUR + 32 * 128 * (j + 1)>(bbv[0]);
+        bf[bb ^ 1][1] = lds_frag32_imm<B_CUR + 32 * 128 * (j + 1)>(bbv[1]);
+      }
+      if constexpr (t == TB) {
+        bf[bb ^ 1][0] = lds_frag32_imm<B_NXT>(bbv[0]);
+        bf[bb ^ 1][1] = lds_frag32_imm<B_NXT>(bbv[1]);
+        af[0][0] = lds_frag32_imm<A_NXT>(ab[0]);
+        af[0][1] = lds_frag32_imm<A_NXT>(ab[1]);
+      }
+      if constexpr (t == NT - 1) {
+        af[1][0] = lds_frag32_imm<A_NXT + 32 * 128>(ab[0]);
+        af[1][1] = lds_frag32_imm<A_NXT + 32 * 128>(ab[1]);
+      }
+      // loads: the rest of block s+1 (slot SL^1) early in the block, the first share of
+      // block s+2 (slot SL, released at this block's barrier) after the barrier
+      if constexpr (t < TB - 2 || t >= TB) {
+        constexpr int u = t >= TB ? t - TB : U0 + t;
+        constexpr int q0 = u * LPS / NU, q1 = (u + 1) * LPS / NU;
+#pragma unroll
+        for (int q = q0; q < q1; ++q) {
+          if constexpr (t >= TB) issue(SL, kb2, q);
+          else issue(SL ^ 1, kb1, q);
+        }
+      }
+    });
+  };
+  // blocks in pairs so that the slot and the bf buffer parity are compile-time
+  for (int s = 0; s < nk; s += 2) {
+    stage(s, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+    stage(s + 1, std::integral_constant<int, 1>{}, std::integral_constant<int, NI & 1>{});
+  }
+  // promote the last tile of the last block
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[MI - 1][NI - 1][r] = fmaf(part[(NT - 1) & 1][r], sc_last, acc[MI - 1][NI - 1][r]);
+  wait_vmcnt<0>();  // the clamped trailing loads must land before LDS is reused
+  __syncthreads();
+
+  // epilogue: bf16 pack, stage the wave's 64 x 128 tile in LDS, 16-byte row stores
+  using St = Stager<64, 128>;
+  using Op = MfmaOp<BF16>;
+  uint16_t* stg = (uint16_t*)lds + wave * (64 * 128);
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        St::put(stg, out_row(i, lane), out_col(j, g, lane),
+                u32x2_t{Op::pack2(acc[i][j][4 * g], acc[i][j][4 * g + 1]),
+                        Op::pack2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3])});
+  __syncthreads();
+  const int mw0 = m0 + rowA0, nw0 = n0 + colB0;
+  const bool vec = p.vec_store != 0;
+  St::drain(stg, lane, [&](int row, int col, u32x4_t v) {
+    if (col < 32 * NI) store_row8(p.y + (int64_t)(mw0 + row) * p.ldy + nw0 + col, nw0 + col, p.N, vec, v);
+  });
+}
+
+__global__ void __launch_bounds__(512) gemm_fp8_wide_kernel(const Fp8Params p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[WideCfg::LDS];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // XCD-aware order: each XCD's 32 consecutive tiles form 4 M-tiles x 8 N-tiles
+  const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int width = kFp8GroupM * p.tiles_n;
+  const int grp = bid / width;
+  const int first_m = grp * kFp8GroupM;
+  const int gsz = min(p.tiles_m - first_m, kFp8GroupM);
+  const int tl = bid - grp * width;
+  const int m0 = (first_m + tl % gsz) * WideCfg::BM;
+  const int n0 = (tl / gsz) * WideCfg::BN;
+  if (wave < 4) fp8_wide_wave<4>(p, lds, wave, lane, m0, n0);
+  else fp8_wide_wave<3>(p, lds, wave, lane, m0, n0);
+}
+
+int launch_fp8_wide(Fp8Params p, hipStream_t st) {
+  p.tiles_m = p.M / WideCfg::BM;
+  p.tiles_n = p.N / WideCfg::BN;
+  hipLaunchKernelGGL(gemm_fp8_wide_kernel, dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(512), 0, st, p);
+  return check_launch("gemm_fp8_wide_kernel");
+}
+
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // ------------------------------------------------------------------------------
@@ -865,6 +1164,15 @@ extern "C" int kore_gemm_a8w8_blockscale(const void* xq, int64_t ldx, const void
     // 128x128 tiles on 4 waves (four slots) double the tile count again
     const int64_t tiles256 = (M + 255) / 256 * (N / 256);
     const int64_t tiles256x128 = (M + 255) / 256 * (N / 128);
+    // 256 x 224 tiles when they take fewer CU-rounds of tile area than 256 x 256 ones
+    // (2048 x 7168: 256 tiles, one per CU, against 224 tiles on 256 CUs)
+    const int64_t cus = device_cus();
+    if (xs4 && M % 256 == 0 && N % 224 == 0 && (K / 128) % 4 == 0) {
+      const int64_t t224 = (M / 256) * (N / 224);
+      const int64_t cost224 = (t224 + cus - 1) / cus * 224;
+      const int64_t cost256 = N % 256 == 0 ? (tiles256 + cus - 1) / cus * 256 : INT64_MAX;
+      if (t224 >= cus / 2 && cost224 < cost256) return launch_fp8_wide(p, st);
+    }
     if (N % 256 == 0 && tiles256 >= 192) {
       return xs4 ? launch_fp8_pipe<F8Cfg<256, 256, 8, 2, true>>(p, st)
                  : launch_fp8_pipe<F8Cfg<256, 256, 8, 2, false>>(p, st);

@@ -54,6 +54,26 @@ def test_fp8_wide_tiles(gpu, M, N, K):
     pair_only(out, ref, "fp8", f"{M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("M,N,K", [(2048, 7168, 512), (1024, 7168, 2048), (2048, 4480, 1024), (4096, 7168, 512)])
+def test_fp8_224_tiles(gpu, M, N, K):
+    """M % 256 == 0, N % 224 == 0, K % 512 == 0 with contiguous scales, where 256 x 224
+    tiles take fewer CU-rounds than 256 x 256 ones (one tile per CU at 2048 x 7168 and
+    1024 x 7168; N = 4480 is not a multiple of 256; 4096 x 7168 runs two rounds):
+    parity, bit-exact reruns and power-of-two scale invariance.  Every output element
+    sums the same partial products in the same order as the 256 x 256 / 256 x 128
+    kernels, which column-major x_scale views select: the two must agree bit for bit."""
+    xq, wq, xs, ws = W.fp8_inputs(M, N, K, seed=M + N + K, scale=0.2)
+    out = _run(gpu, xq, wq, xs, ws)
+    ref = matmul_blockscale_ref(xq, wq, xs, ws)
+    verdict(out, ref, "blockscale", "fp8", f"{M}x{N}x{K}")
+    verdict(out, ref, "blockscale_genv", "fp8", f"{M}x{N}x{K} (1e-2)")
+    pair_only(out, ref, "fp8", f"{M}x{N}x{K}")
+    assert bit_equal(_run(gpu, xq, wq, xs, ws), out)
+    assert bit_equal(_run(gpu, xq, wq, xs * 4, ws), out * 4)
+    xs_cm = xs.t().contiguous().t()
+    assert bit_equal(_run(gpu, xq, wq, xs_cm, ws), out), "differs from the 256-row tile kernels"
+
+
 @pytest.mark.parametrize("regime", ["zeros", "ones", "large", "small"])
 def test_fp8_adversarial(gpu, regime):
     """The task's authored adversarial battery (kore/tasks/vendor_ops.py:526-543)."""
