@@ -1,8 +1,11 @@
-"""Build libkore_amd.so (gfx950) in-tree with hipcc.
+"""Build libkore_amd.so (gfx950) and the kore_amd._C host extension in-tree.
 
 Every source under ``kore_amd/csrc`` is compiled to an object for gfx950 (in
 parallel), then linked into ``kore_amd/libkore_amd.so``.  Objects go to
-``kore_amd/_build``.  Run ``python -m kore_amd.build`` or call :func:`build`.
+``kore_amd/_build``.  ``kore_amd/ext/kore_ops.cpp`` (the PyTorch-ROCm operators over
+the C ABI) is then compiled against torch into ``kore_amd/_C.so``, linked to
+``libkore_amd.so`` through an ``$ORIGIN`` runpath.  Run ``python -m kore_amd.build``
+or call :func:`build`.
 """
 
 from __future__ import annotations
@@ -19,6 +22,8 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libkore_amd.so"
+EXT_SRC = PKG / "ext" / "kore_ops.cpp"
+EXT = PKG / "_C.so"
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -88,7 +93,36 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError("link of libkore_amd.so failed")
     os.replace(tmp, LIB)
+    build_ext(verbose)
     return LIB
+
+
+def build_ext(verbose: bool = False) -> Path:
+    """Compile the torch host extension kore_amd/_C.so against the built library."""
+    import sysconfig
+
+    import torch
+
+    tdir = Path(torch.__file__).resolve().parent
+    cxx = os.environ.get("CXX", "g++")
+    abi = int(torch.compiled_with_cxx11_abi())
+    tmp = EXT.with_suffix(".so.tmp")
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wno-unused-function",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", "-DTORCH_EXTENSION_NAME=_C",
+           "-DTORCH_API_INCLUDE_EXTENSION_H", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           f"-I{tdir / 'include'}", f"-I{tdir / 'include' / 'torch' / 'csrc' / 'api' / 'include'}",
+           "-I/opt/rocm/include", f"-I{sysconfig.get_paths()['include']}", f"-I{PKG.parent / 'include'}",
+           str(EXT_SRC), f"-L{tdir / 'lib'}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+           f"-L{PKG}", "-l:libkore_amd.so", "-Wl,-rpath,$ORIGIN", "-o", str(tmp)]
+    t0 = time.time()
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError("build of kore_amd/_C.so failed")
+    os.replace(tmp, EXT)
+    if verbose:
+        print(f"  compiled _C.so in {time.time() - t0:.1f}s")
+    return EXT
 
 
 if __name__ == "__main__":

@@ -272,9 +272,29 @@ def test_every_fusion_op_has_candidates():
             assert (CAND / f"gen_{op}_{dt}" / "kernel.py").exists()
 
 
+def test_host_extension_registers_every_operator():
+    """The product's host layer is the C++ extension kore_amd._C (over the C ABI): every
+    operator is bound on the module and registered as torch.ops.korehip.<op>, with the
+    schema the drivers' callables need."""
+    import kore_amd
+    from kore_amd import _C
+
+    ops = ["gemm", "gemm_fused", "batched_gemm", "gemm_backward", "gemm_a8w8_blockscale", "gemm_a8w8",
+           "moe_align", "fused_moe", "grouped_gemm", "grouped_gemm_fp8", "gather_rows", "scatter_rows"]
+    for op in ops:
+        assert callable(getattr(_C, op)), op
+        assert hasattr(torch.ops.korehip, op), op
+    assert str(torch.ops.korehip.gemm_fused.default._schema) == \
+        "korehip::gemm_fused(Tensor a, Tensor b, Tensor? bias, int act) -> Tensor"
+    assert "libkore_amd.so" in open("/proc/self/maps").read()
+    assert kore_amd.ops._C is _C
+
+
 def test_ops_fail_loudly_without_device_tensors():
     import kore_amd
 
     a = torch.zeros((4, 8), dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="HIP device"):
         kore_amd.gemm(a, a.t())
+    with pytest.raises(ValueError, match="HIP device"):
+        torch.ops.korehip.gemm_a8w8_blockscale(a, a, a, a)
