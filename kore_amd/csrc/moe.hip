@@ -1,10 +1,10 @@
 // Fused top-k MoE with SiLU gated MLP (bf16) for gfx950.
 //
 // Pipeline (all on the caller's stream, no host synchronisation):
-//  1. moe_align_kernel: expert histogram -> block-padded offsets -> stable,
+//  1. moe_align_chunk_kernel: expert histogram -> block-padded offsets -> stable,
 //     expert-sorted slot list (slot s = t*topk + k) and the expert of every
-//     BM-row block.  One workgroup; ranks come from wave ballots, so the result is
-//     deterministic and ascending in slot order inside each expert.
+//     BM-row block.  One workgroup per 256 slots, each computing the histogram it
+//     needs itself; deterministic and ascending in slot order inside each expert.
 //  2. moe_gateup_kernel: for every BM-row block of sorted slots (one expert e) and
 //     every 128/BN-wide column tile of the intermediate dim, A rows are the gathered
 //     tokens hidden[s/topk] and B rows are w1[e] gate and up rows interleaved so that
@@ -33,72 +33,71 @@ namespace {
 // ------------------------------------------------------------------------------
 // 1. sort / align
 // ------------------------------------------------------------------------------
-constexpr int kAlignThreads = 1024;
 constexpr int kAlignMaxE = 1024;
 
-// One workgroup, three barrier-separated phases, no loop over all experts in one
-// thread.  Wave w owns the contiguous slot range of 64-slot groups
-// [w*G, (w+1)*G), so slot order is wave order, then group order, then lane order.
-//  A. each wave counts its slots per expert (one ballot per distinct expert of a
-//     group, counts added to the wave's own LDS row: no barrier inside the phase);
-//  B. thread per expert: histogram = sum of the wave counts, padded offsets by a
-//     wave-shuffle scan, then each wave's start inside the expert;
-//  C. each wave replays its groups and places slot s at its expert's running start
-//     plus its rank in the group.
-// Padding sentinels and block owners are written in B; ids are read in batches of
-// 8 groups so one memory latency covers 8 groups.
-constexpr int kAlignBatch = 8;
+// Chunked sort / align: workgroup g owns R consecutive 256-slot sub-chunks of the slot
+// list (R = 1 up to 65536 slots, so at most 256 workgroups), with no communication
+// between workgroups.  Every workgroup reads all the ids (S ints, L2-resident) and
+// builds in LDS the full expert histogram and the count of each expert in the slots
+// before its range; a block-wide scan of the padded counts gives the expert starts.
+// Slot c + t of a sub-chunk then goes to
+//   start[e] + (slots of e before the sub-chunk) + (slots of e before it in the sub-chunk),
+// the last term from per-wave expert counts and a scan of the wave's ids, so the order
+// inside an expert is ascending slot order, as in the oracle.  The workgroups split the padding
+// sentinels, the tail past the last expert and the block owners between them;
+// workgroup 0 writes the offsets.
+constexpr int kChunk = 256;
 
-__global__ void __launch_bounds__(kAlignThreads)
-    moe_align_kernel(const int32_t* __restrict__ ids, int S, int E, int block, int32_t* __restrict__ offsets,
-                     int32_t* __restrict__ sorted, int32_t* __restrict__ block_expert, int cap) {
-  constexpr int NW = kAlignThreads / 64;
-  __shared__ int cnt[kAlignMaxE];       // tokens per expert
-  __shared__ int base[kAlignMaxE];      // padded start of each expert
-  __shared__ int wrun[NW][kAlignMaxE];  // A: per-wave counts; C: per-wave next slot
-  __shared__ int wsum[NW];
-  __shared__ int s_total;
+__global__ void __launch_bounds__(kChunk)
+    moe_align_chunk_kernel(const int32_t* __restrict__ ids, int S, int E, int block, int R,
+                           int32_t* __restrict__ offsets, int32_t* __restrict__ sorted,
+                           int32_t* __restrict__ block_expert, int cap) {
+  __shared__ int hist[kAlignMaxE], pre[kAlignMaxE], base[kAlignMaxE];
+  __shared__ int wcnt[kChunk / 64][kAlignMaxE];  // per-wave expert counts of a sub-chunk
+  __shared__ __attribute__((aligned(16))) int cid[kChunk];
+  __shared__ int wsum[kChunk / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int ngroups = (S + 63) / 64;
-  const int gpw = (ngroups + NW - 1) / NW;
-  const int g0 = wave * gpw, g1 = min(g0 + gpw, ngroups);
-  for (int e = lane; e < E; e += 64) wrun[wave][e] = 0;  // the wave's own row
-
-  // visit this wave's groups in slot order; for each group, f(s, e, valid) runs the
-  // per-distinct-expert ballot loop (wave-uniform trip count, scalar lane reads)
-  auto for_groups = [&](auto&& f) {
-    for (int gb = g0; gb < g1; gb += kAlignBatch) {
-      int ev[kAlignBatch];
+  const int g = (int)blockIdx.x, G = (int)gridDim.x;
+  const int first = g * R;  // first sub-chunk of this workgroup
+  // this thread's slot of the first sub-chunk, loaded with the first histogram batch
+  int my_e0 = first * kChunk + tid < S ? ids[first * kChunk + tid] : -1;
+  for (int e = tid; e < E; e += kChunk) {
+    hist[e] = pre[e] = 0;
 #pragma unroll
-      for (int u = 0; u < kAlignBatch; ++u) {
-        const int s = (gb + u) * 64 + lane;
-        ev[u] = (gb + u < g1 && s < S) ? ids[s] : -1;
-      }
-#pragma unroll
-      for (int u = 0; u < kAlignBatch; ++u) f((gb + u) * 64 + lane, ev[u], ev[u] >= 0 && ev[u] < E);
-    }
-  };
-  // A: per-wave counts (one LDS add per distinct expert of a group)
-  for_groups([&](int, int e, bool valid) {
-    unsigned long long todo = __ballot(valid);
-    while (todo) {
-      const int leader = __builtin_ctzll(todo);
-      const int le = __builtin_amdgcn_readlane(e, leader);
-      const unsigned long long m = __ballot(valid && e == le);
-      if (lane == leader) atomicAdd(&wrun[wave][le], __popcll(m));
-      todo &= ~m;
-    }
-  });
-  __syncthreads();
-  // B: histogram, padded offsets (thread t = expert t; E <= kAlignThreads), wave starts
-  int mine = 0;
-  if (tid < E) {
-    int c = 0;
-    for (int w = 0; w < NW; ++w) c += wrun[w][tid];
-    cnt[tid] = c;
-    mine = (c + block - 1) / block * block;
+    for (int w = 0; w < kChunk / 64; ++w) wcnt[w][e] = 0;
   }
-  int incl = mine;
+  __syncthreads();
+  // histogram of every slot; sub-chunk i covers slots [256 i, 256 i + 256), all of
+  // them before this workgroup's range when i < first.  Ids are loaded in batches of
+  // kBatch sub-chunks so one memory latency covers the batch.
+  constexpr int kBatch = 16;
+  const int nsub = (S + kChunk - 1) / kChunk;
+  for (int i0 = 0; i0 < nsub; i0 += kBatch) {
+    int ev[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int sl = (i0 + u) * kChunk + tid;
+      ev[u] = sl < S ? ids[sl] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      if (ev[u] >= 0 && ev[u] < E) {
+        atomicAdd(&hist[ev[u]], 1);
+        if (i0 + u < first) atomicAdd(&pre[ev[u]], 1);
+      }
+    }
+  }
+  __syncthreads();
+  // padded exclusive scan over experts: thread t owns experts [q t, q t + q)
+  constexpr int Q = kAlignMaxE / kChunk;
+  int local[Q], sum = 0;
+#pragma unroll
+  for (int k = 0; k < Q; ++k) {
+    const int e = Q * tid + k;
+    local[k] = e < E ? (hist[e] + block - 1) / block * block : 0;
+    sum += local[k];
+  }
+  int incl = sum;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
     const int y = __shfl_up(incl, d);
@@ -106,67 +105,75 @@ __global__ void __launch_bounds__(kAlignThreads)
   }
   if (lane == 63) wsum[wave] = incl;
   __syncthreads();
-  if (tid == 0) {
-    int r = 0;
-    for (int w = 0; w < NW; ++w) {
-      const int v = wsum[w];
-      wsum[w] = r;
-      r += v;
-    }
-    s_total = r;
-    offsets[E] = r;
+  int before = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < kChunk / 64; ++w) {
+    before += w < wave ? wsum[w] : 0;
+    total += wsum[w];
   }
-  __syncthreads();
-  const int total = s_total;
-  if (tid < E) {
-    const int excl = wsum[wave] + incl - mine;
-    base[tid] = excl;
-    offsets[tid] = excl;
-    int r = excl;
-    for (int w = 0; w < NW; ++w) {
-      const int v = wrun[w][tid];
-      wrun[w][tid] = r;
-      r += v;
+  int run = before + incl - sum;
+#pragma unroll
+  for (int k = 0; k < Q; ++k) {
+    const int e = Q * tid + k;
+    if (e < E) {
+      base[e] = run;
+      if (g == 0) offsets[e] = run;
+    }
+    run += local[k];
+  }
+  if (g == 0 && tid == 0) offsets[E] = total;
+  // place the slots of each sub-chunk, stable: a slot's rank is the count of its expert
+  // in the earlier waves of the sub-chunk (per-wave counts, LDS atomics) plus the count
+  // among the earlier lanes of its wave (a scan of the wave's 64 ids in LDS); then the
+  // per-expert counts advance past the sub-chunk
+  for (int r = 0; r < R; ++r) {
+    const int my_s = (first + r) * kChunk + tid;
+    const int my_e = r == 0 ? my_e0 : (my_s < S ? ids[my_s] : -1);
+    const bool valid = my_e >= 0 && my_e < E;
+    cid[tid] = my_e;
+    if (valid) atomicAdd(&wcnt[wave][my_e], 1);
+    __syncthreads();
+    if (valid) {
+      int rank = 0;
+      const int4* c4 = (const int4*)(cid + wave * 64);
+      int4 v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = c4[u];
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        rank += (4 * u < lane && v[u].x == my_e) + (4 * u + 1 < lane && v[u].y == my_e) +
+                (4 * u + 2 < lane && v[u].z == my_e) + (4 * u + 3 < lane && v[u].w == my_e);
+      for (int w = 0; w < wave; ++w) rank += wcnt[w][my_e];
+      sorted[base[my_e] + pre[my_e] + rank] = my_s;
+    }
+    __syncthreads();  // pre[], wcnt[] and cid[] are read: advance pre, clear this wave's counts
+    if (valid) {
+      atomicAdd(&pre[my_e], 1);
+      wcnt[wave][my_e] = 0;
     }
   }
-  __syncthreads();
-  // padding sentinels (wave w fills the padding of experts w, w + NW, ...), the tail
-  // past the last expert, and block owners (the last expert whose start is <= the
-  // block's first slot; empty experts share the start of the next one)
-  for (int e = wave; e < E; e += NW)
-    for (int i = base[e] + cnt[e] + lane; i < base[e] + (cnt[e] + block - 1) / block * block; i += 64) sorted[i] = S;
-  for (int i = total + tid; i < cap; i += kAlignThreads) sorted[i] = S;
+  // positions past the real slots: padding of every expert and the tail [total, cap)
+  // get the sentinel S; the expert of a position (and of a block's first position) is
+  // the last expert whose start is <= it, empty experts sharing the start of the next
+  auto owner_of = [&](int pos) {
+    int lo = 0, hi = E - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (base[mid] <= pos) lo = mid;
+      else hi = mid - 1;
+    }
+    return lo;
+  };
+  for (int i = g * kChunk + tid; i < cap; i += G * kChunk) {
+    if (i >= total) {
+      sorted[i] = S;
+    } else {
+      const int e = owner_of(i);
+      if (i - base[e] >= hist[e]) sorted[i] = S;
+    }
+  }
   const int nblk = cap / block;
-  for (int b = tid; b < nblk; b += kAlignThreads) {
-    int owner = -1;
-    if (b * block < total) {
-      int lo = 0, hi = E - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (base[mid] <= b * block) lo = mid; else hi = mid - 1;
-      }
-      owner = lo;
-    }
-    block_expert[b] = owner;
-  }
-  // C: stable placement.  Each lane reads its expert's running start for the wave
-  // (one LDS read per group), the ballot loop ranks the lanes of each distinct expert
-  // and its leader (lowest lane) advances the running start by the group's count.
-  for_groups([&](int s, int e, bool valid) {
-    const int first = valid ? wrun[wave][e] : 0;
-    unsigned long long todo = __ballot(valid);
-    int rank = 0;
-    while (todo) {
-      const int leader = __builtin_ctzll(todo);
-      const int le = __builtin_amdgcn_readlane(e, leader);
-      const unsigned long long m = __ballot(valid && e == le);
-      if (valid && e == le)
-        rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-      if (lane == leader) atomicAdd(&wrun[wave][le], __popcll(m));
-      todo &= ~m;
-    }
-    if (valid) sorted[first + rank] = s;
-  });
+  for (int b = g * kChunk + tid; b < nblk; b += G * kChunk) block_expert[b] = b * block < total ? owner_of(b * block) : -1;
 }
 
 // ------------------------------------------------------------------------------
@@ -642,6 +649,21 @@ int launch_moe_buf(MoeGemmParams p, int64_t cap, hipStream_t st) {
 }  // namespace
 }  // namespace kore
 
+namespace kore {
+namespace {
+// Sort/align of S slots: the chunked kernel, one workgroup per 256 slots.
+int launch_align(const int32_t* ids, int64_t S, int64_t E, int block, int32_t* offsets, int32_t* sorted,
+                 int32_t* block_expert, int64_t cap, hipStream_t st) {
+  const int64_t chunks = std::max<int64_t>(1, (S + kChunk - 1) / kChunk);
+  const int R = (int)((chunks + 255) / 256);  // sub-chunks per workgroup: at most 256 workgroups
+  const int grid = (int)((chunks + R - 1) / R);
+  hipLaunchKernelGGL(moe_align_chunk_kernel, dim3((unsigned)grid), dim3(kChunk), 0, st, ids, (int)S, (int)E, block, R,
+                     offsets, sorted, block_expert, (int)cap);
+  return check_launch("moe_align_chunk_kernel");
+}
+}  // namespace
+}  // namespace kore
+
 extern "C" int64_t kore_moe_align_capacity(int64_t T, int64_t topk, int64_t E, int64_t block) {
   if (T < 0 || topk <= 0 || E <= 0 || block <= 0) return -1;
   return kore::align_capacity(T * topk, E, block);
@@ -658,9 +680,8 @@ extern "C" int kore_moe_align(const int32_t* topk_ids, int64_t T, int64_t topk, 
   if (cap < align_capacity(T * topk, E, block) || cap % block != 0)
     return set_error(KORE_EINVAL, "moe_align: cap %lld too small or not a multiple of block (need %lld)",
                      (long long)cap, (long long)align_capacity(T * topk, E, block));
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, (hipStream_t)stream, topk_ids,
-                     (int)(T * topk), (int)E, (int)block, offsets, sorted_slots, block_expert, (int)cap);
-  return check_launch("moe_align_kernel");
+  return launch_align(topk_ids, T * topk, E, (int)block, offsets, sorted_slots, block_expert, cap,
+                      (hipStream_t)stream);
 }
 
 extern "C" size_t kore_fused_moe_workspace_bytes(int64_t T, int64_t topk, int64_t E, int64_t D, int64_t I) {
@@ -691,9 +712,7 @@ extern "C" int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, c
   hipStream_t st = (hipStream_t)stream;
   const int BM = moe_block_rows(S, E);
   const int64_t cap = align_capacity(S, E, BM);
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, st, topk_ids, (int)S, (int)E, BM, ws.offsets,
-                     ws.sorted, ws.block_expert, (int)cap);
-  int rc = check_launch("moe_align_kernel");
+  int rc = launch_align(topk_ids, S, E, BM, ws.offsets, ws.sorted, ws.block_expert, cap, st);
   if (rc) return rc;
 
   MoeGemmParams p{};
@@ -850,9 +869,7 @@ extern "C" int kore_moe_grouped_gemm(const void* x, int64_t ldx, const void* w, 
                      kore_moe_grouped_gemm_workspace_bytes(M, E));
   hipStream_t st = (hipStream_t)stream;
   const int64_t cap = align_capacity(M, E, BM);
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, st, expert_ids, (int)M, (int)E, BM,
-                     ws.offsets, ws.sorted, ws.block_expert, (int)cap);
-  int rc = check_launch("moe_align_kernel");
+  int rc = launch_align(expert_ids, M, E, BM, ws.offsets, ws.sorted, ws.block_expert, cap, st);
   if (rc) return rc;
   MoeGemmParams p{};
   p.x = (const uint16_t*)x;
@@ -908,9 +925,7 @@ extern "C" int kore_moe_grouped_gemm_fp8(const void* xq, int64_t ldx, const void
   const GroupedWorkspace w = carve_grouped(workspace, M, E, BM);
   const int64_t cap = align_capacity(M, E, BM);
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, st, expert_ids, (int)M, (int)E, BM, w.offsets,
-                     w.sorted, w.block_expert, (int)cap);
-  int rc = check_launch("moe_align_kernel");
+  int rc = launch_align(expert_ids, M, E, BM, w.offsets, w.sorted, w.block_expert, cap, st);
   if (rc) return rc;
   GroupedA8Args a{};
   a.xq = xq;

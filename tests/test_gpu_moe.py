@@ -15,8 +15,12 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("T,topk,E,block", [(64, 2, 8, 32), (4096, 2, 8, 256), (256, 8, 32, 64),
-                                            (1, 1, 4, 16), (333, 3, 70, 64), (2000, 8, 256, 128)])
+                                            (1, 1, 4, 16), (333, 3, 70, 64), (2000, 8, 256, 128),
+                                            (16384, 8, 128, 64), (2000, 4, 1024, 32), (1000, 1, 3, 1)])
 def test_moe_align_bit_exact(gpu, T, topk, E, block):
+    """One workgroup per 256 slots (two sub-chunks per workgroup at 131072 slots),
+    up to 1024 experts, block 1 (the expert-offsets case): bit-exact against the
+    brute-force oracle, invalid ids dropped."""
     g = torch.Generator().manual_seed(T + E)
     ids = torch.randint(0, E, (T, topk), generator=g, dtype=torch.int32)
     if T > 4:
