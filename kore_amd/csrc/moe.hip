@@ -18,9 +18,11 @@
 //  4. moe_combine_kernel: out[t] = bf16(sum_k Yw[t*topk + k]) in fixed k order over
 //     the slots whose id is in [0, E): no atomics, bit-reproducible.
 // Grids are sized for the worst case (every expert adds < 1 block of padding) and
-// blocks past the real end exit after reading offsets[E].  With few slots per expert
-// (decode) blocks are 32 rows and both GEMMs stream weights on a deep direct-to-LDS
-// ring (moe_decode_kernel), the down projection split in two along K.
+// blocks past the real end exit after reading offsets[E].  Up to 128 slots per expert
+// (decode and small batches) blocks are 32 or 128 rows and both GEMMs stream the expert
+// weights once per block on a direct-to-LDS ring with non-temporal loads
+// (moe_decode_kernel); padding rows of a block are zero-filled by the buffer range
+// check at no memory cost.  Beyond 128 slots per expert: 256-row prefill tiles.
 #include "../../include/kore_amd.h"
 #include "kore_common.hpp"
 #include "tile_engine.hpp"
@@ -197,7 +199,6 @@ struct MoeGemmParams {
   int64_t w_rstride;      // elements between rows of w[e]
   int max_mblocks, ntiles;
   int abm;                // rows per aligned block of the sorted slot list
-  int ksplit;             // K splits (down decode): split k writes Yw + k*S*D
   uint16_t* out;          // plain grouped GEMM: bf16 output rows, scattered by token
   int64_t ldo;
 };
@@ -451,39 +452,58 @@ __global__ void __launch_bounds__(256)
   moe_epilogue<MODE, MI, NI, E::WROWS, E::WCOLS>(acc, lds, p, pos0, n0, wm, wn, wave, lane);
 }
 
-// Decode path (32-row blocks): weight streaming on the skinny ring engine.  Grid =
-// ksplit x ntiles x max_mblocks; a workgroup multiplies one BM-slot block (32 or 64) by BN rows
-// of its expert's weights over K / ksplit, so w1/w2 are streamed once per block with
-// NSLOT-1 stages in flight per CU.  The down projection splits K so its grid (32
-// column tiles per block) covers the CUs; split k writes its own Yw slab, summed in
-// fixed order by the combine.
+// Down projection grid: workgroup b runs on XCD b % 8 (round-robin dispatch), so XCD x
+// takes the blocks mb = x, x + 8, ... with all of their column tiles; each L2 then holds
+// the H rows of an eighth of the blocks instead of every XCD streaming all of H, and the
+// live blocks (the low mb) are spread evenly over the XCDs.  The grid is the block count
+// rounded up to a multiple of 8 times ntiles.
+__device__ __forceinline__ void down_coords(int b, int ntiles, int& mb, int& nt) {
+  const int q = b >> 3;
+  mb = (q / ntiles) * 8 + (b & 7);
+  nt = q % ntiles;
+}
+
+// Weight-streaming path (32- and 128-row blocks) on the skinny ring engine.  Grid =
+// ntiles x max_mblocks; a workgroup multiplies one BM-slot block by BN rows of its
+// expert's weights over the whole K, so w1/w2 are streamed once per block, NSLOT-1
+// stages in flight per workgroup, with the non-temporal load policy (each weight row is
+// read by exactly one workgroup).
 template <int MODE, int BN, int NSLOT, int BM>
 __global__ void __launch_bounds__(256)
     moe_decode_kernel(const MoeGemmParams p) {
   constexpr int AP = (MODE == MOE_DOWN) ? 2 : 1;
-  using E = SkinnyRingEngine<BF16, BN, AP, NSLOT, BM>;
+  using E = SkinnyRingEngine<BF16, BN, AP, NSLOT, BM, kCpolNT>;  // each weight row is read by one workgroup
   constexpr int MI = E::MI, NI = E::NI;
   __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-  const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-  const int mb = bid % p.max_mblocks, rest = bid / p.max_mblocks;
-  const int nt = rest % p.ntiles, ks = rest / p.ntiles;
+  int mb, nt;
+  if constexpr (MODE == MOE_DOWN) {
+    down_coords((int)blockIdx.x, p.ntiles, mb, nt);
+    if (mb >= p.max_mblocks) return;
+  } else {
+    const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    mb = bid % p.max_mblocks;
+    nt = bid / p.max_mblocks;
+  }
   const int total = p.offsets[p.E];
   if (mb * E::BM >= total) return;  // uniform: the whole workgroup leaves
   const int e = p.block_expert[(mb * E::BM) / p.abm];
   const int pos0 = mb * E::BM;
 
   E eng;
-  // A: gathered token rows (gate_up, plain) or the H planes of this block (down)
+  // A: gathered token rows (gate_up, plain) or the H planes of this block (down).
+  // A padding row (sorted slot >= S) gets the resource's byte size as its offset: the
+  // buffer range check turns its loads into zeros with no memory traffic, and its
+  // output row is never used (rows of an MFMA product are independent).
   if constexpr (MODE != MOE_DOWN) {
-    eng.ra = make_rsrc(p.x, (uint32_t)((int64_t)p.T * p.ldx * 2));
+    const uint32_t bytes = (uint32_t)((int64_t)p.T * p.ldx * 2);
+    eng.ra = make_rsrc(p.x, bytes);
 #pragma unroll
     for (int j = 0; j < E::AJ; ++j) {
       const int ar = E::a_row(wave, lane, j);
       const int sl = p.sorted[pos0 + ar];
-      const int64_t row = (sl < p.S) ? sl / p.topk : 0;  // padding rows read token 0; never stored
-      eng.a_voff[j] = (uint32_t)((row * p.ldx + 8 * E::chunk(ar, lane)) * 2);
+      eng.a_voff[j] = sl < p.S ? (uint32_t)(((int64_t)(sl / p.topk) * p.ldx + 8 * E::chunk(ar, lane)) * 2) : bytes;
     }
   } else {
     const uint32_t tile_bytes = (uint32_t)((int64_t)E::BM * p.ldx * 2);
@@ -492,7 +512,8 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int j = 0; j < E::AJ; ++j) {
       const int ar = E::a_row(wave, lane, j);
-      eng.a_voff[j] = (uint32_t)(((int64_t)ar * p.ldx + 8 * E::chunk(ar, lane)) * 2);
+      eng.a_voff[j] = p.sorted[pos0 + ar] < p.S ? (uint32_t)(((int64_t)ar * p.ldx + 8 * E::chunk(ar, lane)) * 2)
+                                                : tile_bytes;
     }
   }
   // B: interleaved gate/up rows of w1[e] (gate_up) or consecutive rows of w[e]
@@ -521,13 +542,10 @@ __global__ void __launch_bounds__(256)
       eng.b_voff[j] = (uint32_t)(((int64_t)r * p.w_rstride + 8 * E::chunk(r, lane)) * 2);
     }
   }
-  const int kper = p.K / p.ksplit;
   f32x16_t acc[MI][NI];
   E::zero(acc);
-  eng.mainloop(lds, ks * kper, (ks + 1) * kper, acc);
-  MoeGemmParams q = p;
-  q.yw = p.yw + (int64_t)ks * p.S * p.Nout;
-  moe_epilogue<MODE, MI, NI, E::BM, E::WCOLS>(acc, lds, q, pos0, n0, 0, wave, wave, lane);
+  eng.mainloop(lds, 0, p.K, acc);
+  moe_epilogue<MODE, MI, NI, E::BM, E::WCOLS>(acc, lds, p, pos0, n0, 0, wave, wave, lane);
 }
 
 // ------------------------------------------------------------------------------
@@ -535,28 +553,24 @@ __global__ void __launch_bounds__(256)
 // ------------------------------------------------------------------------------
 __global__ void __launch_bounds__(256)
     moe_combine_kernel(const float* __restrict__ yw, const int32_t* __restrict__ ids, uint16_t* __restrict__ out,
-                       int T, int D, int topk, int E, int ksplit) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // one thread per 8 outputs
-  const int per_row = D / 8;
+                       int T, int D, int topk, int E) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // one thread per 4 outputs
+  const int per_row = D / 4;
   if (idx >= (int64_t)T * per_row) return;
-  const int t = (int)(idx / per_row), d0 = (int)(idx % per_row) * 8;
-  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const int t = (int)(idx / per_row), d0 = (int)(idx % per_row) * 4;
+  f32x4_t s = {0.f, 0.f, 0.f, 0.f};
+  // every row is loaded (a slot with an invalid id has an unwritten row) and selected
+  // away, so the loads of all k are independent and go out together
+#pragma unroll 8
   for (int k = 0; k < topk; ++k) {
     const int e = ids[t * topk + k];
-    if (e < 0 || e >= E) continue;
-    for (int sp = 0; sp < ksplit; ++sp) {
-      const float* src = yw + ((int64_t)sp * T * topk + (int64_t)t * topk + k) * D + d0;
-      const f32x4_t a = *(const f32x4_t*)src, b = *(const f32x4_t*)(src + 4);
+    const bool ok = e >= 0 && e < E;
+    const f32x4_t v = *(const f32x4_t*)(yw + ((int64_t)t * topk + k) * D + d0);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        s[q] += a[q];
-        s[4 + q] += b[q];
-      }
-    }
+    for (int q = 0; q < 4; ++q) s[q] += ok ? v[q] : 0.0f;
   }
   using Op = MfmaOp<BF16>;
-  *(u32x4_t*)(out + (int64_t)t * D + d0) =
-      u32x4_t{Op::pack2(s[0], s[1]), Op::pack2(s[2], s[3]), Op::pack2(s[4], s[5]), Op::pack2(s[6], s[7])};
+  *(u32x2_t*)(out + (int64_t)t * D + d0) = u32x2_t{Op::pack2(s[0], s[1]), Op::pack2(s[2], s[3])};
 }
 
 // ------------------------------------------------------------------------------
@@ -569,13 +583,11 @@ inline int64_t align_capacity(int64_t S, int64_t E, int64_t block) {
   return align_up(S + E * (block - 1), block);
 }
 
-// Block size of the grouped GEMMs: skinny blocks when experts see few rows.
-// Up to 32 rows per expert on average: 32-row blocks; up to 128: 64-row blocks (each
-// expert's weights streamed once or twice rather than two to four times); beyond: 256.
-inline int moe_block_rows(int64_t S, int64_t E) { return S <= 32 * E ? 32 : S <= 128 * E ? 64 : 256; }
-
-// K splits of the down projection: 2 on the decode path (32-row blocks).
-inline int moe_down_ksplit(int64_t S, int64_t E) { return moe_block_rows(S, E) <= 64 ? 2 : 1; }
+// Block size of the fused MoE GEMMs: skinny blocks when experts see few rows.
+// Up to 16 slots per expert on average: 32-row blocks; up to 128: 128-row blocks, so
+// nearly every expert's weights are streamed once (padding rows cost MFMA cycles, which
+// are idle on these weight-bound shapes, but no memory traffic); beyond: 256.
+inline int moe_block_rows(int64_t S, int64_t E) { return S <= 16 * E ? 32 : S <= 128 * E ? 128 : 256; }
 
 struct MoeWorkspace {
   int32_t* offsets;
@@ -603,7 +615,7 @@ inline MoeWorkspace carve(void* base, int64_t T, int64_t topk, int64_t E, int64_
   const size_t o_blk = take(sizeof(int32_t) * (cap / BM));
   const size_t o_h = take(sizeof(uint16_t) * cap * I);
   const size_t o_hlo = take(sizeof(uint16_t) * cap * I);
-  const size_t o_yw = take(sizeof(float) * S * D * moe_down_ksplit(S, E));
+  const size_t o_yw = take(sizeof(float) * S * D);
   char* b = (char*)base;
   w.offsets = (int32_t*)(b + o_off);
   w.sorted = (int32_t*)(b + o_sorted);
@@ -630,7 +642,8 @@ template <int MODE, int BN, int NSLOT, int BM = 32>
 int launch_moe_decode(MoeGemmParams p, int64_t cap, hipStream_t st) {
   p.ntiles = (MODE == MOE_GATEUP) ? p.Nout / (BN / 2) : p.Nout / BN;
   p.max_mblocks = (int)(cap / BM);
-  const int64_t blocks = (int64_t)p.max_mblocks * p.ntiles * p.ksplit;
+  const int64_t mblocks = MODE == MOE_DOWN ? align_up(p.max_mblocks, 8) : p.max_mblocks;  // down_coords
+  const int64_t blocks = mblocks * p.ntiles;
   if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "fused_moe: grid too large");
   hipLaunchKernelGGL((moe_decode_kernel<MODE, BN, NSLOT, BM>), dim3((unsigned)blocks), dim3(256), 0, st, p);
   return check_launch(MODE == MOE_GATEUP ? "moe_gateup_decode_kernel" : "moe_down_decode_kernel");
@@ -724,7 +737,6 @@ extern "C" int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, c
   p.h_lo = ws.h_lo;
   p.yw = ws.yw;
   p.abm = BM;
-  p.ksplit = 1;
   p.E = (int)E;
   p.T = (int)T;
   p.S = (int)S;
@@ -737,12 +749,14 @@ extern "C" int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, c
   p.Nout = (int)I;
   p.w_estride = 2 * I * D;
   p.w_rstride = D;
-  // buffer-load engine needs operand byte ranges below 4 GiB and K % 64 == 0
-  const bool buf_ok = T * ldh * 2 < (1ll << 32) && 2 * I * D * 2 < (1ll << 32) && D % 64 == 0 && I % 64 == 0;
-  // 64-row blocks without the buffer engine run 32-row tiles (two per aligned block)
+  // buffer-load engine needs operand byte ranges (plus a K step past a padding row's
+  // offset) below 4 GiB and K % 64 == 0
+  const bool buf_ok =
+      T * ldh * 2 + 4 * D < (1ll << 32) && 2 * I * D * 2 < (1ll << 32) && D % 64 == 0 && I % 64 == 0;
+  // 128-row blocks without the buffer engine run 32-row tiles (four per aligned block)
   rc = (BM == 32 && buf_ok) ? launch_moe_decode<MOE_GATEUP, 128, 7>(p, cap, st)
-       : (BM == 64 && buf_ok) ? launch_moe_decode<MOE_GATEUP, 128, 6, 64>(p, cap, st)
-       : (BM <= 64) ? launch_moe_gemm<MOE_GATEUP, 32, 256, 1, 4>(p, cap, st)
+       : (BM == 128 && buf_ok) ? launch_moe_decode<MOE_GATEUP, 128, 2, 128>(p, cap, st)
+       : (BM <= 128) ? launch_moe_gemm<MOE_GATEUP, 32, 256, 1, 4>(p, cap, st)
        : buf_ok   ? launch_moe_buf<MOE_GATEUP, 256, 256>(p, cap, st)
                   : launch_moe_gemm<MOE_GATEUP, 256, 256, 2, 2>(p, cap, st);
   if (rc) return rc;
@@ -756,14 +770,11 @@ extern "C" int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, c
   p.w_rstride = I;
   // two A planes double the A tile: prefill runs 128-row tiles (halves of a 256-row
   // aligned block) to stay inside the 160 KiB LDS budget.
-  const int ksplit = moe_down_ksplit(S, E);
   if (BM == 32 && buf_ok) {
-    p.ksplit = ksplit;  // I % 128 == 0, so every split is a multiple of 64
     rc = launch_moe_decode<MOE_DOWN, 128, 6>(p, cap, st);
-  } else if (BM == 64 && buf_ok) {
-    p.ksplit = ksplit;
-    rc = launch_moe_decode<MOE_DOWN, 128, 4, 64>(p, cap, st);
-  } else if (BM <= 64) {
+  } else if (BM == 128 && buf_ok) {
+    rc = launch_moe_decode<MOE_DOWN, 128, 3, 128>(p, cap, st);
+  } else if (BM <= 128) {
     rc = launch_moe_gemm<MOE_DOWN, 32, 128, 1, 4>(p, cap, st);
   } else if (buf_ok && D % 256 == 0) {
     rc = launch_moe_buf<MOE_DOWN, 128, 256>(p, cap, st);
@@ -773,9 +784,9 @@ extern "C" int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, c
     rc = launch_moe_gemm<MOE_DOWN, 128, 128, 2, 2>(p, cap, st);
   }
   if (rc) return rc;
-  const int64_t threads = T * (D / 8);
+  const int64_t threads = T * (D / 4);
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, ws.yw, topk_ids,
-                     (uint16_t*)out, (int)T, (int)D, (int)topk, (int)E, p.ksplit);
+                     (uint16_t*)out, (int)T, (int)D, (int)topk, (int)E);
   return check_launch("moe_combine_kernel");
 }
 
@@ -887,10 +898,9 @@ extern "C" int kore_moe_grouped_gemm(const void* x, int64_t ldx, const void* w, 
   p.w_estride = N * K;
   p.w_rstride = K;
   p.abm = BM;
-  p.ksplit = 1;
   p.out = (uint16_t*)out;
   p.ldo = ldo;
-  const bool buf_ok = K % 64 == 0 && M * ldx * 2 < (1ll << 32) && N * K * 2 < (1ll << 32);
+  const bool buf_ok = K % 64 == 0 && M * ldx * 2 + 4 * K < (1ll << 32) && N * K * 2 < (1ll << 32);
   if (BM == 32) {
     rc = buf_ok ? launch_moe_decode<MOE_PLAIN, 128, 7>(p, cap, st) : launch_moe_gemm<MOE_PLAIN, 32, 128, 1, 4>(p, cap, st);
   } else if (buf_ok) {

@@ -66,15 +66,18 @@ def test_fused_moe_prefill_tiles(gpu, T, E, topk, D, I):
     verdict(out, ref, "north_star", "bf16", f"prefill tiles T{T} (1e-2)")
 
 
-@pytest.mark.parametrize("T,E,topk,D,I", [(300, 4, 1, 256, 384), (500, 8, 2, 512, 256), (200, 4, 2, 384, 640)])
-def test_fused_moe_64row_blocks(gpu, T, E, topk, D, I):
-    """Slot counts of 33-128 per expert select 64-row blocks on the skinny ring engine
-    (each expert's weights streamed once per 64 slots); ragged counts leave padding rows."""
+@pytest.mark.parametrize("T,E,topk,D,I", [(300, 4, 1, 256, 384), (500, 8, 2, 512, 256), (200, 4, 2, 384, 640),
+                                          (1024, 32, 2, 768, 512)])
+def test_fused_moe_128row_blocks(gpu, T, E, topk, D, I):
+    """Slot counts of 17-128 per expert select 128-row blocks on the skinny ring engine
+    (each expert's weights streamed once per block, two workgroups per CU for gate_up, the
+    XCD-grouped grid for down).  Ragged counts leave padding rows, which the buffer range
+    check zero-fills and the epilogues never store; K = 256 is the shortest ring."""
     hidden, w1, w2, tw, ti = W.moe_inputs(T, E, topk, D, I, seed=T + 1, wscale=0.05)
     out = kore_amd.fused_moe(*[t.to(gpu) for t in (hidden, w1, w2, tw, ti)])
     ref = moe_ref(hidden, w1, w2, tw, ti)
-    verdict(out, ref, "fused_moe", "bf16", f"64-row blocks T{T} E{E} k{topk} D{D} I{I}")
-    verdict(out, ref, "north_star", "bf16", f"64-row blocks T{T} (1e-2)")
+    verdict(out, ref, "fused_moe", "bf16", f"128-row blocks T{T} E{E} k{topk} D{D} I{I}")
+    verdict(out, ref, "north_star", "bf16", f"128-row blocks T{T} (1e-2)")
 
 
 def test_fused_moe_decode_config(gpu):
