@@ -19,16 +19,20 @@ gaps, which for microsecond kernels (fp8 M=16) is otherwise dominated by the Pyt
 call.  Per-configuration ``tflops``/``tb_per_s``/``frac_of_bound`` use the lower of
 ``kernel_ms`` and ``graph_ms`` (graph replay adds a few microseconds of per-node
 overhead on long kernels); the headline ``value`` is wall time and its ``roofline``
-uses ``kernel_ms``.  ``cold_ms`` follows the reference drivers' protocol: median of events
-around one step preceded by a 512 MiB cache flush (``kore/tasks/_genops.py:787-813`` flushes
-256 MiB; MI355X has 256 MiB of Infinity Cache).  Roofline fractions use the
+uses ``kernel_ms``.  ``cold_ms`` follows the reference drivers' protocol
+(``kore/tasks/_genops.py:787-813``): median of events around one step preceded by a
+256 MiB ``zero_()`` flush, which leaves the 256 MiB Infinity Cache full of dirty lines;
+``cold_frac_of_bound`` is the roofline fraction at that time.  Roofline fractions use the
 algorithmic FLOPs/bytes of ``kore_amd.roofline`` and MI355X peaks (bf16 2.5 PF, fp8
 5.0 PF, HBM 8 TB/s).  ``roofline.traffic`` is the HBM traffic per launch of the
 headline kernel recorded by rocprofv3 FETCH_SIZE/WRITE_SIZE runs
 (``profiles/hbm_traffic.md``, written by ``python -m kore_amd.profiling traffic``).
 
-``cpu_baseline`` times the CPU oracle (the restated torch-fp32 reference) on a row
-sample of the headline workload, on the host's cores; it is a reported baseline.
+``cpu_baseline`` (per configuration, and for the headline at the top level) times the
+CPU oracle -- the restated torch-fp32 reference, ``oracle/`` -- on a bounded sample of
+the same seeded inputs (rows, batches or tokens, copied from the device), with
+``torch.set_num_threads`` at the host's thread budget, and names the CPU model.  It is
+a reported baseline, never a gate.
 """
 
 from __future__ import annotations
@@ -43,6 +47,8 @@ import time
 import torch
 
 HEADLINE = "fp8_blockscale_2048x7168x4096"
+# the kernel the headline dispatches to on MI355X (256 CUs): 256x224 tiles, one per CU
+HEADLINE_KERNEL = "gemm_fp8_wide_kernel"
 
 
 def _parse():
@@ -51,7 +57,7 @@ def _parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--only", default=None, help="comma-separated config names to run")
-    p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baselines")
     p.add_argument("--cold-iters", type=int, default=10)
     p.add_argument("--no-graph", action="store_true", help="skip the graph-replay timing")
     return p.parse_args()
@@ -103,7 +109,7 @@ class Timer:
         cold = []
         if self.cold_iters:
             if self._flush is None:
-                self._flush = torch.empty(512 * 1024 * 1024, dtype=torch.int8, device="cuda")
+                self._flush = torch.empty(256 * 1024 * 1024, dtype=torch.int8, device="cuda")
             for _ in range(self.cold_iters):
                 self._flush.zero_()
                 s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -124,6 +130,7 @@ def _entry(name, op, dims, dtype, wall, kern, cold, graph):
     # time (eager includes host launch gaps for microsecond kernels; graph replay adds
     # per-node overhead that shows on long kernels)
     t = (min(kern, graph) if graph is not None else kern) * 1e-3
+    tc = cold * 1e-3 if cold is not None else None
     return {
         "name": name, "op": op, "dims": dims, "dtype": dtype,
         "ms_per_step": round(wall, 5), "kernel_ms": round(kern, 5),
@@ -133,34 +140,115 @@ def _entry(name, op, dims, dtype, wall, kern, cold, graph):
         "tb_per_s": round(rf.bytes / t / 1e12, 3),
         "bound": rf.bound,
         "frac_of_bound": round(rf.t_min_s / t, 4),
+        "cold_frac_of_bound": round(rf.t_min_s / tc, 4) if tc else None,
         "frac_mfma_peak": round(rf.flops / t / rf.peak_flops, 4),
         "frac_hbm_peak": round(rf.bytes / t / rf.peak_bw, 4),
     }
 
 
-def cpu_baseline(seconds_budget: float = 20.0):
-    """Time the CPU oracle (restated torch-fp32 reference) on a row sample of the
-    headline fp8 workload: rows [0, m) of X against the full W [7168, 4096]."""
-    from kore_amd import workloads as W
-    from oracle.quant import matmul_blockscale_ref
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
 
-    threads = os.cpu_count() or 1
+    return platform.processor() or platform.machine()
+
+
+def _cpu_threads() -> int:
+    # the host's thread budget (OMP_NUM_THREADS where the job sets it, else every core)
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return int(env) if env.isdigit() and int(env) > 0 else (os.cpu_count() or 1)
+
+
+def _cpu_sample(op, dims, dtype, args, target_flops=4e10):
+    """(run, work, unit, what): the oracle on a bounded sample of the same inputs."""
+    import oracle.gemm as og
+    import oracle.moe as om
+    import oracle.quant as oq
+
+    cpu = lambda t: t.cpu() if isinstance(t, torch.Tensor) else t  # noqa: E731
+    if op == "gemm":
+        a, b, bias, act = args
+        M, N, K = dims["M"], dims["N"], dims["K"]
+        m = max(1, min(M, int(target_flops / (2.0 * N * K))))
+        a_s, b_s, bias_s = cpu(a[:m]), cpu(b), cpu(bias)
+        return (lambda: og.gemm_fusion_ref(a_s, b_s, bias_s, act)), 2.0 * m * N * K, "TFLOP/s", \
+            f"oracle.gemm.gemm_fusion_ref on rows 0..{m} of A"
+    if op == "batched_gemm":
+        a, b = args
+        per = 2.0 * dims["M"] * dims["N"] * dims["K"]
+        nb = max(1, min(dims["B"], int(target_flops / per)))
+        a_s, b_s = cpu(a[:nb]), cpu(b[:nb])
+        return (lambda: og.batched_gemm_ref(a_s, b_s)), per * nb, "TFLOP/s", \
+            f"oracle.gemm.batched_gemm_ref on batches 0..{nb}"
+    if op == "gemm_backward":
+        x, w, dy = args
+        M, N, K = dims["M"], dims["N"], dims["K"]
+        m = max(1, min(M, int(target_flops / (4.0 * N * K))))
+        x_s, w_s, dy_s = cpu(x[:m]), cpu(w), cpu(dy[:m])
+        return (lambda: og.gemm_backward_ref(x_s, w_s, dy_s)), 4.0 * m * N * K, "TFLOP/s", \
+            f"oracle.gemm.gemm_backward_ref on rows 0..{m} of X and dY"
+    if op in ("gemm_fp8", "gemm_a8w8"):
+        xq, wq, xs, ws = args
+        M, N, K = dims["M"], dims["N"], dims["K"]
+        m = max(1, min(M, int(target_flops / (2.0 * N * K))))
+        xq_s, wq_s, xs_s, ws_s = cpu(xq[:m]), cpu(wq), cpu(xs[:m]), cpu(ws)
+        fn = oq.matmul_blockscale_ref if op == "gemm_fp8" else oq.matmul_a8w8_ref
+        return (lambda: fn(xq_s, wq_s, xs_s, ws_s)), 2.0 * m * N * K, "TFLOP/s", \
+            f"oracle.quant.{fn.__name__} on rows 0..{m} of X"
+    if op == "fused_moe":
+        h, w1, w2, tw, ti = args
+        t = min(dims["M"], 16)
+        h_s, w1_s, w2_s, tw_s, ti_s = cpu(h[:t]), cpu(w1), cpu(w2), cpu(tw[:t]), cpu(ti[:t])
+        work = 6.0 * t * dims["topk"] * dims["D"] * dims["I"]
+        return (lambda: om.moe_ref(h_s, w1_s, w2_s, tw_s, ti_s)), work, "TFLOP/s", \
+            f"oracle.moe.moe_ref on tokens 0..{t} (all experts' weights upcast per call, as the oracle does)"
+    if op == "moe_grouped_gemm":
+        target_flops /= 4  # the oracle loops over the experts, upcasting each one's weights
+        if dtype == "fp8":
+            xq, wq, xs, ws, ids = args
+            m = max(1, min(dims["M"], int(target_flops / (2.0 * dims["N"] * dims["K"]))))
+            sl = (cpu(xq[:m]), cpu(wq), cpu(xs[:m]), cpu(ws), cpu(ids[:m]))
+            return (lambda: om.grouped_gemm_fp8_ref(*sl)), 2.0 * m * dims["N"] * dims["K"], "TFLOP/s", \
+                f"oracle.moe.grouped_gemm_fp8_ref on tokens 0..{m}"
+        x, w, ids = args
+        m = max(1, min(dims["M"], int(target_flops / (2.0 * dims["N"] * dims["K"]))))
+        sl = (cpu(x[:m]), cpu(w), cpu(ids[:m]))
+        return (lambda: om.grouped_gemm_ref(*sl)), 2.0 * m * dims["N"] * dims["K"], "TFLOP/s", \
+            f"oracle.moe.grouped_gemm_ref on tokens 0..{m}"
+    if op == "moe_permute":
+        h, sidx = args
+        h_s, sidx_s = cpu(h), cpu(sidx)
+        return (lambda: om.permute_ref(h_s, sidx_s)), 2.0 * h.numel() * h.element_size(), "GB/s", \
+            "oracle.moe.permute_ref on the whole input"
+    return None
+
+
+def cpu_baseline(op, dims, dtype, args, budget_s: float = 1.5):
+    """Median of up to 3 oracle runs on the sample (after one untimed run), within a
+    per-configuration time budget."""
+    sample = _cpu_sample(op, dims, dtype, args)
+    if sample is None:
+        return None
+    run, work, unit, what = sample
+    threads = _cpu_threads()
     torch.set_num_threads(threads)
-    m = 128
-    xq, wq, xs, ws = W.fp8_inputs(2048, 7168, 4096, seed=0, device="cpu")
-    xq, xs = xq[:m].contiguous(), xs[:m].contiguous()
-    matmul_blockscale_ref(xq, wq, xs, ws)  # warm-up
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 3 and time.perf_counter() - t_start < seconds_budget:
+    run()
+    times, t_start = [], time.perf_counter()
+    while len(times) < 3 and (not times or time.perf_counter() - t_start < budget_s):
         t0 = time.perf_counter()
-        matmul_blockscale_ref(xq, wq, xs, ws)
+        run()
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
-    return {"value": round(2.0 * m * 7168 * 4096 / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
-            "sample": f"oracle.quant.matmul_blockscale_ref on rows 0..{m} of the 2048x7168x4096 workload "
-                      f"(fp32 dequant + torch CPU matmul on {threads} threads), median of {len(times)} runs, "
+    scale = 1e12 if unit == "TFLOP/s" else 1e9
+    return {"value": round(work / t / scale, 4), "unit": unit, "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": f"{what}, fp32 torch on {threads} threads, median of {len(times)} runs, "
                       f"{t * 1e3:.1f} ms per run"}
 
 
@@ -187,14 +275,17 @@ def main():
         names = [n for n in names if n in args.only.split(",")]
     results = {}
     for name in names:
-        fn, op, dims, dtype = work[name](dev)
-        wall, kern, cold, graph = timer.run(fn)
-        results[name] = _entry(name, op, dims, dtype, wall, kern, cold, graph)
+        w = work[name](dev)
+        wall, kern, cold, graph = timer.run(w.fn)
+        results[name] = _entry(name, w.op, w.dims, w.dtype, wall, kern, cold, graph)
         r = results[name]
         gtxt = f"graph {graph * 1e3:.1f} us, " if graph is not None else ""
         print(f"# {name}: {r['tflops']} TFLOP/s, {r['tb_per_s']} TB/s, kernel {kern * 1e3:.1f} us, "
-              f"{gtxt}wall {wall * 1e3:.1f} us, frac_of_bound {r['frac_of_bound']}", file=sys.stderr, flush=True)
-        del fn
+              f"{gtxt}wall {wall * 1e3:.1f} us, " + (f"cold {cold * 1e3:.1f} us, " if cold is not None else "") +
+              f"frac_of_bound {r['frac_of_bound']} (cold {r['cold_frac_of_bound']})", file=sys.stderr, flush=True)
+        if not args.no_cpu:
+            r["cpu_baseline"] = cpu_baseline(w.op, w.dims, w.dtype, w.args)
+        del w
         torch.cuda.empty_cache()
     head = results.get(HEADLINE) or next(iter(results.values()))
     flops = 2.0 * head["dims"]["M"] * head["dims"]["N"] * head["dims"]["K"] if "K" in head["dims"] else None
@@ -224,16 +315,17 @@ def main():
         "frac_mfma_peak": head["frac_mfma_peak"],
         "roofline": {"bound": head["bound"], "achieved": achieved, "peak": peak, "unit": unit,
                      "frac": round(achieved / peak, 4), "traffic": read_traffic(head["name"]),
-                     "kernel": "gemm_fp8_pipe_kernel" if head["dtype"] == "fp8" else None,
-                     "kernel_ms": head["kernel_ms"]},
+                     "kernel": HEADLINE_KERNEL if head["name"] == HEADLINE else None,
+                     "kernel_ms": head["kernel_ms"], "cold_ms": head["cold_ms"],
+                     "cold_frac": head["cold_frac_of_bound"]},
         "configs": results,
     }
     if "bf16_gemm_4096" in results:
         r = results["bf16_gemm_4096"]
         line["bf16_gemm_4096"] = {"tflops": r["tflops"], "frac_mfma_peak": r["frac_mfma_peak"],
                                   "kernel_ms": r["kernel_ms"], "ms_per_step": r["ms_per_step"]}
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline()
+    if head.get("cpu_baseline"):
+        line["cpu_baseline"] = head["cpu_baseline"]
     print(json.dumps(line))
     return 0
 

@@ -249,10 +249,11 @@ struct F8Cfg {
   static_assert(NW * WROWS * 64 * 2 <= LDS, "epilogue staging fits");
 };
 
+template <int CPOL = kCpolDefault>
 __device__ __forceinline__ void buf_lds(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint8_t* lds_dst,
                                         int size) {
-  if (size == 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_dst, 16, (int)voff, (int)soff, 0, 0);
-  else __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_dst, 4, (int)voff, (int)soff, 0, 0);
+  if (size == 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_dst, 16, (int)voff, (int)soff, 0, CPOL);
+  else __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_dst, 4, (int)voff, (int)soff, 0, CPOL);
 }
 
 __device__ __forceinline__ int f8_key(int r) { return (r ^ (r >> 3)) & 7; }
@@ -973,7 +974,7 @@ __global__ void __launch_bounds__(C::NW_ * 64)
 #pragma unroll
     for (int q = 0; q < XQ; ++q) buf_lds(rx, xoff[q], ko, st + q * 1024, 16);
 #pragma unroll
-    for (int q = 0; q < WQ; ++q) buf_lds(rw, woff[q], ko, st + MT * 128 + q * 1024, 16);
+    for (int q = 0; q < WQ; ++q) buf_lds<kCpolNT>(rw, woff[q], ko, st + MT * 128 + q * 1024, 16);  // W: read once
     if constexpr (!ROW) {
       const uint32_t kb = (uint32_t)(wave + NW * j);
 #pragma unroll

@@ -3,7 +3,7 @@
 Run under the profiler (the program itself follows ``--``)::
 
     rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o run -- \\
-        python3 -m kore_amd.profiling run <workload> [--iters N]
+        python3 -m kore_amd.profiling run <workload> [--iters K]   # prints "W warm-up + K timed calls"
     rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir> -o run -- \\
         python3 -m kore_amd.profiling run <workload>
     rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir> -o run -- \\
@@ -12,7 +12,7 @@ Run under the profiler (the program itself follows ``--``)::
 then, anywhere (no GPU needed), turn the CSV output into the text summaries kept
 under ``profiles/``::
 
-    python3 -m kore_amd.profiling stats <dir> --out profiles/<name>.md --cmd "<command>"
+    python3 -m kore_amd.profiling stats <dir> --warmup-calls W --iters K --out profiles/<name>.md --cmd "<command>"
     python3 -m kore_amd.profiling traffic --workload <w> --kernel <substr> \\
         --fetch <dir> --write <dir> --copy-fetch <dir> --copy-write <dir> --copy-mib 256 \\
         --out profiles/hbm_traffic.md --cmd "<commands>"
@@ -39,7 +39,13 @@ TRAFFIC_FILE = os.path.join(PROFILES, "hbm_traffic.md")
 # --------------------------------------------------------------------------- #
 # GPU side: the programs rocprofv3 runs
 # --------------------------------------------------------------------------- #
-def _run(workload: str, iters: int, warmup: int) -> None:
+def _run(workload: str, iters: int, warmup: int, min_warm_s: float = 0.5) -> None:
+    """``warmup`` calls, and at least ``min_warm_s`` of them (the GPU clock ramps up
+    over the first few hundred microseconds of load, as in ``bench.py``), then
+    ``iters`` calls.  The printed counts let ``stats --warmup-calls W --iters K`` keep
+    only the dispatches of the last K calls."""
+    import time
+
     import torch
 
     from kore_amd import _lib
@@ -49,14 +55,18 @@ def _run(workload: str, iters: int, warmup: int) -> None:
     wl = bench_workloads()
     if workload not in wl:
         raise SystemExit(f"unknown workload {workload!r}; choose from {', '.join(wl)}")
-    fn, _, _, _ = wl[workload](torch.device("cuda:0"))
-    for _ in range(warmup):
+    fn = wl[workload](torch.device("cuda:0")).fn
+    t0, n = time.perf_counter(), 0
+    while n < warmup or time.perf_counter() - t0 < min_warm_s:
         fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     for _ in range(iters):
         fn()
     torch.cuda.synchronize()
-    print(f"profiling.run {workload}: {warmup} warm-up + {iters} timed calls done", flush=True)
+    print(f"profiling.run {workload}: {n} warm-up + {iters} timed calls done", flush=True)
 
 
 def _copy(mib: int, iters: int) -> None:
@@ -102,6 +112,66 @@ def kernel_stats(directory: str) -> list[dict]:
         return list(csv.DictReader(f))
 
 
+def timed_dispatches(directory: str, warmup_calls: int | None = None, iters: int | None = None):
+    """``(name, duration_ns)`` of the traced dispatches in start order, restricted to the
+    timed calls: with ``W`` warm-up and ``K`` timed calls, a kore kernel dispatched
+    ``n`` times (n a multiple of W + K) keeps its last ``n K / (W + K)`` dispatches, and
+    the window opens at the earliest start among those, so every other dispatch inside
+    it (workspace fills, copies) is kept too."""
+    path = _one(os.path.join(directory, "**", "*kernel_trace.csv"))
+    with open(path) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    recs = [(r["Kernel_Name"], int(r["Start_Timestamp"]), int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+            for r in rows]
+    if not warmup_calls or not iters:
+        return [(n, d) for n, _, d in recs]
+    total = warmup_calls + iters
+    starts: dict[str, list[int]] = {}
+    for n, t, _ in recs:
+        if "kore" in n:
+            starts.setdefault(n, []).append(t)
+    opens = []
+    for n, ts in starts.items():
+        if len(ts) % total:
+            raise SystemExit(f"{_short(n)}: {len(ts)} dispatches is not a multiple of {total} calls")
+        opens.append(ts[len(ts) - len(ts) // total * iters])
+    if not opens:
+        raise SystemExit(f"no kore kernels in {path}")
+    t_open = min(opens)
+    return [(n, d) for n, t, d in recs if t >= t_open]
+
+
+def write_stats(directory: str, out: str, cmd: str, title: str, warmup_calls: int | None = None,
+                iters: int | None = None) -> None:
+    recs = timed_dispatches(directory, warmup_calls, iters)
+    per: dict[str, list[int]] = {}
+    for n, d in recs:
+        per.setdefault(n, []).append(d)
+    total_ns = sum(d for _, d in recs)
+    scope = (f"Dispatches of the last {iters} of {warmup_calls + iters} calls ({warmup_calls} warm-up calls, at "
+             "least 0.5 s of them, so the clock has ramped)." if warmup_calls and iters else "All traced dispatches.")
+    lines = [f"# {title}", "", "Command (from the repository root, on one MI355X):", "", "```", cmd, "```", "",
+             scope, "",
+             "| kernel | calls | average (us) | median (us) | min (us) | max (us) | share |",
+             "|---|---|---|---|---|---|---|"]
+    other_calls, other_ns = 0, 0
+    for n, ds in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        if "kore" not in n:  # torch kernels: input generation, workspace fills, copies
+            other_calls += len(ds)
+            other_ns += sum(ds)
+            continue
+        lines.append(f"| `{_short(n)}` | {len(ds)} | {statistics.mean(ds) / 1e3:.1f} | "
+                     f"{statistics.median(ds) / 1e3:.1f} | {min(ds) / 1e3:.1f} | {max(ds) / 1e3:.1f} | "
+                     f"{100.0 * sum(ds) / total_ns:.1f}% |")
+    if other_calls:
+        lines.append(f"| other (torch kernels: fills, copies) | {other_calls} | {other_ns / other_calls / 1e3:.1f} | "
+                     f"| | | {100.0 * other_ns / total_ns:.1f}% |")
+    os.makedirs(os.path.dirname(os.path.abspath(out)), exist_ok=True)
+    with open(out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print(f"wrote {out}")
+
+
 def counter_values(directory: str, counter: str, kernel_substr: str) -> list[float]:
     """Per-dispatch values of one counter for the kernels whose name contains
     ``kernel_substr`` (dimension instances summed)."""
@@ -115,28 +185,6 @@ def counter_values(directory: str, counter: str, kernel_substr: str) -> list[flo
     if not per:
         raise SystemExit(f"{counter} for {kernel_substr!r} not found in {path}")
     return [per[k] for k in sorted(per, key=int)]
-
-
-def write_stats(directory: str, out: str, cmd: str, title: str) -> None:
-    rows = kernel_stats(directory)
-    lines = [f"# {title}", "", "Command (from the repository root, on one MI355X):", "", "```", cmd, "```", "",
-             "| kernel | calls | average (us) | min (us) | max (us) | share |", "|---|---|---|---|---|---|"]
-    other_calls, other_ns, other_share = 0, 0.0, 0.0
-    for r in rows:
-        if "kore" not in r["Name"]:  # torch kernels that generate the inputs, copies
-            other_calls += int(r["Calls"])
-            other_ns += float(r["TotalDurationNs"])
-            other_share += float(r["Percentage"])
-            continue
-        lines.append(f"| `{_short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
-                     f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.1f}% |")
-    if other_calls:
-        lines.append(f"| other (input generation, copies; {other_calls} calls) | {other_calls} | "
-                     f"{other_ns / other_calls / 1e3:.1f} | | | {other_share:.1f}% |")
-    os.makedirs(os.path.dirname(os.path.abspath(out)), exist_ok=True)
-    with open(out, "w") as f:
-        f.write("\n".join(lines) + "\n")
-    print(f"wrote {out}")
 
 
 def write_traffic(a) -> None:
@@ -308,11 +356,35 @@ def grounding_derived(c: dict[str, float], xcds: int = 8, simds: int = 1024) -> 
     return d
 
 
+def copy_fetch_factor(path: str = TRAFFIC_FILE) -> float | None:
+    """known / counted read bytes of the plain device copy recorded in ``path`` (the
+    ``copy calibration`` line written by ``traffic``), or None."""
+    if not os.path.exists(path):
+        return None
+    factor = None
+    with open(path) as f:
+        for ln in f:
+            if ln.startswith("copy calibration:"):
+                # "... counted FETCH <f> KiB, WRITE <w> KiB (known <k> KiB)"
+                parts = ln.replace(",", " ").replace("(", " ").split()
+                fetch = float(parts[parts.index("FETCH") + 1])
+                known = float(parts[parts.index("known") + 1])
+                factor = known / fetch
+    return factor
+
+
 def write_grounding(a) -> None:
     c = grounding_counters(a.dirs, a.kernel)
     if not c:
         raise SystemExit(f"no counters for {a.kernel!r} in {a.dirs}")
     d = grounding_derived(c)
+    f = copy_fetch_factor()
+    if f is not None and "hbm_read_bytes" in d:
+        # the EA0 read requests cover a fixed share of the reads on this device; the copy
+        # calibration of profiles/hbm_traffic.md measures it (same counter basis as FETCH_SIZE)
+        d["hbm_read_bytes_ea0"] = d["hbm_read_bytes"]
+        d["hbm_read_bytes"] = d["hbm_read_bytes_ea0"] * f
+        d["copy_fetch_factor"] = f
     section = ["Commands (from the repository root, on one MI355X), one per pass:", "", "```", a.cmd, "```", "",
                f"Kernel: `{a.kernel}`; medians per dispatch.", "", "| counter | value |", "|---|---|"]
     section += [f"| `{k}` | {v:.6g} |" for k, v in sorted(c.items())]
@@ -328,7 +400,11 @@ def write_grounding(a) -> None:
               "+ 32 x (WRREQ - WRREQ_64B)); `mfma_busy_fraction` = min(1, MFMA_BUSY / GRBM_GUI_ACTIVE);",
               "`mfma_ops` = sum of the MFMA counters.  On MI355X MFMA_BUSY sums all 1024 SIMDs and",
               "GRBM_GUI_ACTIVE sums the 8 XCDs, so that fraction saturates; `mfma_busy_pct` =",
-              "MFMA_BUSY / (GRBM_GUI_ACTIVE / 8 x 1024) is per SIMD-cycle.  `mfma_flops` = 512 x MOPS."]
+              "MFMA_BUSY / (GRBM_GUI_ACTIVE / 8 x 1024) is per SIMD-cycle.  `mfma_flops` = 512 x MOPS.",
+              "The EA0 read requests count half of a plain device copy's reads on MI355X (the copy",
+              "calibration in `hbm_traffic.md`, where FETCH_SIZE has the same basis), so",
+              "`hbm_read_bytes` = `hbm_read_bytes_ea0` x `copy_fetch_factor`; writes need no factor.",
+              "These are the same bytes as `hbm_traffic.md`'s FETCH figures."]
     _replace_section(a.out, header, a.workload, section)
     print("\n".join(section))
 
@@ -360,6 +436,8 @@ def main(argv=None) -> int:
     s.add_argument("--out", required=True)
     s.add_argument("--cmd", required=True)
     s.add_argument("--title", default="rocprofv3 kernel-trace summary")
+    s.add_argument("--warmup-calls", type=int, default=None, help="warm-up calls printed by `run`")
+    s.add_argument("--iters", type=int, default=None, help="timed calls of `run`")
     t = sub.add_parser("traffic")
     t.add_argument("--workload", required=True)
     t.add_argument("--kernel", required=True)
@@ -391,7 +469,7 @@ def main(argv=None) -> int:
     elif a.action == "copy":
         _copy(a.mib, a.iters)
     elif a.action == "stats":
-        write_stats(a.dir, a.out, a.cmd, a.title)
+        write_stats(a.dir, a.out, a.cmd, a.title, a.warmup_calls, a.iters)
     elif a.action == "pmc":
         write_pmc(a)
     elif a.action == "grounding-passes":

@@ -17,6 +17,8 @@ Configurations (BASELINE.json):
 
 from __future__ import annotations
 
+from typing import Callable, NamedTuple
+
 import torch
 
 FP8 = torch.float8_e4m3fn
@@ -214,23 +216,32 @@ def grouped_fp8_inputs(M: int, E: int, N: int, K: int, seed: int = 0, device="cp
     return xq, wq, xs, ws, ti[:, 0].contiguous()
 
 
+class Workload(NamedTuple):
+    """One benchmark step: ``fn()`` runs the operator once on ``args`` (its device
+    inputs); ``(op, dims, dtype)`` key the roofline model (``kore_amd.roofline``)."""
+    fn: Callable[[], object]
+    op: str
+    dims: dict
+    dtype: str
+    args: tuple
+
+
 def bench_workloads():
-    """Ordered ``name -> builder(device)``; a builder returns ``(fn, op, dims, dtype)``
-    where ``fn()`` runs one step of the operator and ``(op, dims, dtype)`` key the
-    roofline model (``kore_amd.roofline``)."""
+    """Ordered ``name -> builder(device)``; a builder returns a :class:`Workload`."""
     import kore_amd  # deferred: the package imports this module
 
     def fp8(M):
         def build(dev):
             xq, wq, xs, ws = fp8_inputs(M, 7168, 4096, seed=0, device=dev)
-            return (lambda: kore_amd.gemm_a8w8_blockscale(xq, wq, xs, ws)), "gemm_fp8", \
-                {"M": M, "N": 7168, "K": 4096}, "fp8"
+            return Workload(lambda: kore_amd.gemm_a8w8_blockscale(xq, wq, xs, ws), "gemm_fp8",
+                            {"M": M, "N": 7168, "K": 4096}, "fp8", (xq, wq, xs, ws))
         return build
 
     def dense(n):
         def build(dev):
             a, b = dense_inputs(n, n, n, seed=0, device=dev)
-            return (lambda: kore_amd.gemm(a, b)), "gemm", {"M": n, "N": n, "K": n}, "bf16"
+            return Workload(lambda: kore_amd.gemm(a, b), "gemm", {"M": n, "N": n, "K": n}, "bf16",
+                            (a, b, None, "none"))
         return build
 
     def dense_kn(n):
@@ -240,26 +251,27 @@ def bench_workloads():
             g = _gen(dev, 0)
             a = (torch.randn((n, n), generator=g, device=dev) / n ** 0.5).to(torch.bfloat16)
             b = torch.randn((n, n), generator=g, device=dev).to(torch.bfloat16)
-            return (lambda: kore_amd.gemm(a, b)), "gemm", {"M": n, "N": n, "K": n}, "bf16"
+            return Workload(lambda: kore_amd.gemm(a, b), "gemm", {"M": n, "N": n, "K": n}, "bf16",
+                            (a, b, None, "none"))
         return build
 
     def fused(act):
         def build(dev):
             a, b, bias = fused_inputs(4096, 4096, 4096, seed=0, device=dev)
-            return (lambda: kore_amd.gemm_fused(a, b, bias, act)), "gemm", \
-                {"M": 4096, "N": 4096, "K": 4096}, "fp16"
+            return Workload(lambda: kore_amd.gemm_fused(a, b, bias, act), "gemm",
+                            {"M": 4096, "N": 4096, "K": 4096}, "fp16", (a, b, bias, act))
         return build
 
     def batched(dev):
         a, b = batched_inputs(64, 1024, 1024, 128, seed=0, device=dev)
-        return (lambda: kore_amd.batched_gemm(a, b)), "batched_gemm", \
-            {"B": 64, "M": 1024, "N": 1024, "K": 128}, "bf16"
+        return Workload(lambda: kore_amd.batched_gemm(a, b), "batched_gemm",
+                        {"B": 64, "M": 1024, "N": 1024, "K": 128}, "bf16", (a, b))
 
     def moe(T):
         def build(dev):
             args = moe_inputs(T, 8, 2, 4096, 14336, seed=0, device=dev)
-            return (lambda: kore_amd.fused_moe(*args)), "fused_moe", \
-                {"M": T, "E": 8, "topk": 2, "D": 4096, "I": 14336}, "bf16"
+            return Workload(lambda: kore_amd.fused_moe(*args), "fused_moe",
+                            {"M": T, "E": 8, "topk": 2, "D": 4096, "I": 14336}, "bf16", tuple(args))
         return build
 
     w = {"fp8_blockscale_2048x7168x4096": fp8(2048),
@@ -273,7 +285,8 @@ def bench_workloads():
     def backward(M, N, K):
         def build(dev):
             x, wt, dy = backward_inputs(M, N, K, seed=0, device=dev)
-            return (lambda: kore_amd.gemm_backward(x, wt, dy)), "gemm_backward", {"M": M, "N": N, "K": K}, "bf16"
+            return Workload(lambda: kore_amd.gemm_backward(x, wt, dy), "gemm_backward", {"M": M, "N": N, "K": K},
+                            "bf16", (x, wt, dy))
         return build
 
     # gemm_backward_bf16 primary shape (task.yaml): dX = dY.W and dW = dY^T.X
@@ -285,7 +298,8 @@ def bench_workloads():
             a = torch.randn((M, K), generator=g, device=dev) / K ** 0.5
             b = torch.randn((K, N), generator=g, device=dev) / K ** 0.5
             bias = torch.randn((N,), generator=g, device=dev)
-            return (lambda: kore_amd.gemm_bias(a, b, bias)), "gemm", {"M": M, "N": N, "K": K}, "fp32"
+            return Workload(lambda: kore_amd.gemm_bias(a, b, bias), "gemm", {"M": M, "N": N, "K": K}, "fp32",
+                            (a, b, bias, "none"))
         return build
 
     def task_kn(M, N, K, dtype, op):
@@ -297,8 +311,8 @@ def bench_workloads():
             a = (torch.randn((M, K), generator=g, device=dev) / K ** 0.5).to(dtype)
             b = (torch.randn((K, N), generator=g, device=dev) / K ** 0.5).to(dtype)
             bias = torch.randn((N,), generator=g, device=dev).to(dtype) if has_bias else None
-            return (lambda: kore_amd.gemm_fused(a, b, bias, act)), "gemm", {"M": M, "N": N, "K": K}, \
-                "bf16" if dtype == torch.bfloat16 else "fp16"
+            return Workload(lambda: kore_amd.gemm_fused(a, b, bias, act), "gemm", {"M": M, "N": N, "K": K},
+                            "bf16" if dtype == torch.bfloat16 else "fp16", (a, b, bias, act))
         return build
 
     # the gen_gemm_* primary (deep ring), its K-tail validation shape (packed path) and
@@ -314,8 +328,8 @@ def bench_workloads():
     def a8w8(M, N, K, kind):
         def build(dev):
             xq, wq, xs, ws = a8w8_inputs(M, N, K, kind, "pertoken", seed=0, device=dev)
-            return (lambda: kore_amd.gemm_a8w8(xq, wq, xs, ws)), "gemm_a8w8", \
-                {"M": M, "N": N, "K": K}, kind
+            return Workload(lambda: kore_amd.gemm_a8w8(xq, wq, xs, ws), "gemm_a8w8",
+                            {"M": M, "N": N, "K": K}, kind, (xq, wq, xs, ws))
         return build
 
     # a8w8 with per-token / per-channel scales (task primaries + decode)
@@ -329,8 +343,8 @@ def bench_workloads():
         def build(dev):
             hidden, wt, ids = grouped_inputs(M, E, N, K, seed=0, device=dev, router_bias=jagged_bias(E))
             used = int(torch.unique(ids).numel())
-            return (lambda: kore_amd.grouped_gemm(hidden, wt, ids)), "moe_grouped_gemm", \
-                {"M": M, "E": E, "N": N, "K": K, "E_used": used}, "bf16"
+            return Workload(lambda: kore_amd.grouped_gemm(hidden, wt, ids), "moe_grouped_gemm",
+                            {"M": M, "E": E, "N": N, "K": K, "E_used": used}, "bf16", (hidden, wt, ids))
         return build
 
     def permute(M, E, D):
@@ -339,7 +353,8 @@ def bench_workloads():
             hidden = torch.randn((M, D), generator=g, device=dev).to(torch.bfloat16)
             _, _, ids = grouped_inputs(M, E, 128, 8, seed=1, device=dev, router_bias=jagged_bias(E))
             sidx = torch.argsort(ids, stable=True).to(torch.int32)
-            return (lambda: kore_amd.moe_permute(hidden, sidx)), "moe_permute", {"M": M, "D": D}, "bf16"
+            return Workload(lambda: kore_amd.moe_permute(hidden, sidx), "moe_permute", {"M": M, "D": D}, "bf16",
+                            (hidden, sidx))
         return build
 
     # expert-dispatch stages: top-1 grouped GEMM and the token permute (task primaries)
@@ -350,8 +365,8 @@ def bench_workloads():
         def build(dev):
             xq, wq, xs, ws, ids = grouped_fp8_inputs(M, E, N, K, seed=0, device=dev, router_bias=jagged_bias(E))
             used = int(torch.unique(ids).numel())
-            return (lambda: kore_amd.grouped_gemm_fp8(xq, wq, xs, ws, ids)), "moe_grouped_gemm", \
-                {"M": M, "E": E, "N": N, "K": K, "E_used": used}, "fp8"
+            return Workload(lambda: kore_amd.grouped_gemm_fp8(xq, wq, xs, ws, ids), "moe_grouped_gemm",
+                            {"M": M, "E": E, "N": N, "K": K, "E_used": used}, "fp8", (xq, wq, xs, ws, ids))
         return build
 
     w["moe_grouped_gemm_fp8_4096x32x2048x4096"] = grouped_fp8(4096, 32, 2048, 4096)

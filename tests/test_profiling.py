@@ -52,6 +52,54 @@ def test_traffic_calibration_and_roundtrip(tmp_path):
     assert P.read_traffic("w1", str(tmp_path / "nope.md")) is None
 
 
+def _trace(d: Path, rows):
+    d.mkdir(parents=True)
+    with open(d / "run_kernel_trace.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        w.writeheader()
+        for name, start, dur in rows:
+            w.writerow({"Kernel_Name": name, "Start_Timestamp": start, "End_Timestamp": start + dur})
+
+
+def test_stats_keep_only_the_timed_calls(tmp_path):
+    """3 warm-up + 2 timed calls of a two-kernel step: only the last two calls' dispatches
+    (and the torch fill inside their window) are summarised; the slow first calls (clock
+    ramp) and the input generation before them are not."""
+    ka = "void kore::(anonymous namespace)::gemm_a_kernel<1>(P)"
+    kb = "kore::(anonymous namespace)::combine_kernel(P)"
+    fill = "void at::native::vectorized_elementwise_kernel<FillFunctor>(int)"
+    rows, t = [(fill, 0, 500)], 1000
+    for call, (da, db) in enumerate([(90, 9), (50, 5), (40, 4), (10, 2), (12, 2)]):
+        rows += [(ka, t, da), (kb, t + 100, db)]
+        if call == 4:
+            rows.append((fill, t + 150, 7))
+        t += 1000
+    _trace(tmp_path / "tr", rows)
+    kept = P.timed_dispatches(str(tmp_path / "tr"), warmup_calls=3, iters=2)
+    assert [d for n, d in kept if n == ka] == [10, 12] and [d for n, d in kept if n == kb] == [2, 2]
+    assert [d for n, d in kept if n == fill] == [7]
+    assert len(P.timed_dispatches(str(tmp_path / "tr"))) == 12
+    out = tmp_path / "s.md"
+    P.write_stats(str(tmp_path / "tr"), str(out), "cmd", "t", 3, 2)
+    row = [ln for ln in out.read_text().splitlines() if ln.startswith("| `gemm_a_kernel")][0]
+    assert row.startswith("| `gemm_a_kernel<1>` | 2 | 0.0 |")  # 11 ns average, printed in us
+    # a kernel count that is not a multiple of the calls is an error, not a silent average
+    _trace(tmp_path / "bad", rows[:-2])
+    try:
+        P.timed_dispatches(str(tmp_path / "bad"), warmup_calls=3, iters=2)
+    except SystemExit as e:
+        assert "not a multiple" in str(e)
+    else:
+        raise AssertionError("expected SystemExit")
+
+
+def test_copy_fetch_factor(tmp_path):
+    f = tmp_path / "t.md"
+    f.write_text("x\ncopy calibration: 256 MiB copy counted FETCH 131084 KiB, WRITE 262144 KiB (known 262144 KiB)\n")
+    assert math.isclose(P.copy_fetch_factor(str(f)), 262144 / 131084)
+    assert P.copy_fetch_factor(str(tmp_path / "none.md")) is None
+
+
 def test_short_kernel_names():
     assert P._short("void kore::(anonymous namespace)::gemm_buf_kernel<kore::BF16, 256, 256>(kore::P)") == \
         "gemm_buf_kernel<BF16, 256, 256>"
