@@ -428,6 +428,8 @@ def main(argv=None) -> int:
     r.add_argument("workload")
     r.add_argument("--iters", type=int, default=20)
     r.add_argument("--warmup", type=int, default=3)
+    r.add_argument("--min-warm-s", type=float, default=0.5,
+                   help="seconds of warm-up calls at least (0 for counter runs, which serialise dispatches)")
     c = sub.add_parser("copy")
     c.add_argument("--mib", type=int, default=256)
     c.add_argument("--iters", type=int, default=5)
@@ -465,7 +467,7 @@ def main(argv=None) -> int:
     gr.add_argument("--note", default="")
     a = p.parse_args(argv)
     if a.action == "run":
-        _run(a.workload, a.iters, a.warmup)
+        _run(a.workload, a.iters, a.warmup, a.min_warm_s)
     elif a.action == "copy":
         _copy(a.mib, a.iters)
     elif a.action == "stats":

@@ -339,6 +339,16 @@ def bench_workloads():
     w["moe_decode_T64"] = moe(64)
     w["moe_prefill_T4096"] = moe(4096)
 
+    def moe_task(T, E, topk, D, I):
+        # the fused_moe_silu_bf16 task's primary shape and inputs (weights ~ N(0,1) * 0.05)
+        def build(dev):
+            args = moe_inputs(T, E, topk, D, I, seed=0, device=dev, wscale=0.05)
+            return Workload(lambda: kore_amd.fused_moe(*args), "fused_moe",
+                            {"M": T, "E": E, "topk": topk, "D": D, "I": I}, "bf16", tuple(args))
+        return build
+
+    w["fused_moe_M256_E32_top8_D1024_I768"] = moe_task(256, 32, 8, 1024, 768)
+
     def grouped(M, E, N, K):
         def build(dev):
             hidden, wt, ids = grouped_inputs(M, E, N, K, seed=0, device=dev, router_bias=jagged_bias(E))
