@@ -276,33 +276,57 @@ __global__ void __launch_bounds__(256) gemm_splitk_kernel(const TileParams p, fl
   }
 }
 
-template <typename T>
+// Fixed-order sum of the split-K partials (slice 0, 1, ...), then bias, activation and
+// the store.  CW columns per thread: 4 with 16-byte partial loads when N % 4 == 0 -- the
+// loads of four slices go out before their adds, so their latencies overlap (a decode
+// GEMM reduces one row on a handful of workgroups) -- otherwise 8 scalar columns.
+template <typename T, int CW>
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(const float* part, int splits, int M, int N,
                                                             const uint16_t* bias, int act, uint16_t* C, int64_t ldc,
                                                             int vec) {
   using Op = MfmaOp<T>;
-  const int nc = (N + 7) / 8;
+  const int nc = (N + CW - 1) / CW;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)M * nc) return;
-  const int m = (int)(idx / nc), n = (int)(idx % nc) * 8;
-  float v[8];
+  const int m = (int)(idx / nc), n = (int)(idx % nc) * CW;
+  float v[CW];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) v[e] = 0.0f;
-  for (int s = 0; s < splits; ++s) {
-    const float* q = part + ((int64_t)s * M + m) * N + n;
+  for (int e = 0; e < CW; ++e) v[e] = 0.0f;
+  if constexpr (CW == 4) {
+    const float* q = part + (int64_t)m * N + n;
+    const int64_t slice = (int64_t)M * N;
+    int s = 0;
+    for (; s + 4 <= splits; s += 4) {
+      f32x4_t a[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      if (n + e < N) v[e] += q[e];
+      for (int u = 0; u < 4; ++u) a[u] = *(const f32x4_t*)(q + (s + u) * slice);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += a[u][e];
+    }
+    for (; s < splits; ++s) {
+      const f32x4_t a = *(const f32x4_t*)(q + s * slice);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += a[e];
+    }
+  } else {
+    for (int s = 0; s < splits; ++s) {
+      const float* q = part + ((int64_t)s * M + m) * N + n;
+#pragma unroll
+      for (int e = 0; e < CW; ++e)
+        if (n + e < N) v[e] += q[e];
+    }
   }
   if (bias != nullptr) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
+    for (int e = 0; e < CW; ++e)
       if (n + e < N) v[e] += Op::to_f32(bias[n + e]);
   }
   auto fin = [&](auto act_tag) {
     constexpr int ACT = decltype(act_tag)::value;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = apply_act<ACT>(v[e]);
+    for (int e = 0; e < CW; ++e) v[e] = apply_act<ACT>(v[e]);
   };
   switch (act) {
     case ACT_RELU: fin(std::integral_constant<int, ACT_RELU>{}); break;
@@ -313,11 +337,15 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const float* part, i
     default: break;
   }
   uint16_t* out = C + (int64_t)m * ldc + n;
-  if (vec && n + 8 <= N) {
-    *(u32x4_t*)out = u32x4_t{Op::pack2(v[0], v[1]), Op::pack2(v[2], v[3]), Op::pack2(v[4], v[5]), Op::pack2(v[6], v[7])};
+  if (vec && n + CW <= N) {
+    if constexpr (CW == 4)
+      *(u32x2_t*)out = u32x2_t{Op::pack2(v[0], v[1]), Op::pack2(v[2], v[3])};
+    else
+      *(u32x4_t*)out = u32x4_t{Op::pack2(v[0], v[1]), Op::pack2(v[2], v[3]), Op::pack2(v[4], v[5]),
+                               Op::pack2(v[6], v[7])};
   } else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
+    for (int e = 0; e < CW; ++e)
       if (n + e < N) out[e] = (uint16_t)(Op::pack2(v[e], 0.0f) & 0xffffu);
   }
 }
@@ -1062,11 +1090,19 @@ int launch_splitk(const GemmDesc& d, int splits, int kper, Ws& ws, hipStream_t s
                      dim3(256), 0, stream, p, part, splits, kper);
   int rc = check_launch("gemm_splitk_kernel");
   if (rc == KORE_OK) {
-    const int vec = (d.scm % 8 == 0) && aligned16(d.c);
-    const int64_t threads = d.M * ((d.N + 7) / 8);
-    hipLaunchKernelGGL((splitk_reduce_kernel<T>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
-                       (const float*)part, splits, (int)d.M, (int)d.N, (const uint16_t*)d.bias, d.act, (uint16_t*)d.c,
-                       d.scm, vec);
+    if (d.N % 4 == 0) {  // 16-byte partial loads (the workspace is 256-byte aligned)
+      const int vec = (d.scm % 4 == 0) && ((uintptr_t)d.c & 7u) == 0;
+      const int64_t threads = d.M * (d.N / 4);
+      hipLaunchKernelGGL((splitk_reduce_kernel<T, 4>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
+                         (const float*)part, splits, (int)d.M, (int)d.N, (const uint16_t*)d.bias, d.act,
+                         (uint16_t*)d.c, d.scm, vec);
+    } else {
+      const int vec = (d.scm % 8 == 0) && aligned16(d.c);
+      const int64_t threads = d.M * ((d.N + 7) / 8);
+      hipLaunchKernelGGL((splitk_reduce_kernel<T, 8>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
+                         (const float*)part, splits, (int)d.M, (int)d.N, (const uint16_t*)d.bias, d.act,
+                         (uint16_t*)d.c, d.scm, vec);
+    }
     rc = check_launch("splitk_reduce_kernel");
   }
   return rc;

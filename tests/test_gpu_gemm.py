@@ -179,11 +179,13 @@ def test_gemm_packed_path(gpu, M, N, K, dtype, op, layout):
                                                     (16, 11008, 4096, torch.float16, "gemm_bias_gelu", "kn"),
                                                     (7, 1002, 2048, torch.bfloat16, "gemm_bias_relu", "nk"),
                                                     (33, 3000, 1024, torch.float16, "gemm_sigmoid", "nk"),
-                                                    (64, 4096, 4096, torch.bfloat16, "gemm_bias_silu", "kn")])
+                                                    (64, 4096, 4096, torch.bfloat16, "gemm_bias_silu", "kn"),
+                                                    (1, 5120, 4096, torch.bfloat16, "gemm_bias", "nk")])
 def test_gemm_splitk(gpu, M, N, K, dtype, op, layout):
     """Decode-sized M with a long K splits K over the CUs (32x128 ring per slice, fp32
     partials, fixed-order reduce with the epilogue): ragged N (not a multiple of 4 on the
-    W.t() layout), several slice counts, and bit-identical repeated calls."""
+    W.t() layout: the 8-column scalar reduce), 2, 4, 6 and 8 slices (the 4-column reduce's
+    unrolled and remainder loops), and bit-identical repeated calls."""
     has_bias, act = kore_amd.GEMM_FUSION_OPS.get(op, (False, "none"))
     g = torch.Generator().manual_seed(M + N + K + 1)
     sc = 1.0 / K ** 0.5
