@@ -1162,9 +1162,12 @@ extern "C" int kore_gemm_a8w8_blockscale(const void* xq, int64_t ldx, const void
     hipStream_t st = (hipStream_t)stream;
     // 256x256 tiles halve LDS and L2 traffic per MFMA but need enough of them to
     // occupy the 256 CUs; then 256x128 tiles (three LDS slots); with fewer than that,
-    // 128x128 tiles on 4 waves (four slots) double the tile count again
+    // 128x128 tiles on 4 waves (four slots) double the tile count again -- unless
+    // those would need a second round on the CUs (M=768, N=7168: 128x128 41.0 us,
+    // 256x128 28.2 us)
     const int64_t tiles256 = (M + 255) / 256 * (N / 256);
     const int64_t tiles256x128 = (M + 255) / 256 * (N / 128);
+    const int64_t tiles128 = (M + 127) / 128 * (N / 128);
     // 256 x 224 tiles when they take fewer CU-rounds of tile area than 256 x 256 ones
     // (2048 x 7168: 256 tiles, one per CU, against 224 tiles on 256 CUs)
     const int64_t cus = device_cus();
@@ -1178,7 +1181,7 @@ extern "C" int kore_gemm_a8w8_blockscale(const void* xq, int64_t ldx, const void
       return xs4 ? launch_fp8_pipe<F8Cfg<256, 256, 8, 2, true>>(p, st)
                  : launch_fp8_pipe<F8Cfg<256, 256, 8, 2, false>>(p, st);
     }
-    if (tiles256x128 >= 192) {
+    if (tiles256x128 >= 192 || tiles128 > cus) {
       return xs4 ? launch_fp8_pipe<F8Cfg<256, 128, 8, 3, true>>(p, st)
                  : launch_fp8_pipe<F8Cfg<256, 128, 8, 3, false>>(p, st);
     }
@@ -1293,10 +1296,13 @@ int launch_a8w8(const Fp8Params& p0, bool skinny, hipStream_t st) {
     if (p.M <= 64) return launch_fp8_skinny<SkinnyCfg<64, 4, 3, MODE>>(p, st);
     return launch_fp8_skinny<SkinnyCfg<128, 4, 2, MODE>>(p, st);
   }
+  // tile choice as for the block-scale kernels
   const int64_t tiles256 = (int64_t)(p.M + 255) / 256 * (p.N / 256);
   const int64_t tiles256x128 = (int64_t)(p.M + 255) / 256 * (p.N / 128);
+  const int64_t tiles128 = (int64_t)(p.M + 127) / 128 * (p.N / 128);
   if (p.N % 256 == 0 && tiles256 >= 192) return launch_fp8_pipe<F8Cfg<256, 256, 8, 2, false, MODE>>(p, st);
-  if (tiles256x128 >= 192) return launch_fp8_pipe<F8Cfg<256, 128, 8, 3, false, MODE>>(p, st);
+  if (tiles256x128 >= 192 || tiles128 > device_cus())
+    return launch_fp8_pipe<F8Cfg<256, 128, 8, 3, false, MODE>>(p, st);
   return launch_fp8_pipe<F8Cfg<128, 128, 4, 4, false, MODE>>(p, st);
 }
 

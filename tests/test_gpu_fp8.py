@@ -41,12 +41,14 @@ def test_fp8_task_shapes(gpu, M, N, K, seed):
 
 
 @pytest.mark.parametrize("M,N,K", [(4000, 3072, 640), (4000, 3072, 512), (3840, 3072, 1024),
-                                   (1100, 6016, 512), (1100, 6016, 640)])
+                                   (1100, 6016, 512), (1100, 6016, 640), (768, 7168, 1024), (700, 7168, 512)])
 def test_fp8_wide_tiles(gpu, M, N, K):
     """Problems with at least 192 tiles of 256x256 run on the 256x256 (two-slot) kernel:
     a partial last M tile (M=4000), per-step scale loads (K/128 = 5) and four-step
     scale loads (K/128 = 4, 8).  N = 6016 (not a multiple of 256) with 235 tiles of
-    256x128 runs the 256x128 (three-slot) kernel; smaller problems run 128x128 tiles."""
+    256x128 runs the 256x128 (three-slot) kernel, and so do M = 768 / 700 at N = 7168
+    (168 tiles, where 336 / 336 tiles of 128x128 would need two rounds of the CUs);
+    smaller problems run 128x128 tiles."""
     xq, wq, xs, ws = W.fp8_inputs(M, N, K, seed=M + K, scale=0.2)
     out = _run(gpu, xq, wq, xs, ws)
     ref = matmul_blockscale_ref(xq, wq, xs, ws)
