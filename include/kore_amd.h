@@ -198,6 +198,15 @@ int kore_gemm_a8w8(int qtype, const void* xq, int64_t ldx_m, int64_t ldx_k,
  *           align_offsets in kore/tasks/breadth/moe_ext.py:617-621.
  */
 int64_t kore_moe_align_capacity(int64_t T, int64_t topk, int64_t E, int64_t block);
+
+/*
+ * Test hook, no counterpart in the reference: with on != 0, kore_fused_moe and
+ * kore_moe_grouped_gemm take the register-staged tile paths that operands of 4 GiB or
+ * more would take, so tests can check them at small sizes.  Process-wide, not
+ * thread-safe; returns the previous setting.
+ */
+int kore_moe_test_force_generic(int on);
+
 int kore_moe_align(const int32_t* topk_ids, int64_t T, int64_t topk, int64_t E,
                    int64_t block, int32_t* offsets, int32_t* sorted_slots,
                    int32_t* block_expert, int64_t cap, void* stream);

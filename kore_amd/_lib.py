@@ -41,6 +41,7 @@ SIGNATURES = {
     "kore_gemm_a8w8": (_i32, [_i32, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64,
                               _i64, _i64, _i64, _vp]),
     "kore_moe_align_capacity": (_i64, [_i64, _i64, _i64, _i64]),
+    "kore_moe_test_force_generic": (_i32, [_i32]),
     "kore_moe_grouped_gemm_workspace_bytes": (_sz, [_i64, _i64]),
     "kore_moe_grouped_gemm": (_i32, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _sz, _vp]),
     "kore_moe_grouped_gemm_fp8": (_i32, [_vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,

@@ -664,6 +664,11 @@ int launch_moe_buf(MoeGemmParams p, int64_t cap, hipStream_t st) {
 
 namespace kore {
 namespace {
+// Test hook (kore_moe_test_force_generic): route the MoE GEMMs to the register-staged
+// tile paths that operands beyond the 32-bit buffer range take, so tests reach them at
+// small sizes.  Process-wide; off by default.
+int g_force_generic = 0;
+
 // Sort/align of S slots: the chunked kernel, one workgroup per 256 slots.
 int launch_align(const int32_t* ids, int64_t S, int64_t E, int block, int32_t* offsets, int32_t* sorted,
                  int32_t* block_expert, int64_t cap, hipStream_t st) {
@@ -676,6 +681,12 @@ int launch_align(const int32_t* ids, int64_t S, int64_t E, int block, int32_t* o
 }
 }  // namespace
 }  // namespace kore
+
+extern "C" int kore_moe_test_force_generic(int on) {
+  const int prev = kore::g_force_generic;
+  kore::g_force_generic = on != 0;
+  return prev;
+}
 
 extern "C" int64_t kore_moe_align_capacity(int64_t T, int64_t topk, int64_t E, int64_t block) {
   if (T < 0 || topk <= 0 || E <= 0 || block <= 0) return -1;
@@ -751,8 +762,8 @@ extern "C" int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, c
   p.w_rstride = D;
   // buffer-load engine needs operand byte ranges (plus a K step past a padding row's
   // offset) below 4 GiB and K % 64 == 0
-  const bool buf_ok =
-      T * ldh * 2 + 4 * D < (1ll << 32) && 2 * I * D * 2 < (1ll << 32) && D % 64 == 0 && I % 64 == 0;
+  const bool buf_ok = T * ldh * 2 + 4 * D < (1ll << 32) && 2 * I * D * 2 < (1ll << 32) && D % 64 == 0 &&
+                      I % 64 == 0 && !g_force_generic;
   // 128-row blocks without the buffer engine run 32-row tiles (four per aligned block)
   rc = (BM == 32 && buf_ok) ? launch_moe_decode<MOE_GATEUP, 128, 7>(p, cap, st)
        : (BM == 128 && buf_ok) ? launch_moe_decode<MOE_GATEUP, 128, 2, 128>(p, cap, st)
@@ -900,7 +911,8 @@ extern "C" int kore_moe_grouped_gemm(const void* x, int64_t ldx, const void* w, 
   p.abm = BM;
   p.out = (uint16_t*)out;
   p.ldo = ldo;
-  const bool buf_ok = K % 64 == 0 && M * ldx * 2 + 4 * K < (1ll << 32) && N * K * 2 < (1ll << 32);
+  const bool buf_ok =
+      K % 64 == 0 && M * ldx * 2 + 4 * K < (1ll << 32) && N * K * 2 < (1ll << 32) && !g_force_generic;
   if (BM == 32) {
     rc = buf_ok ? launch_moe_decode<MOE_PLAIN, 128, 7>(p, cap, st) : launch_moe_gemm<MOE_PLAIN, 32, 128, 1, 4>(p, cap, st);
   } else if (buf_ok) {

@@ -105,6 +105,28 @@ def test_fused_moe_prefill_config_sampled(gpu):
     verdict(out[rows], ref, "north_star", "bf16", "prefill T=4096 (1e-2)")
 
 
+@pytest.mark.parametrize("T,E,topk,D,I", [(64, 8, 2, 256, 384), (300, 4, 1, 256, 384), (640, 4, 2, 512, 384),
+                                          (700, 4, 3, 384, 256)])
+def test_fused_moe_generic_tile_paths(gpu, T, E, topk, D, I):
+    """The register-staged tile paths that operands beyond the 32-bit buffer range take
+    (forced with the kore_moe_test_force_generic hook): 32-row tiles over 32- and
+    128-row aligned blocks (block_expert indexed through the aligned block size) and
+    the 256 / 128-row prefill tiles (D % 256 == 0 and not), against the oracle."""
+    from kore_amd import _lib
+
+    lib = _lib.load()
+    hidden, w1, w2, tw, ti = W.moe_inputs(T, E, topk, D, I, seed=T + 3, wscale=0.05)
+    args = [t.to(gpu) for t in (hidden, w1, w2, tw, ti)]
+    prev = lib.kore_moe_test_force_generic(1)
+    try:
+        out = kore_amd.fused_moe(*args)
+    finally:
+        lib.kore_moe_test_force_generic(prev)
+    ref = moe_ref(hidden, w1, w2, tw, ti)
+    verdict(out, ref, "fused_moe", "bf16", f"generic tiles T{T} E{E} k{topk} D{D} I{I}")
+    verdict(out, ref, "north_star", "bf16", f"generic tiles T{T} (1e-2)")
+
+
 def test_fused_moe_invariants(gpu):
     """Token-permutation equivariance and top-k slot-order invariance."""
     hidden, w1, w2, tw, ti = W.moe_inputs(96, 8, 2, 512, 384, seed=5, wscale=0.05)
