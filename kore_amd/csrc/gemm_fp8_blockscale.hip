@@ -1152,7 +1152,7 @@ extern "C" int kore_gemm_a8w8_blockscale(const void* xq, int64_t ldx, const void
     if (M <= 16) return launch_fp8_skinny<SkinnyCfg<16, 8, 3>>(p, st);
     if (M <= 32) return launch_fp8_skinny<SkinnyCfg<32, 8, 2>>(p, st);
     if (M <= 64) return launch_fp8_skinny<SkinnyCfg<64, 4, 3>>(p, st);
-    return launch_fp8_skinny<SkinnyCfg<128, 2, 3>>(p, st);
+    return launch_fp8_skinny<SkinnyCfg<128, 2, 2>>(p, st);  // 2 stages: 16.8 us at M=128 (3: 19.7)
   }
   if (pipe_ok) {
     // four K steps of scales per 16-byte load when scale rows are contiguous, 16-byte
