@@ -8,7 +8,7 @@ import torch
 import kore_amd
 from kore_amd import workloads as W
 from oracle.gemm import batched_gemm_ref
-from tests.fourprong import bit_equal, pair_only, verdict
+from tests.fourprong import adversarial, bit_equal, pair_only, verdict
 
 pytestmark = pytest.mark.gpu
 
@@ -34,6 +34,19 @@ def test_batched_task_shapes(gpu, Bn, M, N, K, seed):
     ref = batched_gemm_ref(a, b)
     verdict(out, ref, "batched_gemm", "bf16", f"B{Bn} {M}x{N}x{K}")
     pair_only(out, ref, "bf16", f"B{Bn} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("Bn,M,N,K", [(64, 1024, 1024, 128), (4, 256, 384, 512)])
+def test_batched_adversarial(gpu, Bn, M, N, K):
+    """The generic adversarial fills (kore/tasks/_genops.py:855-879) through the
+    persistent short-K kernel (the config's K = 128) and the tiled batched path:
+    constant, alternating-sign, large (1e3: 1e8-scale sums) and small operands."""
+    g = torch.Generator().manual_seed(Bn + K)
+    a = (torch.randn((Bn, M, K), generator=g) * 0.1).bfloat16()
+    b = (torch.randn((Bn, N, K), generator=g) * 0.1).bfloat16()
+    for name, (aa, bb) in adversarial((a, b)):
+        out = kore_amd.batched_gemm(aa.to(gpu), bb.to(gpu))
+        verdict(out, batched_gemm_ref(aa, bb), "batched_gemm", "bf16", f"B{Bn} {M}x{N}x{K} adversarial {name}")
 
 
 def test_batched_metamorphic_and_determinism(gpu):

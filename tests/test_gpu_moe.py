@@ -9,7 +9,7 @@ import torch
 import kore_amd
 from kore_amd import workloads as W
 from oracle.moe import moe_align_ref, moe_ref, trace32_bias
-from tests.fourprong import bit_equal, pair_only, verdict  # noqa: F401
+from tests.fourprong import ADV_FILLS, bit_equal, pair_only, verdict  # noqa: F401
 
 pytestmark = pytest.mark.gpu
 
@@ -91,17 +91,19 @@ def test_fused_moe_decode_config(gpu):
 
 
 def test_fused_moe_prefill_config_sampled(gpu):
-    """BASELINE config 5 prefill: T=4096 on the GPU; the oracle checks 48 sampled tokens
-    (tokens are independent), plus determinism of the whole output."""
+    """BASELINE config 5 prefill: T=4096 on the GPU; the oracle checks 256 sampled tokens
+    (tokens are independent; 512 expert slots cover all 8 experts), plus determinism of
+    the whole output."""
     T, E, topk, D, I = 4096, 8, 2, 4096, 14336
     dev = gpu
     hidden, w1, w2, tw, ti = W.moe_inputs(T, E, topk, D, I, seed=1, device=dev)
     out = kore_amd.fused_moe(hidden, w1, w2, tw, ti)
     out2 = kore_amd.fused_moe(hidden, w1, w2, tw, ti)
     assert bit_equal(out, out2), "determinism"
-    rows = torch.randperm(T, generator=torch.Generator().manual_seed(0))[:48].to(dev)
+    rows = torch.randperm(T, generator=torch.Generator().manual_seed(0))[:256].to(dev)
+    assert len(torch.unique(ti[rows])) == E
     ref = moe_ref(hidden[rows].cpu(), w1.cpu(), w2.cpu(), tw[rows].cpu(), ti[rows].cpu())
-    verdict(out[rows], ref, "fused_moe", "bf16", "prefill T=4096 (48 sampled tokens)")
+    verdict(out[rows], ref, "fused_moe", "bf16", "prefill T=4096 (256 sampled tokens)")
     verdict(out[rows], ref, "north_star", "bf16", "prefill T=4096 (1e-2)")
 
 
@@ -125,6 +127,21 @@ def test_fused_moe_generic_tile_paths(gpu, T, E, topk, D, I):
     ref = moe_ref(hidden, w1, w2, tw, ti)
     verdict(out, ref, "fused_moe", "bf16", f"generic tiles T{T} E{E} k{topk} D{D} I{I}")
     verdict(out, ref, "north_star", "bf16", f"generic tiles T{T} (1e-2)")
+
+
+@pytest.mark.parametrize("T,E,topk,D,I", [(64, 8, 2, 256, 384), (600, 4, 2, 256, 256)])
+def test_fused_moe_adversarial(gpu, T, E, topk, D, I):
+    """The generic adversarial fills (kore/tasks/_genops.py:855-879) on the activations
+    and both weight tensors, the router's weights and ids kept: constant operands
+    (h = silu(g) * u at 1e16 scale for the 'large' fill, silu of large negative gates
+    at -0), alternating signs and small values; 32-row decode blocks and 256-row
+    prefill tiles."""
+    hidden, w1, w2, tw, ti = W.moe_inputs(T, E, topk, D, I, seed=T + 5, wscale=0.05)
+    for name, fill in ADV_FILLS.items():
+        h, a1, a2 = fill(hidden), fill(w1), fill(w2)
+        out = kore_amd.fused_moe(h.to(gpu), a1.to(gpu), a2.to(gpu), tw.to(gpu), ti.to(gpu))
+        ref = moe_ref(h, a1, a2, tw, ti)
+        verdict(out, ref, "fused_moe", "bf16", f"adversarial {name} T{T} E{E} k{topk} D{D} I{I}")
 
 
 def test_fused_moe_invariants(gpu):
