@@ -859,6 +859,52 @@ __global__ void __launch_bounds__(256) pack16_kernel(const uint16_t* in, int64_t
   }
 }
 
+// The common packing case, K-contiguous rows whose element stride leaves them unaligned
+// (K = 4095): out[b][r][k] = in[b * sbat + r * sr + k] for k < K, 0 for K <= k < Kp.
+// One thread per 16-byte output chunk of 8 elements, built from the naturally aligned
+// dwords that cover it (five when the chunk starts at a 2 mod 4 byte address, shifted
+// into place with alignbyte); the row's last partial chunk and the zero tail go element
+// by element.  Each wave streams 1 KiB of a row, so this is a straight copy at HBM rate
+// instead of pack16_kernel's 2-byte loads and LDS round trip.
+__global__ void __launch_bounds__(256) repitch16_kernel(const uint16_t* in, int64_t sr, int64_t sbat,
+                                                        uint16_t* out, int64_t obat, int R, int K, int Kp) {
+  const int cpr = Kp / 8;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)R * cpr) return;
+  const int r = (int)(idx / cpr), k0 = (int)(idx % cpr) * 8;
+  const uint16_t* src = in + (int64_t)blockIdx.y * sbat + (int64_t)r * sr + k0;
+  u32x4_t v;
+  if (k0 + 8 < K) {
+    // elements k0 .. k0 + 8 exist, so the covering dwords stay inside the row
+    const uintptr_t addr = (uintptr_t)src;
+    const uint32_t* p = (const uint32_t*)(addr & ~(uintptr_t)3);
+    const bool odd = (addr & 2) != 0;
+    const uint32_t d0 = p[0], d1 = p[1], d2 = p[2], d3 = p[3], d4 = p[odd ? 4 : 3];
+    v = odd ? u32x4_t{__builtin_amdgcn_alignbyte(d1, d0, 2), __builtin_amdgcn_alignbyte(d2, d1, 2),
+                      __builtin_amdgcn_alignbyte(d3, d2, 2), __builtin_amdgcn_alignbyte(d4, d3, 2)}
+            : u32x4_t{d0, d1, d2, d3};
+  } else {
+    uint32_t e[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) e[j] = k0 + j < K ? (uint32_t)src[j] : 0u;
+    v = u32x4_t{e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16)};
+  }
+  *(u32x4_t*)(out + (int64_t)blockIdx.y * obat + (int64_t)r * Kp + k0) = v;
+}
+
+int launch_pack16(const uint16_t* in, int64_t sr, int64_t sk, int64_t sbat, uint16_t* out, int64_t obat, int64_t R,
+                  int64_t K, int64_t Kp, int64_t batch, hipStream_t stream) {
+  if (sk == 1) {
+    const int64_t chunks = R * (Kp / 8);
+    hipLaunchKernelGGL(repitch16_kernel, dim3((unsigned)((chunks + 255) / 256), (unsigned)batch), dim3(256), 0, stream,
+                       in, sr, sbat, out, obat, (int)R, (int)K, (int)Kp);
+    return check_launch("repitch16_kernel");
+  }
+  hipLaunchKernelGGL(pack16_kernel, dim3((unsigned)(Kp / 64), (unsigned)((R + 63) / 64), (unsigned)batch), dim3(256), 0,
+                     stream, in, sr, sk, sbat, out, obat, (int)R, (int)K, (int)Kp);
+  return check_launch("pack16_kernel");
+}
+
 // ---------------------------------------------------------------------------------
 // Host dispatch
 // ---------------------------------------------------------------------------------
@@ -1182,9 +1228,7 @@ int launch_padded(const GemmDesc& d, Ws& ws, hipStream_t stream) {
                      ws_bytes(a_bytes + b_bytes), ws.bytes);
   uint16_t* ap = (uint16_t*)buf;
   uint16_t* bp = (uint16_t*)((char*)buf + a_bytes);
-  hipLaunchKernelGGL(pack16_kernel, dim3((unsigned)(Kp / 64), (unsigned)((d.M + 63) / 64), (unsigned)d.batch), dim3(256),
-                     0, stream, (const uint16_t*)d.a, d.sam, d.sak, d.sa, ap, d.M * Kp, (int)d.M, (int)d.K, (int)Kp);
-  int rc = check_launch("pack16_kernel");
+  int rc = launch_pack16((const uint16_t*)d.a, d.sam, d.sak, d.sa, ap, d.M * Kp, d.M, d.K, Kp, d.batch, stream);
   GemmDesc q = d;
   q.a = ap;
   q.sam = Kp;
@@ -1193,10 +1237,7 @@ int launch_padded(const GemmDesc& d, Ws& ws, hipStream_t stream) {
   q.K = Kp;
   if (rc == KORE_OK && !b_nc) {
     // B^T rows (n) with K-contiguous, zero-padded K
-    hipLaunchKernelGGL(pack16_kernel, dim3((unsigned)(Kp / 64), (unsigned)((d.N + 63) / 64), (unsigned)d.batch),
-                       dim3(256), 0, stream, (const uint16_t*)d.b, d.sbn, d.sbk, d.sb, bp, d.N * Kp, (int)d.N, (int)d.K,
-                       (int)Kp);
-    rc = check_launch("pack16_kernel");
+    rc = launch_pack16((const uint16_t*)d.b, d.sbn, d.sbk, d.sb, bp, d.N * Kp, d.N, d.K, Kp, d.batch, stream);
     q.b = bp;
     q.sbk = 1;
     q.sbn = Kp;

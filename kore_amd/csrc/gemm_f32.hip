@@ -375,6 +375,40 @@ __global__ void __launch_bounds__(256) pack32_kernel(const float* in, int64_t sr
   }
 }
 
+// K-contiguous rows (any row stride, e.g. K = 4095): out[r][k] = in[r * sr + k] for k < K,
+// 0 for K <= k < Kp.  One thread per 16-byte output chunk of 4 floats (dword loads, the
+// row's last partial chunk and the zero tail element by element): a straight copy at HBM
+// rate instead of pack32_kernel's LDS round trip.
+__global__ void __launch_bounds__(256) repitch32_kernel(const float* in, int64_t sr, float* out, int R, int K,
+                                                        int Kp) {
+  const int cpr = Kp / 4;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)R * cpr) return;
+  const int r = (int)(idx / cpr), k0 = (int)(idx % cpr) * 4;
+  const float* src = in + (int64_t)r * sr + k0;
+  f32x4v v;
+  if (k0 + 4 <= K) {
+    v = f32x4v{src[0], src[1], src[2], src[3]};
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = k0 + j < K ? src[j] : 0.0f;
+  }
+  *(f32x4v*)(out + (int64_t)r * Kp + k0) = v;
+}
+
+int launch_pack32(const float* in, int64_t sr, int64_t sk, float* out, int64_t R, int64_t K, int64_t Kp,
+                  hipStream_t st) {
+  if (sk == 1) {
+    const int64_t chunks = R * (Kp / 4);
+    hipLaunchKernelGGL(repitch32_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, st, in, sr, out, (int)R,
+                       (int)K, (int)Kp);
+    return check_launch("repitch32_kernel");
+  }
+  hipLaunchKernelGGL(pack32_kernel, dim3((unsigned)(Kp / 64), (unsigned)((R + 63) / 64)), dim3(256), 0, st, in, sr, sk,
+                     out, (int)R, (int)K, (int)Kp);
+  return check_launch("pack32_kernel");
+}
+
 // ---------------------------------------------------------------------------------
 // Deep-ring fp32 kernel.  The register-staged kernel above stalls once per K step on
 // its LDS stores and the barrier, with one step of loads in flight.  Here an NSLOT-deep
@@ -618,9 +652,7 @@ int launch_gemm_f32(const GemmF32Args& d, Ws& ws, hipStream_t st) {
     {
       float* ap = buf;
       float* bp = (float*)((char*)buf + a_bytes);
-      hipLaunchKernelGGL(pack32_kernel, dim3((unsigned)(Kp / 64), (unsigned)((d.M + 63) / 64)), dim3(256), 0, st,
-                         (const float*)d.a, d.sam, d.sak, ap, (int)d.M, (int)d.K, (int)Kp);
-      int rc = check_launch("pack32_kernel");
+      int rc = launch_pack32((const float*)d.a, d.sam, d.sak, ap, d.M, d.K, Kp, st);
       if (rc == KORE_OK && b_inplace) {
         F32Params p{};
         p.a = ap;
@@ -642,9 +674,7 @@ int launch_gemm_f32(const GemmF32Args& d, Ws& ws, hipStream_t st) {
       }
       if (rc == KORE_OK) {
         // rows of B^T: element (n, k) at b[k * sbk + n * sbn]
-        hipLaunchKernelGGL(pack32_kernel, dim3((unsigned)(Kp / 64), (unsigned)((d.N + 63) / 64)), dim3(256), 0, st,
-                           (const float*)d.b, d.sbn, d.sbk, bp, (int)d.N, (int)d.K, (int)Kp);
-        rc = check_launch("pack32_kernel");
+        rc = launch_pack32((const float*)d.b, d.sbn, d.sbk, bp, d.N, d.K, Kp, st);
       }
       if (rc == KORE_OK) {
         F32Params p{};

@@ -357,6 +357,38 @@ def test_gemm_determinism(gpu):
     assert bit_equal(x1, x2)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("K,start", [(4089, 1), (4095, 0), (4093, 3), (1031, 1)])
+def test_gemm_repitch_k_tails(gpu, dtype, K, start):
+    """Packed path through the row re-stride kernels: A as a view of a wider tensor
+    starting `start` elements in (row 0 at a 2 mod 4 byte address for odd starts in 16-bit
+    types), row stride K + 9, K % 8 in {1, 3, 7}; B given as W.t() with W [N, K] in the
+    same layout, so B^T is re-strided too (fp32: B read in place when N-contiguous, here
+    packed).  Zero K tails padded to the kernels' K step."""
+    M, N = 512, 1024
+    g = torch.Generator().manual_seed(K + start)
+    afull = (torch.randn((M, K + 9), generator=g) / 16).to(dtype)
+    wfull = (torch.randn((N, K + 9), generator=g) / 16).to(dtype)
+    a, w = afull[:, start:start + K], wfull[:, start:start + K]
+    ad, wd = afull.to(gpu)[:, start:start + K], wfull.to(gpu)[:, start:start + K]
+    assert ad.stride() == (K + 9, 1) and wd.stride() == (K + 9, 1)
+    out = kore_amd.gemm_fused(ad, wd.t(), None, "none")
+    ref = gemm_fusion_ref(a, w.t(), None, "none")
+    verdict(out, ref, "gemm_fusion", str(dtype), f"re-stride {M}x{N}x{K} start {start}")
+    assert bit_equal(kore_amd.gemm_fused(ad, wd.t(), None, "none"), out), "determinism"
+
+
+def test_batched_repitch_k_tail(gpu):
+    """Batched packed path with a K tail (K = 1001): per-batch re-stride of A and B^T."""
+    Bn, M, N, K = 4, 512, 512, 1001
+    g = torch.Generator().manual_seed(1)
+    a = (torch.randn((Bn, M, K), generator=g) * 0.1).bfloat16()
+    b = (torch.randn((Bn, N, K), generator=g) * 0.1).bfloat16()
+    out = kore_amd.batched_gemm(a.to(gpu), b.to(gpu))
+    from oracle.gemm import batched_gemm_ref
+    verdict(out, batched_gemm_ref(a, b), "batched_gemm", "bf16", f"re-stride B{Bn} {M}x{N}x{K}")
+
+
 def test_gemm_strided_and_degenerate(gpu):
     """Non-unit strides on both operands (generic kernel), K=0 and empty outputs."""
     g = torch.Generator().manual_seed(5)
