@@ -242,7 +242,7 @@ __global__ void __launch_bounds__(256) gemm_deep_kernel(const TileParams p) {
 // ---------------------------------------------------------------------------------
 template <typename T, int BL, int BM, int BN, int WM, int WN, int NSLOT>
 __global__ void __launch_bounds__(256) gemm_splitk_kernel(const TileParams p, float* part, int splits, int kper) {
-  using E = RingEngine<T, BM, BN, WM, WN, NSLOT, BL>;
+  using E = RingEngine<T, BM, BN, WM, WN, NSLOT, BL, kCpolNT>;
   __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int s = (int)blockIdx.x % splits, t = (int)blockIdx.x / splits;
@@ -824,8 +824,8 @@ __global__ void __launch_bounds__(256) transpose16_kernel(const uint16_t* in, in
 }
 
 // ---------------------------------------------------------------------------------
-// Operand packing for layouts the direct-to-LDS engines cannot read in place (K not a
-// multiple of 8 so rows are not 16-byte aligned, transposed or strided operands):
+// Operand packing for transposed or strided layouts the direct-to-LDS engines cannot
+// read in place (K-contiguous rows that are only misaligned go to repitch16_kernel):
 // out[b][r][k] = in[b * sbat + r * sr + k * sk] for k < K and 0 for K <= k < Kp, with
 // out rows of Kp (a multiple of 64) elements.  64 x 64 tiles through LDS; the loads
 // walk whichever of r and k is unit-stride so they coalesce, the stores are 16-byte

@@ -348,8 +348,8 @@ __global__ void __launch_bounds__(256) gemm_f32_generic_kernel(const F32GenericP
 
 inline bool al16(const void* q) { return ((uintptr_t)q & 15u) == 0; }
 
-// Operands the MFMA kernel cannot read (K % 64 != 0, e.g. the tasks' K = 4095; unaligned
-// rows; transposed or strided operands): out[r][k] = in[r * sr + k * sk] for k < K, 0 for
+// Transposed or strided operands the MFMA kernel cannot read (K-contiguous rows go to
+// repitch32_kernel below): out[r][k] = in[r * sr + k * sk] for k < K, 0 for
 // K <= k < Kp (a multiple of 64), rows of Kp floats.  64 x 64 tiles through LDS, loads
 // along whichever index is unit-stride, 16-byte row stores.
 __global__ void __launch_bounds__(256) pack32_kernel(const float* in, int64_t sr, int64_t sk, float* out, int R, int K,

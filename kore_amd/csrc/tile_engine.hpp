@@ -330,12 +330,17 @@ __device__ __forceinline__ u32x2_t lds_read_tr16(const uint16_t* p) {
 // the load pipeline.  Loads issued this way are invisible to the compiler: the callers
 // order them with explicit vmcnt waits and barriers, and no compiler-generated M0 use
 // may sit between them (M0 is not preserved).
+template <int CPOL = kCpolDefault>
 __device__ __forceinline__ void buf_lds16_asm(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
                                               const uint16_t* lds_dst) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds_dst);
   // one wait state between the SALU write of M0 and the LDS DMA that reads it
-  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
-               :: "v"(voff), "s"(r), "s"(soff), "s"(m0) : "memory");
+  if constexpr (CPOL == kCpolNT)
+    asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen nt lds"
+                 :: "v"(voff), "s"(r), "s"(soff), "s"(m0) : "memory");
+  else
+    asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :: "v"(voff), "s"(r), "s"(soff), "s"(m0) : "memory");
 }
 
 // N-contiguous B stage layout shared by the direct-to-LDS engines: 64 K-rows of BN
@@ -660,8 +665,10 @@ namespace kore {
 // reads), so every wave issues the same loads and the vmcnt arithmetic is uniform.
 // A and K-contiguous B use 128-byte rows with the swz8 chunk swizzle; N-contiguous B
 // uses the nc_x layout and LDS transpose reads (loads then go out as inline asm).
+// BCPOL is the cache policy of the B loads: non-temporal where every B element is read
+// by one workgroup only (the split-K decode GEMM streams its weights once).
 // ---------------------------------------------------------------------------------
-template <typename T, int BM, int BN, int WM, int WN, int NSLOT, int BL>
+template <typename T, int BM, int BN, int WM, int WN, int NSLOT, int BL, int BCPOL = kCpolDefault>
 struct RingEngine {
   static constexpr int NW = 4;
   static_assert(WM * WN == NW, "4 waves");
@@ -690,14 +697,17 @@ struct RingEngine {
 
   __device__ __forceinline__ void issue(uint16_t* lds, int slot, uint32_t soff, uint32_t soffb, int wave) const {
     uint16_t* st = lds + slot * STAGE;
-    auto ld = [&](__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t so, uint16_t* dst) {
-      if constexpr (NC) buf_lds16_asm(r, voff, so, dst);
-      else buf_lds16(r, voff, so, dst);
+    auto ld = [&](__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t so, uint16_t* dst, auto cpol_tag) {
+      constexpr int CP = decltype(cpol_tag)::value;
+      if constexpr (NC) buf_lds16_asm<CP>(r, voff, so, dst);
+      else buf_lds16_cp<CP>(r, voff, so, dst);
     };
 #pragma unroll
-    for (int j = 0; j < AJ; ++j) ld(ra, a_voff[j], soff, st + (wave + NW * j) * 8 * kBK);
+    for (int j = 0; j < AJ; ++j)
+      ld(ra, a_voff[j], soff, st + (wave + NW * j) * 8 * kBK, std::integral_constant<int, kCpolDefault>{});
 #pragma unroll
-    for (int j = 0; j < BJ; ++j) ld(rb, b_voff[j], soffb, st + B_OFF + (wave + NW * j) * 8 * kBK);
+    for (int j = 0; j < BJ; ++j)
+      ld(rb, b_voff[j], soffb, st + B_OFF + (wave + NW * j) * 8 * kBK, std::integral_constant<int, BCPOL>{});
   }
 
   static __device__ __forceinline__ void zero(f32x16_t (&acc)[MI][NI]) {
