@@ -356,8 +356,9 @@ __global__ void __launch_bounds__(C::NW * 64)
       const uint32_t so = (uint32_t)kb * 128u + (FULL_M ? (uint32_t)q * a_rstep : 0u);
       buf_lds(ra, v, so, base + (wave + NW * q) * 1024, 16);
     } else if (q < AQ + BQ) {
-      buf_lds(rb, b_voff, (uint32_t)kb * 128u + (uint32_t)(q - AQ) * b_rstep,
-              base + C::A_BYTES + (wave + NW * (q - AQ)) * 1024, 16);
+      // grouped: expert weights, read by that expert's row blocks only -> non-temporal
+      buf_lds<GROUPED ? kCpolNT : kCpolDefault>(rb, b_voff, (uint32_t)kb * 128u + (uint32_t)(q - AQ) * b_rstep,
+                                                base + C::A_BYTES + (wave + NW * (q - AQ)) * 1024, 16);
     } else if constexpr (!ROW) {
       // scale load (wave-uniform selects): activation scales, or weight-scale copies
       const bool xload = (NW == 4 ? q == AQ + BQ : wave < 4) && (!XS4 || (kb & 3) == 0);

@@ -372,7 +372,9 @@ template <int MODE, int BM, int BN>
 __global__ void __launch_bounds__(256)
     moe_buf_kernel(const MoeGemmParams p) {
   constexpr int AP = (MODE == MOE_DOWN) ? 2 : 1;
-  using E = BufPipeEngine<BF16, BM, BN, 2, 2, AP>;
+  // grouped (plain) GEMM: an expert's weight tile is read by that expert's row blocks
+  // only, running side by side on one XCD (L2), so its loads are non-temporal
+  using E = BufPipeEngine<BF16, BM, BN, 2, 2, AP, B_KC, MODE == MOE_PLAIN ? kCpolNT : kCpolDefault>;
   constexpr int MI = E::MI, NI = E::NI;
   __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;

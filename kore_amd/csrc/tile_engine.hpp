@@ -364,7 +364,9 @@ __device__ __forceinline__ void nc_frag_offsets(int lane, int col0, int (&off)[N
     off[j] = (8 * hh + (c >> 2)) * BN + (((col0 / 8 + 4 * j + low) ^ x) << 3) + 4 * (c & 1);
 }
 
-template <typename T, int BM, int BN, int WM_ = 2, int WN_ = 2, int AP = 1, int BL = B_KC>
+// BCPOL: cache policy of the B (weight) loads -- non-temporal where each weight tile
+// is read by the row blocks of one expert only.
+template <typename T, int BM, int BN, int WM_ = 2, int WN_ = 2, int AP = 1, int BL = B_KC, int BCPOL = kCpolDefault>
 struct BufPipeEngine {
   static constexpr int WM = WM_, WN = WN_, NW = WM * WN;
   static_assert(NW == 4, "4 waves");
@@ -412,7 +414,8 @@ struct BufPipeEngine {
       ld(ra2, a_voff[j], soff, sA + A_ELEMS + (wave + NW * j) * 8 * kBK);
     } else {
       const int j = q - AP * AJ;
-      ld(rb, b_voff[j], soffb, sA + B_OFF + (wave + NW * j) * 8 * kBK);
+      if constexpr (NC) buf_lds16_asm<BCPOL>(rb, b_voff[j], soffb, sA + B_OFF + (wave + NW * j) * 8 * kBK);
+      else buf_lds16_cp<BCPOL>(rb, b_voff[j], soffb, sA + B_OFF + (wave + NW * j) * 8 * kBK);
     }
   }
 
