@@ -552,7 +552,7 @@ __global__ void __launch_bounds__(512) gemm_shortk_kernel(const TileParams p, co
       const int r = rowA0 + row, c = chunk * 8;
       const bool ok = r < rows_c && c < cols_c;  // N % 8 == 0: 8 columns wholly in or out
       const uint32_t voff = ok ? (uint32_t)((r * (int)p.ldc + c) * 2) : 0xfffffff0u;
-      __builtin_amdgcn_raw_buffer_store_b128(v, rc, voff, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(v, rc, voff, 0, 2);  // nt: C is written once
     }
   };
 
