@@ -51,7 +51,7 @@ constexpr int kGroupM = 4;
 
 // Bias + activation in fp32, RNE pack, per-wave LDS staging, 16-byte row stores.
 // Must be entered after a barrier that ends all reads of the K-loop buffers.
-template <typename T, int MI, int NI, int WROWS, int WCOLS>
+template <typename T, int MI, int NI, int WROWS, int WCOLS, bool M16 = false>
 __device__ __forceinline__ void dense_epilogue(f32x16_t (&acc)[MI][NI], uint16_t* lds, const TileParams& p, int m0,
                                                int n0, int wm, int wn, int wave, int lane, uint16_t* C) {
   using Op = MfmaOp<T>;
@@ -65,7 +65,7 @@ __device__ __forceinline__ void dense_epilogue(f32x16_t (&acc)[MI][NI], uint16_t
     for (int j = 0; j < NI; ++j) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int nl = out_col(j, g, lane);
+        const int nl = acc_col<M16>(j, g, lane);
         float bv[4] = {0.f, 0.f, 0.f, 0.f};
         if (p.bias != nullptr) {
           const int n = nw0 + nl;
@@ -85,7 +85,7 @@ __device__ __forceinline__ void dense_epilogue(f32x16_t (&acc)[MI][NI], uint16_t
           float v[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = apply_act<ACT>(acc[i][j][4 * g + e] + bv[e]);
-          St::put(stg, out_row(i, lane), nl, u32x2_t{Op::pack2(v[0], v[1]), Op::pack2(v[2], v[3])});
+          St::put(stg, acc_row<M16>(i, g, lane), nl, u32x2_t{Op::pack2(v[0], v[1]), Op::pack2(v[2], v[3])});
         }
       }
     }
@@ -201,7 +201,8 @@ __device__ __forceinline__ void setup_operands(E& eng, const TileParams& p, int 
 template <typename T, int BM, int BN, int BL>
 __global__ void __launch_bounds__(256)
     gemm_buf_kernel(const TileParams p) {
-  using E = BufPipeEngine<T, BM, BN, 2, 2, 1, BL>;
+  // K-contiguous B: 16x16x32 MFMAs (the N-contiguous transpose reads are laid out for 32x32)
+  using E = BufPipeEngine<T, BM, BN, 2, 2, 1, BL, kCpolDefault, BL == B_KC>;
   constexpr int MI = E::MI, NI = E::NI;
   __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -213,7 +214,7 @@ __global__ void __launch_bounds__(256)
   f32x16_t acc[MI][NI];
   E::zero(acc);
   eng.mainloop(lds, p.K, acc);
-  dense_epilogue<T, MI, NI, E::WROWS, E::WCOLS>(acc, lds, p, m0, n0, wm, wn, wave, lane, p.c + batch * p.sc);
+  dense_epilogue<T, MI, NI, E::WROWS, E::WCOLS, E::M16>(acc, lds, p, m0, n0, wm, wn, wave, lane, p.c + batch * p.sc);
 }
 
 // Mid-size problems (a few hundred tiles, long K) on the deep ring engine: NSLOT - 1

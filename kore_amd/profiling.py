@@ -421,6 +421,71 @@ def read_traffic(workload: str, path: str = TRAFFIC_FILE):
     return None
 
 
+def _vendor(iters: int, min_warm_s: float = 0.5) -> None:
+    """The vendor library (hipBLASLt through torch) on the shapes where it is the bar:
+    bf16 4096^3 A.B^T, bf16 8192x4096 . 4096x8192, fp32 512x4096x4096 + bias (addmm) and
+    fp8 e4m3 2048x7168x4096 with unit per-tensor scales (_scaled_mm).  Each op is warmed
+    up for ``min_warm_s`` seconds, then called ``iters`` times.  Timing only: the vendor
+    library is run, never read."""
+    import time
+
+    import torch
+
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(0)
+    rn = lambda *s: torch.randn(s, generator=g, device=dev)
+    a, b = rn(4096, 4096).bfloat16(), rn(4096, 4096).bfloat16()
+    a2, b2 = rn(8192, 4096).bfloat16(), rn(4096, 8192).bfloat16()
+    a3, b3, bias = rn(512, 4096), rn(4096, 4096), rn(4096)
+    x8, w8 = rn(2048, 4096).to(torch.float8_e4m3fn), rn(7168, 4096).to(torch.float8_e4m3fn)
+    one = torch.ones((), device=dev)
+    ops = [("bf16 4096^3 A.B^T", lambda: torch.matmul(a, b.t())),
+           ("bf16 8192x8192x4096", lambda: torch.matmul(a2, b2)),
+           ("fp32 512x4096x4096 + bias", lambda: torch.addmm(bias, a3, b3)),
+           ("fp8 2048x7168x4096 per-tensor",
+            lambda: torch._scaled_mm(x8, w8.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16))]
+    for name, fn in ops:
+        t0, w = time.perf_counter(), 0
+        while time.perf_counter() - t0 < min_warm_s:
+            fn()
+            w += 1
+            if w % 64 == 0:
+                torch.cuda.synchronize()
+        for _ in range(iters):
+            fn()
+        torch.cuda.synchronize()
+        print(f"profiling.vendor {name}: {w} warm-up + {iters} timed calls done", flush=True)
+
+
+def write_vendor(trace_dir: str, out: str, cmd: str, iters: int) -> None:
+    """Average duration of the last ``iters`` dispatches of every vendor GEMM kernel
+    (names containing ``Cijk``) in a rocprofv3 kernel trace."""
+    paths = glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True)
+    if not paths:
+        raise SystemExit(f"no kernel_trace.csv under {trace_dir}")
+    per: dict[str, list[tuple[int, int]]] = {}
+    with open(paths[0]) as f:
+        for r in csv.DictReader(f):
+            if "Cijk" in r["Kernel_Name"]:
+                per.setdefault(r["Kernel_Name"], []).append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    lines = ["# hipBLASLt kernels on the same box (the vendor bar; timed, never read)", "",
+             "Commands (from the repository root, on one MI355X):", "", "```", cmd, "```", "",
+             f"Average over the last {iters} dispatches of each kernel, after at least 0.5 s of warm-up",
+             "calls (back to back, warm cache).  This build on the same shapes: `bf16_gemm_4096.md`,",
+             "`fp8_blockscale_2048x7168x4096.md` (block scales, more work than per-tensor),",
+             "`fp32_gemm_bias_512x4096x4096.md`; cold task-driver medians in `driver_protocol.md`.", "",
+             "| first dispatch order | average (us) | min (us) | kernel (name as printed, truncated) |",
+             "|---|---|---|---|"]
+    order = sorted(per, key=lambda k: per[k][0][0])
+    for i, name in enumerate(order):
+        d = sorted(per[name])[-iters:]
+        durs = [(e - s_) / 1e3 for s_, e in d]
+        lines.append(f"| {i + 1} | {statistics.mean(durs):.1f} | {min(durs):.1f} | `{name[:150]}` |")
+    with open(out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print(f"wrote {out}")
+
+
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(prog="python -m kore_amd.profiling")
     sub = p.add_subparsers(dest="action", required=True)
@@ -457,6 +522,13 @@ def main(argv=None) -> int:
     m.add_argument("--out", default=PMC_FILE)
     m.add_argument("--cmd", required=True)
     m.add_argument("--note", default="")
+    vd = sub.add_parser("vendor", help="run the vendor library's GEMMs on the bar shapes")
+    vd.add_argument("--iters", type=int, default=20)
+    vs = sub.add_parser("vendor-stats")
+    vs.add_argument("dir")
+    vs.add_argument("--out", required=True)
+    vs.add_argument("--cmd", required=True)
+    vs.add_argument("--iters", type=int, default=20)
     sub.add_parser("grounding-passes", help="print the grounding counter groups, one pass per line")
     gr = sub.add_parser("grounding")
     gr.add_argument("dirs", nargs="+")
@@ -474,6 +546,10 @@ def main(argv=None) -> int:
         write_stats(a.dir, a.out, a.cmd, a.title, a.warmup_calls, a.iters)
     elif a.action == "pmc":
         write_pmc(a)
+    elif a.action == "vendor":
+        _vendor(a.iters)
+    elif a.action == "vendor-stats":
+        write_vendor(a.dir, a.out, a.cmd, a.iters)
     elif a.action == "grounding-passes":
         print("\n".join(" ".join(g) for g in GROUNDING_PASSES))
     elif a.action == "grounding":

@@ -156,3 +156,20 @@ def test_grounding_passes_and_derived():
     assert d["hbm_read_bytes"] == 32 * 4 + 64 * 6 and d["hbm_write_bytes"] == 64 * 5
     assert d["mfma_busy_fraction"] == 1.0 and d["mfma_busy_pct"] == 400.0
     assert d["mfma_flops"] == 1024.0 and d["mfma_ops"] == 514.0
+
+
+def test_vendor_stats_last_dispatches(tmp_path):
+    """The vendor summary averages the last `iters` dispatches of each vendor kernel and
+    ignores everything else (the warm-up calls, torch's own kernels)."""
+    rows, t = [], 0
+    for name, durs in [("Cijk_A_MT256", [900, 800, 100, 110]), ("Custom_Cijk_B", [50, 40, 30, 30]),
+                       ("at::native::fill", [5, 5])]:
+        for d in durs:
+            rows.append((name, t, d))
+            t += 1000
+    _trace(tmp_path / "v", rows)
+    out = tmp_path / "v.md"
+    P.write_vendor(str(tmp_path / "v"), str(out), "cmd", 2)
+    text = out.read_text()
+    assert "| 1 | 0.1 | 0.1 | `Cijk_A_MT256` |" in text and "| 2 | 0.0 | 0.0 | `Custom_Cijk_B` |" in text
+    assert "fill" not in text
