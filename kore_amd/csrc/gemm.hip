@@ -51,9 +51,11 @@ constexpr int kGroupM = 4;
 
 // Bias + activation in fp32, RNE pack, per-wave LDS staging, 16-byte row stores.
 // Must be entered after a barrier that ends all reads of the K-loop buffers.
-template <typename T, int MI, int NI, int WROWS, int WCOLS, bool M16 = false>
-__device__ __forceinline__ void dense_epilogue(f32x16_t (&acc)[MI][NI], uint16_t* lds, const TileParams& p, int m0,
-                                               int n0, int wm, int wn, int wave, int lane, uint16_t* C) {
+// get(i, j, g, e): element 4g + e of the lane's accumulator of 32x32 tile (i, j), whose
+// output position is (acc_row<M16>(i, g), acc_col<M16>(j, g) + e).
+template <typename T, int MI, int NI, int WROWS, int WCOLS, bool M16, typename Get>
+__device__ __forceinline__ void dense_epilogue_at(Get&& get, uint16_t* lds, const TileParams& p, int m0, int n0, int wm,
+                                                  int wn, int wave, int lane, uint16_t* C) {
   using Op = MfmaOp<T>;
   using St = Stager<WROWS, WCOLS>;
   const int M = p.M, N = p.N;
@@ -84,7 +86,7 @@ __device__ __forceinline__ void dense_epilogue(f32x16_t (&acc)[MI][NI], uint16_t
         for (int i = 0; i < MI; ++i) {
           float v[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = apply_act<ACT>(acc[i][j][4 * g + e] + bv[e]);
+          for (int e = 0; e < 4; ++e) v[e] = apply_act<ACT>(get(i, j, g, e) + bv[e]);
           St::put(stg, acc_row<M16>(i, g, lane), nl, u32x2_t{Op::pack2(v[0], v[1]), Op::pack2(v[2], v[3])});
         }
       }
@@ -104,6 +106,19 @@ __device__ __forceinline__ void dense_epilogue(f32x16_t (&acc)[MI][NI], uint16_t
     const int gm = mw0 + row, gn = nw0 + col;
     if (gm < M) store_row8(C + (int64_t)gm * p.ldc + gn, gn, N, vec, v);
   });
+}
+
+template <typename T, int MI, int NI, int WROWS, int WCOLS>
+__device__ __forceinline__ void dense_epilogue(f32x16_t (&acc)[MI][NI], uint16_t* lds, const TileParams& p, int m0,
+                                               int n0, int wm, int wn, int wave, int lane, uint16_t* C) {
+  dense_epilogue_at<T, MI, NI, WROWS, WCOLS, false>([&](int i, int j, int g, int e) { return acc[i][j][4 * g + e]; },
+                                                    lds, p, m0, n0, wm, wn, wave, lane, C);
+}
+template <typename T, int MI, int NI, int WROWS, int WCOLS>
+__device__ __forceinline__ void dense_epilogue16(f32x4_t (&c4)[MI][NI][4], uint16_t* lds, const TileParams& p, int m0,
+                                                 int n0, int wm, int wn, int wave, int lane, uint16_t* C) {
+  dense_epilogue_at<T, MI, NI, WROWS, WCOLS, true>([&](int i, int j, int g, int e) { return c4[i][j][g][e]; }, lds, p,
+                                                   m0, n0, wm, wn, wave, lane, C);
 }
 
 // Tile coordinates: XCD-aware remap, then grouped raster per batch.
@@ -211,10 +226,17 @@ __global__ void __launch_bounds__(256)
   tile_coords(p, BM, BN, batch, m0, n0);
   E eng;
   setup_operands<E, BM, BN, BL>(eng, p, batch, m0, n0, wave, lane);
-  f32x16_t acc[MI][NI];
-  E::zero(acc);
-  eng.mainloop(lds, p.K, acc);
-  dense_epilogue<T, MI, NI, E::WROWS, E::WCOLS, E::M16>(acc, lds, p, m0, n0, wm, wn, wave, lane, p.c + batch * p.sc);
+  if constexpr (E::M16) {
+    f32x4_t acc[MI][NI][4];
+    E::zero16(acc);
+    eng.mainloop16(lds, p.K, acc);
+    dense_epilogue16<T, MI, NI, E::WROWS, E::WCOLS>(acc, lds, p, m0, n0, wm, wn, wave, lane, p.c + batch * p.sc);
+  } else {
+    f32x16_t acc[MI][NI];
+    E::zero(acc);
+    eng.mainloop(lds, p.K, acc);
+    dense_epilogue<T, MI, NI, E::WROWS, E::WCOLS>(acc, lds, p, m0, n0, wm, wn, wave, lane, p.c + batch * p.sc);
+  }
 }
 
 // Mid-size problems (a few hundred tiles, long K) on the deep ring engine: NSLOT - 1

@@ -452,10 +452,7 @@ struct BufPipeEngine {
 
   // K must be a multiple of 64.
   __device__ __forceinline__ void mainloop(uint16_t* lds, int K, f32x16_t (&acc)[MI][NI]) {
-    if constexpr (M16) {
-      mainloop16(lds, K, acc);
-      return;
-    }
+    static_assert(!M16, "the 16x16 engine accumulates in f32x4_t[MI][NI][4] (mainloop16)");
     using Op = MfmaOp<T>;
     // wave index as a scalar so LDS destinations (M0) are pure scalar arithmetic
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -560,7 +557,18 @@ struct BufPipeEngine {
 
   // The same pipeline on 16x16x32 MFMAs: per 64-wide stage two sub-steps of K = 32.
   // Lane l reads row 16 * s + (l % 16) of a 32-row block, 16-byte chunk 4 * ks + l / 16.
-  __device__ __forceinline__ void mainloop16(uint16_t* lds, int K, f32x16_t (&acc)[MI][NI]) {
+  // The accumulators stay 4-register tuples from the caller to the epilogue (c4[i][j][g]:
+  // sub-tile g of 32x32 tile (i, j)); converting them to and from 16-register tiles made
+  // the register allocator copy every chain between AGPRs and VGPRs once per stage.
+  static __device__ __forceinline__ void zero16(f32x4_t (&c4)[MI][NI][4]) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) c4[i][j][g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  __device__ __forceinline__ void mainloop16(uint16_t* lds, int K, f32x4_t (&c4)[MI][NI][4]) {
     static_assert(!NC, "16x16 fragments are read from K-contiguous B tiles");
     using Op = MfmaOp<T>;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -592,14 +600,6 @@ struct BufPipeEngine {
     };
     const int nk = K / kBK;
     if (nk == 0) return;
-    f32x4_t c4[MI][NI][4];
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-      for (int j = 0; j < NI; ++j)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-          c4[i][j][g] = f32x4_t{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
     constexpr int HALF = LPS / 2;
     constexpr int NMMA = AP * MI * NI * 4;  // MFMAs per sub-step
     constexpr int NRD = NFA + NFB;          // fragment reads per sub-step
@@ -612,9 +612,14 @@ struct BufPipeEngine {
     for (int q = 0; q < HALF; ++q) issue_one(lds, 1, soff_of(1), soff_of(1), wave, q);
     wait_vmcnt<HALF>();
     exec_barrier();
-    u32x4_t fa[2][NFA], fb[2][NFB];
+    // A fragments are single-buffered: A block (pl, i, half sm) of the next sub-step is
+    // read right after its last MFMA in this one (tile j = NI - 1, sub-tile g = 2 sm + 1),
+    // at least (MI - 1) * NI * 4 MFMAs before its first use; B fragments are double-
+    // buffered and read over the first MFMAs.  This keeps 32 VGPRs free, which the
+    // register allocator otherwise finds by moving accumulators through AGPR copies.
+    u32x4_t fa[NFA], fb[2][NFB], fa_unused[NFA];
 #pragma unroll
-    for (int f = 0; f < NRD; ++f) read_one(0, 0, f, fa[0], fb[0]);
+    for (int f = 0; f < NRD; ++f) read_one(0, 0, f, fa, fb[0]);
     for (int s = 0; s < nk; ++s) {
       const int slot = s & 1;
       const uint32_t soff1 = soff_of(s + 1), soff2 = soff_of(s + 2);
@@ -634,8 +639,9 @@ struct BufPipeEngine {
           __builtin_amdgcn_sched_barrier(0);
           const int pl = m / (MI * NI * 4), i = (m / (NI * 4)) % MI, j = (m / 4) % NI, g = m & 3;
           const int sm = g >> 1, sn = g & 1;
-          c4[i][j][g] = Op::mma16(fb[c][j * 2 + sn], fa[c][(pl * MI + i) * 2 + sm], c4[i][j][g]);
-          if (m < NRD) read_one(rslot, rks, m, fa[c ^ 1], fb[c ^ 1]);
+          c4[i][j][g] = Op::mma16(fb[c][j * 2 + sn], fa[(pl * MI + i) * 2 + sm], c4[i][j][g]);
+          if (j == NI - 1 && (g & 1)) read_one(rslot, rks, (pl * MI + i) * 2 + sm, fa, fb[c ^ 1]);
+          if (m < NFB) read_one(rslot, rks, NFA + m, fa_unused, fb[c ^ 1]);
           if (m < HALF) {
             if (ks == 0) issue_one(lds, slot ^ 1, soff1, soff1, wave, HALF + m);  // 2nd half of s+1
             else issue_one(lds, slot, soff2, soff2, wave, m);                      // 1st half of s+2
@@ -646,14 +652,6 @@ struct BufPipeEngine {
     }
     wait_vmcnt<0>();  // drain the clamped trailing loads before LDS is reused
     __syncthreads();
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-      for (int j = 0; j < NI; ++j)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[i][j][4 * g + e] = c4[i][j][g][e];
   }
 };
 
