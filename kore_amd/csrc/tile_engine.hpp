@@ -390,7 +390,7 @@ template <typename T, int BM, int BN, int WM_ = 2, int WN_ = 2, int AP = 1, int 
 struct BufPipeEngine {
   static constexpr bool M16 = M16_;
   static constexpr int WM = WM_, WN = WN_, NW = WM * WN;
-  static_assert(NW == 4, "4 waves");
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
   static_assert(AP == 1 || AP == 2, "one or two A planes");
   static constexpr int WROWS = BM / WM, WCOLS = BN / WN;
   static constexpr int MI = WROWS / 32, NI = WCOLS / 32;
