@@ -213,16 +213,15 @@ __device__ __forceinline__ void setup_operands(E& eng, const TileParams& p, int 
 // Buffer-load pipelined variant for K-contiguous A, K % 64 == 0 and either B layout:
 // K-contiguous B (the A.B^T / A.W^T layouts) or N-contiguous B (natural [K, N], N % 8 ==
 // 0), whose fragments come out of LDS through transpose reads.
-// K-contiguous B: 16x16x32 MFMAs on 8 waves (2 x 4, 128 x 64 each, two per SIMD): same
-// process, bit-equal, 4096^3 bf16 102 -> 100 us and fp16 + gelu 113-115 -> 112 us against 4
-// waves of 128 x 128.  N-contiguous B keeps 4 waves on 32x32x16 (its transpose reads are laid
-// out for 32x32 fragments).
-template <int BL>
-constexpr int buf_waves() { return BL == B_KC ? 8 : 4; }
-template <typename T, int BM, int BN, int BL>
-__global__ void __launch_bounds__(64 * buf_waves<BL>())
+// NWV = 8: 16x16x32 MFMAs on 8 waves (2 x 4, 128 x 64 each, two per SIMD); same process,
+// bit-equal, 4096^3 bf16 102 -> 100 us and fp16 + gelu 113-115 -> 112 us against 4 waves of
+// 128 x 128 (K-contiguous B).  An N-contiguous B reaches the 16x16 fragments through transpose
+// reads with the nc_x16 chunk swizzle.  NWV = 4 (N-contiguous B over several rounds of the
+// CUs, see launch_buf): 4 waves of 128 x 128 on 32x32x16 with the nc_x swizzle.
+template <typename T, int BM, int BN, int BL, int NWV>
+__global__ void __launch_bounds__(64 * NWV)
     gemm_buf_kernel(const TileParams p) {
-  using E = BufPipeEngine<T, BM, BN, 2, buf_waves<BL>() / 2, 1, BL, kCpolDefault, BL == B_KC>;
+  using E = BufPipeEngine<T, BM, BN, 2, NWV / 2, 1, BL, kCpolDefault, NWV == 8 || BL == B_KC>;
   constexpr int MI = E::MI, NI = E::NI;
   __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1004,8 +1003,19 @@ int launch_buf(const GemmDesc& d, hipStream_t stream) {
   p.bias_vec = d.bias != nullptr && ((uintptr_t)d.bias & 7u) == 0;
   const int64_t blocks = (int64_t)p.tiles_per_batch * d.batch;
   if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "gemm: grid too large");
-  hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL>), dim3((unsigned)blocks), dim3(64 * buf_waves<BL>()), 0, stream,
-                     p);
+  // 8 waves on 16x16x32 MFMAs, except for an N-contiguous B whose grid needs more than one
+  // round of the CUs: there the 4-wave 32x32x16 tile measured 1-4% faster under the cold
+  // protocol (8192 x 4096 x 4096: 221 against 224-228 us; 8192 x 8192 x 4096: 427-429
+  // against 445 us), while 8 waves were 3-4% faster warm; on one round 8 waves win both
+  // (4096^3: cold 105-108 against 111 us, bit-equal).
+  if constexpr (BL == B_KC) {
+    hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 8>), dim3((unsigned)blocks), dim3(512), 0, stream, p);
+  } else {
+    if (blocks <= device_cus())
+      hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 8>), dim3((unsigned)blocks), dim3(512), 0, stream, p);
+    else
+      hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 4>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+  }
   return check_launch("gemm_buf_kernel");
 }
 

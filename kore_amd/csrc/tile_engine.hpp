@@ -362,6 +362,12 @@ __device__ __forceinline__ void buf_lds16_asm(__amdgpu_buffer_rsrc_t r, uint32_t
 // each) then sit in four distinct 32-byte bank slots of a 128-byte window, and with
 // the next 16 lanes' chunk pair (same K-rows) in eight distinct slots of 256 bytes.
 __device__ __forceinline__ int nc_x(int r) { return ((r & 1) * 4) ^ ((r >> 1) * 10); }
+// The 16x16x32 fragments (BufPipeEngine with M16) read K-rows k0 .. k0 + 3 in lanes 0-15
+// and k0 + 8 .. k0 + 11 in lanes 16-31 at the same columns, so K-rows with bit 3 set
+// move by two more chunks: the 32 lanes of one half-wave then cover 16 distinct
+// 16-byte slots of a 256-byte bank window ({0,1,4,5,10,11,14,15} and {2,3,6,7,8,9,12,13}
+// for an even first chunk).
+__device__ __forceinline__ int nc_x16(int r) { return nc_x(r & 3) ^ (((r >> 3) & 1) * 2); }
 
 // Element offsets (within a stage's B region, sub-step 0, low half) of the transpose
 // reads for the NI 32-column fragments of a wave whose columns start at col0: lane
@@ -415,7 +421,9 @@ struct BufPipeEngine {
   static constexpr int NCR = 512 / BN, NCH = BN / 8;
   static_assert(!NC || BN == 128 || BN == 256, "N-contiguous B tile width");
   static __device__ __forceinline__ int nc_krow(int wave, int lane, int j) { return (wave + NW * j) * NCR + lane / NCH; }
-  static __device__ __forceinline__ int nc_chunk(int krow, int lane) { return (lane % NCH) ^ nc_x(krow & 3); }
+  static __device__ __forceinline__ int nc_chunk(int krow, int lane) {
+    return (lane % NCH) ^ (M16 ? nc_x16(krow) : nc_x(krow & 3));
+  }
 
   __amdgpu_buffer_rsrc_t ra, ra2, rb;  // ra2: second A plane (same offsets), AP == 2
   uint32_t a_voff[AJ], b_voff[BJ];      // bytes: row * row_stride + 16 * chunk
@@ -569,7 +577,6 @@ struct BufPipeEngine {
         for (int g = 0; g < 4; ++g) c4[i][j][g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
   __device__ __forceinline__ void mainloop16(uint16_t* lds, int K, f32x4_t (&c4)[MI][NI][4]) {
-    static_assert(!NC, "16x16 fragments are read from K-contiguous B tiles");
     using Op = MfmaOp<T>;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
@@ -588,6 +595,20 @@ struct BufPipeEngine {
           offB[par][h][ks] = (16 * h + r16) * kBK + (((4 * ks + g4) ^ swz8(rb)) << 3);
         }
     constexpr int NFA = AP * MI * 2, NFB = NI * 2;
+    // N-contiguous B: fragment q = 2 j + h (columns rowB0 + 32 j + 16 h .. + 15) of lane
+    // 16 g + c comes from two transpose reads; lane c points at K-row 8 g + c / 4 (+ 4 for
+    // the second read, + 32 per sub-step), columns + 4 (c % 4) .. + 3, and lane c then
+    // holds column + c at those four K-rows.  Element offsets of sub-step 0, first read.
+    int offNC[NC ? NFB : 1];
+    if constexpr (NC) {
+      const int c = lane & 15, g = lane >> 4;
+      const int x = nc_x16(8 * g + (c >> 2));
+#pragma unroll
+      for (int q = 0; q < NFB; ++q) {
+        const int ch = (rowB0 + 32 * (q / 2) + 16 * (q & 1)) / 8 + ((c & 3) >> 1);
+        offNC[q] = (8 * g + (c >> 2)) * BN + ((ch ^ x) << 3) + 4 * (c & 1);
+      }
+    }
     // fragment f of a sub-step: f < NFA -> A plane, block, half; else B block, half
     auto read_one = [&](int slot, int ks, int f, u32x4_t (&af)[NFA], u32x4_t (&bf)[NFB]) {
       if (f < NFA) {
@@ -595,7 +616,13 @@ struct BufPipeEngine {
         af[f] = *(const u32x4_t*)(lds + slot * STAGE + pl * A_ELEMS + (rowA0 + 32 * i) * kBK + offA[i & 1][h][ks]);
       } else {
         const int q = f - NFA, j = q / 2, h = q & 1;
-        bf[q] = *(const u32x4_t*)(lds + slot * STAGE + B_OFF + (rowB0 + 32 * j) * kBK + offB[j & 1][h][ks]);
+        if constexpr (NC) {
+          const uint16_t* src = lds + slot * STAGE + B_OFF + offNC[q] + 32 * ks * BN;
+          const u32x2_t lo = lds_read_tr16(src), hi = lds_read_tr16(src + 4 * BN);
+          bf[q] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+        } else {
+          bf[q] = *(const u32x4_t*)(lds + slot * STAGE + B_OFF + (rowB0 + 32 * j) * kBK + offB[j & 1][h][ks]);
+        }
       }
     };
     const int nk = K / kBK;
@@ -606,10 +633,11 @@ struct BufPipeEngine {
     static_assert(NRD <= NMMA && HALF <= NMMA, "interleave needs enough MFMAs");
     const uint32_t kmax = (uint32_t)(nk - 1) * (kBK * 2);
     auto soff_of = [&](int stage) { return min((uint32_t)stage * (kBK * 2), kmax); };
+    auto soffb_of = [&](int stage) { return NC ? (uint32_t)min(stage, nk - 1) * b_kstep : soff_of(stage); };
 #pragma unroll
     for (int q = 0; q < LPS; ++q) issue_one(lds, 0, 0u, 0u, wave, q);
 #pragma unroll
-    for (int q = 0; q < HALF; ++q) issue_one(lds, 1, soff_of(1), soff_of(1), wave, q);
+    for (int q = 0; q < HALF; ++q) issue_one(lds, 1, soff_of(1), soffb_of(1), wave, q);
     wait_vmcnt<HALF>();
     exec_barrier();
     // A fragments are single-buffered: A block (pl, i, half sm) of the next sub-step is
@@ -623,6 +651,7 @@ struct BufPipeEngine {
     for (int s = 0; s < nk; ++s) {
       const int slot = s & 1;
       const uint32_t soff1 = soff_of(s + 1), soff2 = soff_of(s + 2);
+      const uint32_t soffb1 = soffb_of(s + 1), soffb2 = soffb_of(s + 2);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const int c = ks;
@@ -643,8 +672,8 @@ struct BufPipeEngine {
           if (j == NI - 1 && (g & 1)) read_one(rslot, rks, (pl * MI + i) * 2 + sm, fa, fb[c ^ 1]);
           if (m < NFB) read_one(rslot, rks, NFA + m, fa_unused, fb[c ^ 1]);
           if (m < HALF) {
-            if (ks == 0) issue_one(lds, slot ^ 1, soff1, soff1, wave, HALF + m);  // 2nd half of s+1
-            else issue_one(lds, slot, soff2, soff2, wave, m);                      // 1st half of s+2
+            if (ks == 0) issue_one(lds, slot ^ 1, soff1, soffb1, wave, HALF + m);  // 2nd half of s+1
+            else issue_one(lds, slot, soff2, soffb2, wave, m);                      // 1st half of s+2
           }
         }
         __builtin_amdgcn_sched_barrier(0);
