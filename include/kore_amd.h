@@ -130,10 +130,11 @@ int kore_batched_gemm(int dtype,
 /*
  * GEMM backward of the linear layer Y = X @ W^T (X [M,K], W [N,K], dY [M,N]):
  *   dX [M,K] = dY @ W,   dW [N,K] = dY^T @ X,   fp32 accumulate, `dtype` out (bf16/fp16).
- *   Row strides ldx, ldw, lddy, lddx, lddw (unit stride along rows).  dY^T is formed
- *   in `workspace` (the A operand of dW must be K-contiguous), followed by the two
- *   GEMMs' own scratch; it must hold kore_gemm_backward_workspace_bytes(<same args>)
- *   bytes.  W and X are read in place.
+ *   Row strides ldx, ldw, lddy, lddx, lddw (unit stride along rows).  dY, W and X are
+ *   read in place (dY^T as a transposed view); `workspace` holds the two GEMMs' own
+ *   scratch (operands packed when a grid is too small for the in-place engine), at
+ *   least kore_gemm_backward_workspace_bytes(<same args>) bytes; may be NULL when that
+ *   is 0.
  * Replaces: gemm_backward(x, w, dy) -> (dx, dw)
  *           kore/tasks/gemm_backward_bf16/seed_triton.py:74-86 (ENTRY reference.py:22,
  *           oracle reference.py:64-72)

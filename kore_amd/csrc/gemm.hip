@@ -182,13 +182,26 @@ __global__ void __launch_bounds__(kEngineThreads)
 template <typename E, int BM, int BN, int BL>
 __device__ __forceinline__ void setup_operands(E& eng, const TileParams& p, int batch, int m0, int n0, int wave,
                                                int lane) {
-  const uint16_t* A = p.a + batch * p.sa + (int64_t)m0 * p.lda;
   const int rows_a = min(BM, p.M - m0), rows_b = min(BN, p.N - n0);
-  eng.ra = make_rsrc(A, (uint32_t)(((int64_t)(rows_a - 1) * p.lda + p.K) * 2));
+  if constexpr (E::AMC) {
+    // M-contiguous A (element (m, k) at a[k * lda + m], M % 8 == 0): K-rows of the tile's
+    // BM columns; chunks past M re-read the last one (their rows are never stored)
+    const uint16_t* A = p.a + batch * p.sa + m0;
+    eng.ra = make_rsrc(A, (uint32_t)(((int64_t)(p.K - 1) * p.lda + rows_a) * 2));
+    eng.a_kstep = (uint32_t)(kBK * p.lda * 2);
 #pragma unroll
-  for (int j = 0; j < E::AJ; ++j) {
-    const int r = E::a_row(wave, lane, j);
-    eng.a_voff[j] = (uint32_t)(((int64_t)min(r, rows_a - 1) * p.lda + 8 * E::chunk(r, lane)) * 2);
+    for (int j = 0; j < E::AJ; ++j) {
+      const int kr = E::amc_krow(wave, lane, j);
+      eng.a_voff[j] = (uint32_t)(((int64_t)kr * p.lda + min(8 * E::amc_chunk(kr, lane), rows_a - 8)) * 2);
+    }
+  } else {
+    const uint16_t* A = p.a + batch * p.sa + (int64_t)m0 * p.lda;
+    eng.ra = make_rsrc(A, (uint32_t)(((int64_t)(rows_a - 1) * p.lda + p.K) * 2));
+#pragma unroll
+    for (int j = 0; j < E::AJ; ++j) {
+      const int r = E::a_row(wave, lane, j);
+      eng.a_voff[j] = (uint32_t)(((int64_t)min(r, rows_a - 1) * p.lda + 8 * E::chunk(r, lane)) * 2);
+    }
   }
   if constexpr (BL == B_KC) {
     const uint16_t* B = p.b + batch * p.sb + (int64_t)n0 * p.ldb;
@@ -217,11 +230,12 @@ __device__ __forceinline__ void setup_operands(E& eng, const TileParams& p, int 
 // bit-equal, 4096^3 bf16 102 -> 100 us and fp16 + gelu 113-115 -> 112 us against 4 waves of
 // 128 x 128 (K-contiguous B).  An N-contiguous B reaches the 16x16 fragments through transpose
 // reads with the nc_x16 chunk swizzle.  NWV = 4 (N-contiguous B over several rounds of the
-// CUs, see launch_buf): 4 waves of 128 x 128 on 32x32x16 with the nc_x swizzle.
-template <typename T, int BM, int BN, int BL, int NWV>
+// CUs, see launch_buf): 4 waves of 128 x 128 on 32x32x16 with the nc_x swizzle.  AL = A_MC: A
+// is M-contiguous (a transposed view) and read like an N-contiguous B (8 waves only).
+template <typename T, int BM, int BN, int BL, int NWV, int AL>
 __global__ void __launch_bounds__(64 * NWV)
     gemm_buf_kernel(const TileParams p) {
-  using E = BufPipeEngine<T, BM, BN, 2, NWV / 2, 1, BL, kCpolDefault, NWV == 8 || BL == B_KC>;
+  using E = BufPipeEngine<T, BM, BN, 2, NWV / 2, 1, BL, kCpolDefault, NWV == 8 || BL == B_KC, AL>;
   constexpr int MI = E::MI, NI = E::NI;
   __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -801,56 +815,6 @@ __global__ void __launch_bounds__(256) gemm_generic_mfma_kernel(const GenericPar
 }
 
 // ---------------------------------------------------------------------------------
-// 16-bit transpose out[c][r] = in[r][c] (the dY^T operand of the weight gradient):
-// 64x64 tiles through LDS, 16-byte row loads, 16-byte row stores of 8 gathered values.
-// The LDS row stride is 66 elements, so a column gather (8 consecutive rows) falls on
-// distinct banks.  HBM-bound: R*C*2 bytes read and written once.
-// ---------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) transpose16_kernel(const uint16_t* in, int64_t ldi, uint16_t* out, int64_t ldo,
-                                                          int R, int C) {
-  __shared__ uint16_t t[64][66];
-  const int tid = threadIdx.x;
-  const int r0 = (int)blockIdx.y * 64, c0 = (int)blockIdx.x * 64;
-  const bool vin = (ldi % 8 == 0) && (((uintptr_t)in & 15u) == 0) && (C % 8 == 0);
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int idx = tid + 256 * q, r = idx >> 3, ch = idx & 7;
-    const int gr = r0 + r, gc = c0 + 8 * ch;
-    uint16_t v[8];
-    if (vin && gr < R && gc + 8 <= C) {
-      const u32x4_t w = *(const u32x4_t*)(in + (int64_t)gr * ldi + gc);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (gr < R && gc + e < C) ? in[(int64_t)gr * ldi + gc + e] : (uint16_t)0;
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) t[r][8 * ch + e] = v[e];
-  }
-  __syncthreads();
-  const bool vout = (ldo % 8 == 0) && (((uintptr_t)out & 15u) == 0) && (R % 8 == 0);
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int idx = tid + 256 * q, c = idx >> 3, ch = idx & 7;  // output row c, its rows 8ch..
-    const int gc = c0 + c, gr = r0 + 8 * ch;
-    if (gc >= C) continue;
-    uint16_t v[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = t[8 * ch + e][c];
-    if (vout && gr + 8 <= R) {
-      *(u32x4_t*)(out + (int64_t)gc * ldo + gr) =
-          u32x4_t{v[0] | ((uint32_t)v[1] << 16), v[2] | ((uint32_t)v[3] << 16), v[4] | ((uint32_t)v[5] << 16),
-                  v[6] | ((uint32_t)v[7] << 16)};
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (gr + e < R) out[(int64_t)gc * ldo + gr + e] = v[e];
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------------
 // Operand packing for transposed or strided layouts the direct-to-LDS engines cannot
 // read in place (K-contiguous rows that are only misaligned go to repitch16_kernel):
 // out[b][r][k] = in[b * sbat + r * sr + k * sk] for k < K and 0 for K <= k < Kp, with
@@ -866,13 +830,33 @@ __global__ void __launch_bounds__(256) pack16_kernel(const uint16_t* in, int64_t
   const uint16_t* src = in + (int64_t)blockIdx.z * sbat;
   uint16_t* dst = out + (int64_t)blockIdx.z * obat;
   const bool r_unit = sr == 1 && sk != 1;
-  // each wave instruction reads 64 consecutive elements along the unit-stride index
+  if (r_unit && sk % 8 == 0 && ((uintptr_t)src & 15u) == 0) {
+    // R-contiguous with 16-byte aligned K-rows (a transposed view): 8 rows per 16-byte load
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int u = tid & 63, v = 4 * i + (tid >> 6);
-    const int r = r_unit ? u : v, k = r_unit ? v : u;
-    const int gr = r0 + r, gk = k0 + k;
-    t[r][k] = (gr < R && gk < K) ? src[(int64_t)gr * sr + (int64_t)gk * sk] : (uint16_t)0;
+    for (int q = 0; q < 2; ++q) {
+      const int idx = tid + 256 * q, k = idx >> 3, ch = idx & 7;
+      const int gk = k0 + k, gr = r0 + 8 * ch;
+      uint16_t v[8];
+      if (gk < K && gr + 8 <= R) {
+        const u32x4_t w = *(const u32x4_t*)(src + (int64_t)gk * sk + gr);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (gk < K && gr + e < R) ? src[(int64_t)gk * sk + gr + e] : (uint16_t)0;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t[8 * ch + e][k] = v[e];
+    }
+  } else {
+    // each wave instruction reads 64 consecutive elements along the unit-stride index
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int u = tid & 63, v = 4 * i + (tid >> 6);
+      const int r = r_unit ? u : v, k = r_unit ? v : u;
+      const int gr = r0 + r, gk = k0 + k;
+      t[r][k] = (gr < R && gk < K) ? src[(int64_t)gr * sr + (int64_t)gk * sk] : (uint16_t)0;
+    }
   }
   __syncthreads();
 #pragma unroll
@@ -977,7 +961,7 @@ int launch_tile(const GemmDesc& d, hipStream_t stream) {
 }
 
 
-template <typename T, int BM, int BN, int BL>
+template <typename T, int BM, int BN, int BL, int AL = A_KC>
 int launch_buf(const GemmDesc& d, hipStream_t stream) {
   TileParams p;
   p.a = (const uint16_t*)d.a;
@@ -988,7 +972,7 @@ int launch_buf(const GemmDesc& d, hipStream_t stream) {
   p.N = (int)d.N;
   p.K = (int)d.K;
   p.kb = (int)(d.kvalid > 0 ? d.kvalid : d.K);
-  p.lda = d.sam;
+  p.lda = AL == A_MC ? d.sak : d.sam;
   p.ldb = (BL == B_KC) ? d.sbn : d.sbk;
   p.ldc = d.scm;
   p.sa = d.sa;
@@ -1003,18 +987,22 @@ int launch_buf(const GemmDesc& d, hipStream_t stream) {
   p.bias_vec = d.bias != nullptr && ((uintptr_t)d.bias & 7u) == 0;
   const int64_t blocks = (int64_t)p.tiles_per_batch * d.batch;
   if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "gemm: grid too large");
+  if constexpr (AL == A_MC) {
+    hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 8, A_MC>), dim3((unsigned)blocks), dim3(512), 0, stream, p);
+    return check_launch("gemm_buf_kernel");
+  }
   // 8 waves on 16x16x32 MFMAs, except for an N-contiguous B whose grid needs more than one
   // round of the CUs: there the 4-wave 32x32x16 tile measured 1-4% faster under the cold
   // protocol (8192 x 4096 x 4096: 221 against 224-228 us; 8192 x 8192 x 4096: 427-429
   // against 445 us), while 8 waves were 3-4% faster warm; on one round 8 waves win both
   // (4096^3: cold 105-108 against 111 us, bit-equal).
   if constexpr (BL == B_KC) {
-    hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 8>), dim3((unsigned)blocks), dim3(512), 0, stream, p);
+    hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 8, A_KC>), dim3((unsigned)blocks), dim3(512), 0, stream, p);
   } else {
     if (blocks <= device_cus())
-      hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 8>), dim3((unsigned)blocks), dim3(512), 0, stream, p);
+      hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 8, A_KC>), dim3((unsigned)blocks), dim3(512), 0, stream, p);
     else
-      hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 4>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 4, A_KC>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
   }
   return check_launch("gemm_buf_kernel");
 }
@@ -1303,6 +1291,15 @@ int dispatch_typed(const GemmDesc& d, Ws& ws, hipStream_t stream) {
   const bool b_kc = d.sbk == 1 && d.sbn % 8 == 0 && aligned16(d.b) && d.sb % 8 == 0;
   const bool b_nc = d.sbn == 1 && d.sbk % 8 == 0 && aligned16(d.b) && d.sb % 8 == 0 && d.N % 8 == 0;
   const bool fits32 = d.M < (1ll << 31) && d.N < (1ll << 31) && d.K < (1ll << 31);
+  // M-contiguous A (a transposed view, e.g. dY^T of the backward) on the 256x256 buffer
+  // engine, read in place through LDS transpose reads; smaller grids pack A instead.
+  const bool a_mc = d.sam == 1 && d.sak % 8 == 0 && aligned16(d.a) && d.sa % 8 == 0 && d.M % 8 == 0 &&
+                    d.K % 64 == 0 && d.K > 256 && d.sak * 2 * d.K + 512 < (1ll << 31);
+  if (a_mc && fits32 && pick_tile(d) == TILE_256x256 &&
+      ((b_kc && d.sbn * 2 * 256 + d.K * 2 < (1ll << 31)) || (b_nc && d.sbk * 2 * d.K + d.N * 2 < (1ll << 31)))) {
+    if (ws.plan) return KORE_OK;
+    return b_kc ? launch_buf<T, 256, 256, B_KC, A_MC>(d, stream) : launch_buf<T, 256, 256, B_NC, A_MC>(d, stream);
+  }
   if (a_ok && (b_kc || b_nc) && fits32) {
     // Macro tile: 256x256 when it still gives >= ~1 wave of tiles, else 128x128.
     const int64_t big_tiles = ((d.M + 255) / 256) * ((d.N + 255) / 256) * d.batch;
@@ -1439,24 +1436,23 @@ extern "C" int kore_batched_gemm(int dtype, const void* a, int64_t sa_b, int64_t
 // must be K-contiguous, so dY^T [N,M] is formed in the caller's workspace by one
 // HBM-bound transpose.
 namespace kore {
-inline int64_t bwd_ld(int64_t n) { return (n + 7) / 8 * 8; }  // 16-byte transposed rows
-inline size_t bwd_part(int64_t rows, int64_t cols) { return (size_t)(rows * bwd_ld(cols) * 2 + 255) / 256 * 256; }
 }  // namespace kore
 
 namespace kore {
 namespace {
-// The two GEMMs of the backward; dyt is the dY^T copy in the workspace.
+// The two GEMMs of the backward.
 GemmDesc bwd_dx(int dtype, const void* w, int64_t ldw, const void* dy, int64_t lddy, void* dx, int64_t lddx,
                 int64_t M, int64_t N, int64_t K) {
   // dX[M,K] = dY[M,N] @ W[N,K]: W read in place as an N-contiguous B (element (n, k) at
   // w[n*ldw + k]); the engines stage it through LDS transpose reads
   return GemmDesc{dtype, KORE_ACT_NONE, dy, w, nullptr, dx, M, K, N, 1, lddy, 1, ldw, 1, lddx, 0, 0, 0};
 }
-GemmDesc bwd_dw(int dtype, const void* x, int64_t ldx, const void* dyt, void* dw, int64_t lddw, int64_t M,
-                int64_t N, int64_t K) {
-  // dW[N,K] = dY^T[N,M] @ X[M,K]: X read in place as an N-contiguous B (element (m, k)
-  // at x[m*ldx + k])
-  return GemmDesc{dtype, KORE_ACT_NONE, dyt, x, nullptr, dw, N, K, M, 1, bwd_ld(M), 1, ldx, 1, lddw, 0, 0, 0};
+GemmDesc bwd_dw(int dtype, const void* x, int64_t ldx, const void* dy, int64_t lddy, void* dw, int64_t lddw,
+                int64_t M, int64_t N, int64_t K) {
+  // dW[N,K] = dY^T[N,M] @ X[M,K]: dY^T is the transposed view of dY (element (n, m) at
+  // dy[m*lddy + n], an M-contiguous A) and X an N-contiguous B (element (m, k) at
+  // x[m*ldx + k]), both read in place by the buffer engine or packed by the dispatch
+  return GemmDesc{dtype, KORE_ACT_NONE, dy, x, nullptr, dw, N, K, M, 1, 1, lddy, ldx, 1, lddw, 0, 0, 0};
 }
 int bwd_check(int dtype, const void* x, int64_t ldx, const void* w, int64_t ldw, const void* dy, int64_t lddy,
               const void* dx, int64_t lddx, const void* dw, int64_t lddw, int64_t M, int64_t N, int64_t K) {
@@ -1473,8 +1469,8 @@ int bwd_check(int dtype, const void* x, int64_t ldx, const void* w, int64_t ldw,
 }  // namespace
 }  // namespace kore
 
-// Workspace: dY^T [N, bwd_ld(M)] at a 256-byte aligned start, then the scratch of the
-// two GEMMs (they run one after the other, so they share it).
+// Workspace: the scratch of the two GEMMs (they run one after the other, so they share
+// it); none when both run on the buffer engine in place.
 extern "C" size_t kore_gemm_backward_workspace_bytes(int dtype, const void* x, int64_t ldx, const void* w,
                                                      int64_t ldw, const void* dy, int64_t lddy, const void* dx,
                                                      int64_t lddx, const void* dw, int64_t lddw, int64_t M,
@@ -1484,9 +1480,9 @@ extern "C" size_t kore_gemm_backward_workspace_bytes(int dtype, const void* x, i
   Ws ws;
   ws.plan = true;
   GemmDesc gx = bwd_dx(dtype, w, ldw, dy, lddy, (void*)dx, lddx, M, N, K);
-  GemmDesc gw = bwd_dw(dtype, x, ldx, (const void*)(uintptr_t)256, (void*)dw, lddw, M, N, K);
+  GemmDesc gw = bwd_dw(dtype, x, ldx, dy, lddy, (void*)dw, lddw, M, N, K);
   if (run_gemm(gx, ws, nullptr) != KORE_OK || run_gemm(gw, ws, nullptr) != KORE_OK) return 0;
-  return 256 + bwd_part(N, M) + ws_bytes(ws.need);
+  return ws_bytes(ws.need);
 }
 
 extern "C" int kore_gemm_backward(int dtype, const void* x, int64_t ldx, const void* w, int64_t ldw, const void* dy,
@@ -1496,24 +1492,17 @@ extern "C" int kore_gemm_backward(int dtype, const void* x, int64_t ldx, const v
   int rc = bwd_check(dtype, x, ldx, w, ldw, dy, lddy, dx, lddx, dw, lddw, M, N, K);
   if (rc != KORE_OK) return rc;
   const size_t need = kore_gemm_backward_workspace_bytes(dtype, x, ldx, w, ldw, dy, lddy, dx, lddx, dw, lddw, M, N, K);
-  if (!workspace || workspace_bytes < need)
+  if (need > 0 && (!workspace || workspace_bytes < need))
     return set_error(KORE_EWORKSPACE, "gemm_backward: needs %zu workspace bytes (got %zu)", need,
                      workspace ? workspace_bytes : (size_t)0);
   hipStream_t st = (hipStream_t)stream;
-  uint8_t* base = (uint8_t*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
-  uint16_t* dyt = (uint16_t*)base;  // dY^T [N, M]
-  Ws ws;  // the GEMMs' scratch follows dY^T
-  ws.ptr = base + bwd_part(N, M);
-  ws.bytes = workspace_bytes - (size_t)(base - (uint8_t*)workspace) - bwd_part(N, M);
+  Ws ws;  // the two GEMMs run one after the other and share the scratch
+  ws.ptr = workspace;
+  ws.bytes = workspace_bytes;
   GemmDesc gx = bwd_dx(dtype, w, ldw, dy, lddy, dx, lddx, M, N, K);
   rc = run_gemm(gx, ws, st);
   if (rc != KORE_OK) return rc;
-  // dY^T: A of dW must be K-contiguous
-  hipLaunchKernelGGL(transpose16_kernel, dim3((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64)), dim3(256), 0, st,
-                     (const uint16_t*)dy, lddy, dyt, bwd_ld(M), (int)M, (int)N);
-  rc = check_launch("transpose16_kernel");
-  if (rc != KORE_OK) return rc;
-  GemmDesc gw = bwd_dw(dtype, x, ldx, dyt, dw, lddw, M, N, K);
+  GemmDesc gw = bwd_dw(dtype, x, ldx, dy, lddy, dw, lddw, M, N, K);
   return run_gemm(gw, ws, st);
 }
 

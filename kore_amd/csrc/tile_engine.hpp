@@ -37,6 +37,9 @@ __device__ __forceinline__ void transpose8x8(const u32x4_t in[8], u32x4_t out[8]
 }
 
 enum { B_KC = 0, B_NC = 1 };
+// A layouts of the direct-to-LDS engines: K-contiguous rows, or M-contiguous (a transposed
+// view, element (m, k) at a[k * lda + m]) staged as K-rows and read back transposed.
+enum { A_KC = 0, A_MC = 1 };
 
 template <typename T, int BM, int BN, int WM, int WN, int BL, int AP = 1>
 struct TileEngine {
@@ -391,10 +394,19 @@ __device__ __forceinline__ void nc_frag_offsets(int lane, int col0, int (&off)[N
 // all CUs: 1.63-1.87 against 1.36-1.43 PF on random operands).  The accumulator of a
 // 32x32 tile then holds sub-tile g = 2 * sm + sn in elements 4g .. 4g + 3
 // (acc_row / acc_col<true>).
+// AL == A_MC: A staged like an N-contiguous B (64 K-rows of BM elements, nc_x16 chunk
+// swizzle) and read through transpose reads; 16x16 engine, one A plane.
 template <typename T, int BM, int BN, int WM_ = 2, int WN_ = 2, int AP = 1, int BL = B_KC, int BCPOL = kCpolDefault,
-          bool M16_ = false>
+          bool M16_ = false, int AL = A_KC>
 struct BufPipeEngine {
   static constexpr bool M16 = M16_;
+  static constexpr bool AMC = AL == A_MC;
+  static_assert(!AMC || (M16_ && AP == 1 && (BM == 128 || BM == 256)), "M-contiguous A: 16x16 engine, one plane");
+  static constexpr int NCRA = 512 / BM, NCHA = BM / 8;  // A_MC: K-rows per load, chunks per K-row
+  static __device__ __forceinline__ int amc_krow(int wave, int lane, int j) {
+    return (wave + WM_ * WN_ * j) * NCRA + lane / NCHA;
+  }
+  static __device__ __forceinline__ int amc_chunk(int krow, int lane) { return (lane % NCHA) ^ nc_x16(krow); }
   static constexpr int WM = WM_, WN = WN_, NW = WM * WN;
   static_assert(NW == 4 || NW == 8, "4 or 8 waves");
   static_assert(AP == 1 || AP == 2, "one or two A planes");
@@ -428,6 +440,7 @@ struct BufPipeEngine {
   __amdgpu_buffer_rsrc_t ra, ra2, rb;  // ra2: second A plane (same offsets), AP == 2
   uint32_t a_voff[AJ], b_voff[BJ];      // bytes: row * row_stride + 16 * chunk
   uint32_t b_kstep;                     // NC: bytes of B between consecutive 64-row K stages
+  uint32_t a_kstep;                     // A_MC: bytes of A between consecutive 64-row K stages
 
   __device__ __forceinline__ void issue_one(uint16_t* lds, int slot, uint32_t soff, uint32_t soffb, int wave,
                                             int q) {
@@ -437,7 +450,8 @@ struct BufPipeEngine {
       else buf_lds16(r, voff, so, dst);
     };
     if (q < AJ) {
-      ld(ra, a_voff[q], soff, sA + (wave + NW * q) * 8 * kBK);
+      if constexpr (AMC) buf_lds16_asm(ra, a_voff[q], soff, sA + (wave + NW * q) * 8 * kBK);
+      else ld(ra, a_voff[q], soff, sA + (wave + NW * q) * 8 * kBK);
     } else if (AP == 2 && q < 2 * AJ) {
       const int j = q - AJ;
       ld(ra2, a_voff[j], soff, sA + A_ELEMS + (wave + NW * j) * 8 * kBK);
@@ -599,6 +613,18 @@ struct BufPipeEngine {
     // 16 g + c comes from two transpose reads; lane c points at K-row 8 g + c / 4 (+ 4 for
     // the second read, + 32 per sub-step), columns + 4 (c % 4) .. + 3, and lane c then
     // holds column + c at those four K-rows.  Element offsets of sub-step 0, first read.
+    // M-contiguous A: the same transpose reads over A's K-rows, fragment f = 2 i + h at
+    // rows rowA0 + 32 i + 16 h .. + 15
+    int offMC[AMC ? NFA : 1];
+    if constexpr (AMC) {
+      const int c = lane & 15, g = lane >> 4;
+      const int x = nc_x16(8 * g + (c >> 2));
+#pragma unroll
+      for (int f = 0; f < NFA; ++f) {
+        const int ch = (rowA0 + 32 * (f / 2) + 16 * (f & 1)) / 8 + ((c & 3) >> 1);
+        offMC[f] = (8 * g + (c >> 2)) * BM + ((ch ^ x) << 3) + 4 * (c & 1);
+      }
+    }
     int offNC[NC ? NFB : 1];
     if constexpr (NC) {
       const int c = lane & 15, g = lane >> 4;
@@ -613,7 +639,13 @@ struct BufPipeEngine {
     auto read_one = [&](int slot, int ks, int f, u32x4_t (&af)[NFA], u32x4_t (&bf)[NFB]) {
       if (f < NFA) {
         const int pl = f / (MI * 2), i = (f / 2) % MI, h = f & 1;
-        af[f] = *(const u32x4_t*)(lds + slot * STAGE + pl * A_ELEMS + (rowA0 + 32 * i) * kBK + offA[i & 1][h][ks]);
+        if constexpr (AMC) {
+          const uint16_t* src = lds + slot * STAGE + offMC[f] + 32 * ks * BM;
+          const u32x2_t lo = lds_read_tr16(src), hi = lds_read_tr16(src + 4 * BM);
+          af[f] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+        } else {
+          af[f] = *(const u32x4_t*)(lds + slot * STAGE + pl * A_ELEMS + (rowA0 + 32 * i) * kBK + offA[i & 1][h][ks]);
+        }
       } else {
         const int q = f - NFA, j = q / 2, h = q & 1;
         if constexpr (NC) {
@@ -634,10 +666,11 @@ struct BufPipeEngine {
     const uint32_t kmax = (uint32_t)(nk - 1) * (kBK * 2);
     auto soff_of = [&](int stage) { return min((uint32_t)stage * (kBK * 2), kmax); };
     auto soffb_of = [&](int stage) { return NC ? (uint32_t)min(stage, nk - 1) * b_kstep : soff_of(stage); };
+    auto soffa_of = [&](int stage) { return AMC ? (uint32_t)min(stage, nk - 1) * a_kstep : soff_of(stage); };
 #pragma unroll
     for (int q = 0; q < LPS; ++q) issue_one(lds, 0, 0u, 0u, wave, q);
 #pragma unroll
-    for (int q = 0; q < HALF; ++q) issue_one(lds, 1, soff_of(1), soffb_of(1), wave, q);
+    for (int q = 0; q < HALF; ++q) issue_one(lds, 1, soffa_of(1), soffb_of(1), wave, q);
     wait_vmcnt<HALF>();
     exec_barrier();
     // A fragments are single-buffered: A block (pl, i, half sm) of the next sub-step is
@@ -650,7 +683,7 @@ struct BufPipeEngine {
     for (int f = 0; f < NRD; ++f) read_one(0, 0, f, fa, fb[0]);
     for (int s = 0; s < nk; ++s) {
       const int slot = s & 1;
-      const uint32_t soff1 = soff_of(s + 1), soff2 = soff_of(s + 2);
+      const uint32_t soff1 = soffa_of(s + 1), soff2 = soffa_of(s + 2);
       const uint32_t soffb1 = soffb_of(s + 1), soffb2 = soffb_of(s + 2);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
@@ -823,6 +856,7 @@ namespace kore {
 // ---------------------------------------------------------------------------------
 template <typename T, int BM, int BN, int WM, int WN, int NSLOT, int BL, int BCPOL = kCpolDefault>
 struct RingEngine {
+  static constexpr bool AMC = false;  // A is K-contiguous
   static constexpr int NW = 4;
   static_assert(WM * WN == NW, "4 waves");
   static constexpr int WROWS = BM / WM, WCOLS = BN / WN;

@@ -175,6 +175,39 @@ def test_gemm_packed_path(gpu, M, N, K, dtype, op, layout):
     assert torch.equal(out, again)
 
 
+@pytest.mark.parametrize("M,N,K,dtype,op,layout", [(4096, 4096, 4096, torch.bfloat16, "gemm", "kn"),
+                                                    (4096, 4096, 4096, torch.float16, "gemm_bias_gelu", "nk"),
+                                                    (3000, 4104, 1024, torch.bfloat16, "gemm_bias_silu", "kn"),
+                                                    (2048, 7168, 2048, torch.float16, "gemm_relu", "nk")])
+def test_gemm_transposed_a_in_place(gpu, M, N, K, dtype, op, layout):
+    """A transposed A (the a.t() view of a [K, M] tensor, M-contiguous) on a grid of at
+    least 192 tiles of 256x256 is read in place by the buffer engine through LDS transpose
+    reads (no workspace): ragged M and N, both B layouts, fused epilogues."""
+    has_bias, act = kore_amd.GEMM_FUSION_OPS.get(op, (False, "none"))
+    g = torch.Generator().manual_seed(M + 5 * N + K)
+    sc = 1.0 / K ** 0.5
+    a = (torch.randn((M, K), generator=g) * sc).to(dtype)
+    ad = a.t().contiguous().to(gpu).t()
+    assert ad.stride() == (1, M)
+    if layout == "kn":
+        b = (torch.randn((K, N), generator=g) * sc).to(dtype)
+        bd = b.to(gpu)
+    else:
+        w = (torch.randn((N, K), generator=g) * sc).to(dtype)
+        b, bd = w.t(), w.to(gpu).t()
+    bias = torch.randn((N,), generator=g).to(dtype) if has_bias else None
+    from kore_amd import _lib
+    lib = _lib.load()
+    assert lib.kore_gemm_workspace_bytes(0 if dtype == torch.bfloat16 else 1, 0, ad.data_ptr(), 1, M, bd.data_ptr(),
+                                         bd.stride(0), bd.stride(1), None, ad.data_ptr(), N, M, N, K) == 0
+    out = kore_amd.gemm_fused(ad, bd, bias.to(gpu) if has_bias else None, act)
+    ref = gemm_fusion_ref(a, b, bias, act)
+    dt = "bf16" if dtype == torch.bfloat16 else "fp16"
+    verdict(out, ref, "gemm_fusion", dt, f"transposed A {op} {M}x{N}x{K} {layout}")
+    pair_only(out, ref, dt, f"transposed A {op} {M}x{N}x{K} {layout}")
+    assert torch.equal(out, kore_amd.gemm_fused(ad, bd, bias.to(gpu) if has_bias else None, act))
+
+
 @pytest.mark.parametrize("M,N,K,dtype,op,layout", [(1, 4096, 4096, torch.bfloat16, "gemm", "kn"),
                                                     (16, 11008, 4096, torch.float16, "gemm_bias_gelu", "kn"),
                                                     (7, 1002, 2048, torch.bfloat16, "gemm_bias_relu", "nk"),
