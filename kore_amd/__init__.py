@@ -4,7 +4,7 @@ Operators (all on HIP device tensors, launched on torch's current stream):
 dense bf16/fp16/fp32 GEMM with fused bias + activation epilogues, the linear-layer GEMM
 backward, batched GEMM, OCP-e4m3
 fp8 a8w8 block-scaled GEMM, fp8/int8 a8w8 GEMM with row/column scales, and the fused top-k MoE SiLU grouped GEMM.  The kernels
-live in ``libkore_amd.so`` (built by ``python -m kore_amd.build``); see
+live in ``libkore_amd.so`` (built by ``python kore_amd/build.py``); see
 ``include/kore_amd.h`` for its C ABI.
 """
 

@@ -67,7 +67,7 @@ def load() -> C.CDLL:
         if _lib is None:
             if not LIB_PATH.exists():
                 raise RuntimeError(
-                    f"{LIB_PATH} is not built; run `python -m kore_amd.build` "
+                    f"{LIB_PATH} is not built; run `python kore_amd/build.py` "
                     "(hipcc --offload-arch=gfx950). kore_amd has no non-HIP fallback.")
             lib = C.CDLL(str(LIB_PATH))
             missing = [n for n in SIGNATURES if not hasattr(lib, n)]

@@ -4,7 +4,7 @@ Every source under ``kore_amd/csrc`` is compiled to an object for gfx950 (in
 parallel), then linked into ``kore_amd/libkore_amd.so``.  Objects go to
 ``kore_amd/_build``.  ``kore_amd/ext/kore_ops.cpp`` (the PyTorch-ROCm operators over
 the C ABI) is then compiled against torch into ``kore_amd/_C.so``, linked to
-``libkore_amd.so`` through an ``$ORIGIN`` runpath.  Run ``python -m kore_amd.build``
+``libkore_amd.so`` through an ``$ORIGIN`` runpath.  Run ``python kore_amd/build.py``
 or call :func:`build`.
 """
 

@@ -111,7 +111,7 @@ def test_header_declarations_are_complete():
 
 @pytest.fixture(scope="module")
 def lib():
-    assert LIB.exists(), "libkore_amd.so is not built (python -m kore_amd.build)"
+    assert LIB.exists(), "libkore_amd.so is not built (python kore_amd/build.py)"
     from kore_amd import _lib
 
     return _lib.load()
