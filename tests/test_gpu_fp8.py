@@ -40,6 +40,20 @@ def test_fp8_task_shapes(gpu, M, N, K, seed):
     pair_only(out, ref, "fp8", f"{M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("M,N,K", [(128, 4096, 4096), (100, 7168, 4096), (65, 4096, 8192), (97, 7168, 5120)])
+def test_fp8_skinny_ragged_rows(gpu, M, N, K):
+    """The skinny (M <= 128) kernel at a full 128-row tile and at ragged row counts
+    (rows past M repeat row M-1 and are never stored), K up to 64 blocks and K/128 not
+    a multiple of the wave count.  Repeated calls must be bit-identical (fixed-order
+    cross-wave sum)."""
+    xq, wq, xs, ws = W.fp8_inputs(M, N, K, seed=M + N + K, scale=0.2)
+    out = _run(gpu, xq, wq, xs, ws)
+    ref = matmul_blockscale_ref(xq, wq, xs, ws)
+    verdict(out, ref, "blockscale", "fp8", f"{M}x{N}x{K}")
+    verdict(out, ref, "blockscale_genv", "fp8", f"{M}x{N}x{K} (1e-2)")
+    assert bit_equal(out, _run(gpu, xq, wq, xs, ws)), "split-K result not reproducible"
+
+
 @pytest.mark.parametrize("M,N,K", [(4000, 3072, 640), (4000, 3072, 512), (3840, 3072, 1024),
                                    (1100, 6016, 512), (1100, 6016, 640), (768, 7168, 1024), (700, 7168, 512)])
 def test_fp8_wide_tiles(gpu, M, N, K):
