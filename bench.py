@@ -147,11 +147,19 @@ def _entry(name, op, dims, dtype, wall, kern, cold, graph):
 
 
 def cpu_model() -> str:
+    """The host CPU's model string, with its family / model / stepping numbers (a
+    virtualised host may report only a generic name such as "AMD EPYC")."""
     try:
+        info: dict[str, str] = {}
         with open("/proc/cpuinfo") as f:
             for ln in f:
-                if ln.startswith("model name"):
-                    return ln.split(":", 1)[1].strip()
+                if not ln.strip():
+                    break  # the first processor's block is enough
+                k, _, v = ln.partition(":")
+                info[k.strip()] = v.strip()
+        if "model name" in info:
+            ids = [f"{k} {info[k]}" for k in ("cpu family", "model", "stepping") if k in info]
+            return f"{info['model name']} ({', '.join(ids)}; {os.cpu_count()} logical CPUs)" if ids else info["model name"]
     except OSError:
         pass
     import platform
