@@ -107,6 +107,20 @@ def test_fused_moe_prefill_config_sampled(gpu):
     verdict(out[rows], ref, "north_star", "bf16", "prefill T=4096 (1e-2)")
 
 
+def test_fused_moe_prefill_config_full(gpu):
+    """BASELINE config 5 prefill, every token: the same fp32 algorithm as the oracle
+    (per-expert gathered fp32 GEMMs, fp32 SiLU gate, router-weighted sum) run by torch on
+    the device in fp32, against the whole T=4096 output.  The CPU oracle itself checks
+    the sampled tokens above; this covers the rows it does not reach."""
+    T, E, topk, D, I = 4096, 8, 2, 4096, 14336
+    hidden, w1, w2, tw, ti = W.moe_inputs(T, E, topk, D, I, seed=1, device=gpu)
+    out = kore_amd.fused_moe(hidden, w1, w2, tw, ti)
+    assert not torch.backends.cuda.matmul.allow_tf32  # full fp32 products in the reference
+    ref = moe_ref(hidden, w1, w2, tw, ti)
+    verdict(out, ref, "fused_moe", "bf16", "prefill T=4096 (all tokens, device fp32 reference)")
+    verdict(out, ref, "north_star", "bf16", "prefill T=4096 (all tokens, 1e-2)")
+
+
 @pytest.mark.parametrize("T,E,topk,D,I", [(64, 8, 2, 256, 384), (300, 4, 1, 256, 384), (640, 4, 2, 512, 384),
                                           (700, 4, 3, 384, 256)])
 def test_fused_moe_generic_tile_paths(gpu, T, E, topk, D, I):
