@@ -54,6 +54,18 @@ def test_fp8_skinny_ragged_rows(gpu, M, N, K):
     assert bit_equal(out, _run(gpu, xq, wq, xs, ws)), "split-K result not reproducible"
 
 
+@pytest.mark.parametrize("M,N,K", [(256, 7168, 4096), (384, 4096, 2048), (512, 1024, 512), (640, 2048, 1536)])
+def test_fp8_128_tiles(gpu, M, N, K):
+    """Problems with too few tiles for the 256-row kernels run 128x128 tiles on 4 waves
+    (four LDS slots, four-block scale loads): K from 4 to 32 blocks, 80 to 112 tiles."""
+    xq, wq, xs, ws = W.fp8_inputs(M, N, K, seed=M + N + K, scale=0.2)
+    out = _run(gpu, xq, wq, xs, ws)
+    ref = matmul_blockscale_ref(xq, wq, xs, ws)
+    verdict(out, ref, "blockscale", "fp8", f"{M}x{N}x{K}")
+    verdict(out, ref, "blockscale_genv", "fp8", f"{M}x{N}x{K} (1e-2)")
+    assert bit_equal(out, _run(gpu, xq, wq, xs, ws)), "not reproducible"
+
+
 @pytest.mark.parametrize("M,N,K", [(4000, 3072, 640), (4000, 3072, 512), (3840, 3072, 1024),
                                    (1100, 6016, 512), (1100, 6016, 640), (768, 7168, 1024), (700, 7168, 512)])
 def test_fp8_wide_tiles(gpu, M, N, K):
