@@ -54,7 +54,10 @@ extern "C" {
 /* Last error message of the calling host thread ("" when none). */
 const char* kore_last_error(void);
 
-/* Library ABI version (major*100 + minor). */
+/* Library ABI version (major*100 + minor).  200: kore_gemm and kore_batched_gemm take
+ * the caller's workspace (pointer and size) before the stream, and
+ * kore_gemm_backward_workspace_bytes takes the full argument list of kore_gemm_backward;
+ * a caller built against 1xx passes its stream where the workspace now is. */
 int kore_abi_version(void);
 
 /*

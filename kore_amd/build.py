@@ -94,27 +94,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
         raise RuntimeError("link of libkore_amd.so failed")
     os.replace(tmp, LIB)
     build_ext(verbose)
-    build_probes(verbose)
     return LIB
-
-
-PROBE_SRC = PKG / "probes" / "intake.hip"
-PROBE_LIB = PKG / "probes" / "libintake.so"
-
-
-def build_probes(verbose: bool = False) -> Path:
-    """Compile the LDS intake microbenchmark (a measurement tool loaded only by
-    ``python -m kore_amd.profiling intake``) into kore_amd/probes/libintake.so."""
-    tmp = PROBE_LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, *COMMON_FLAGS, "-shared", str(PROBE_SRC), "-o", str(tmp)]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError("build of kore_amd/probes/libintake.so failed")
-    os.replace(tmp, PROBE_LIB)
-    if verbose:
-        print(f"  built {PROBE_LIB.name}")
-    return PROBE_LIB
 
 
 def build_ext(verbose: bool = False) -> Path:

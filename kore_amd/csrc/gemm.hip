@@ -2,22 +2,23 @@
 //
 // C[M,N] = act(A[M,K] @ B[K,N] + bias[N]) with fp32 accumulation, one RNE cast.
 //
-// Fast path ("tile kernel"): 256 threads = 4 waves in a 2x2 grid, macro tile BM x BN
-// (256x256 or 128x128), K step 64.  A is K-contiguous; B is either K-contiguous (the
-// A.B^T / A.W^T case) or N-contiguous (natural [K,N]).  Global -> VGPR 16-byte loads
-// are issued for tile k+1 while tile k is multiplied out of the other LDS buffer
-// (double buffering, one barrier per K step).  LDS rows are 128 bytes (64 x 16-bit)
-// with an XOR swizzle of the 16-byte chunks so the MFMA fragment reads
-// (ds_read_b128, 32 consecutive rows per half-wave) are bank-conflict free.  An
-// N-contiguous B tile is transposed in registers (8x8 blocks of 16-bit values with
-// v_perm_b32) before it is written to LDS in the same K-contiguous layout.
-// The MFMA is issued with the B fragment as the first operand, so each lane ends up
-// holding 4 N-consecutive outputs of one row; the epilogue applies bias and the
-// activation in fp32, packs, stages the wave's tile in LDS and writes C with
-// 16-byte row-contiguous stores.
+// Large grids (>= 192 tiles of 256x256, K % 64 == 0): gemm_buf_kernel on the buffer
+// engine (BufPipeEngine, tile_engine.hpp).  Operands go straight from global memory into
+// LDS with buffer_load ... lds (no VGPR staging), two 64-wide K stages in flight, one
+// barrier per stage.  K-contiguous B runs 8 waves (2 x 4, 128 x 64 each, two per SIMD) on
+// 16x16x32 MFMAs; an N-contiguous B (natural [K,N]) or an M-contiguous A (a transposed
+// view) is staged as K-rows and read back with the LDS transpose read
+// ds_read_b64_tr_b16.  LDS rows are 128 bytes with an XOR swizzle of the 16-byte chunks.
+// The MFMA is issued with the B fragment as the first operand, so each lane holds 4
+// N-consecutive outputs of one row; the epilogue applies bias and the activation in fp32,
+// packs, stages the wave's tile in LDS and writes C with 16-byte row-contiguous stores.
 //
-// Generic path: any strides and any K, 128x128 MFMA tiles fed by bounds-checked element
-// reads along the unit-stride index (gemm_generic_mfma_kernel).
+// Mid-size grids run the deep ring engine (gemm_deep_kernel: several K stages in
+// flight); decode-sized M splits K (gemm_splitk_kernel + a fixed-order reduction);
+// 1024^3-like problems the skinny ring (gemm_ring_kernel); K tails and small K the
+// register-staged tile engine (gemm_tile_kernel); batched K of 64 or 128 the persistent
+// short-K kernel.  Generic path: any strides and any K, 128x128 MFMA tiles fed by
+// bounds-checked element reads along the unit-stride index (gemm_generic_mfma_kernel).
 #include "../../include/kore_amd.h"
 #include "kore_common.hpp"
 #include "tile_engine.hpp"
@@ -1431,13 +1432,10 @@ extern "C" int kore_batched_gemm(int dtype, const void* a, int64_t sa_b, int64_t
   return kore::run_gemm(d, ws, stream);
 }
 
-// Linear-layer backward for Y = X @ W^T: dX = dY @ W and dW = dY^T @ X.  W and X are
-// read in place as N-contiguous B operands (LDS transpose reads); the A operand of dW
-// must be K-contiguous, so dY^T [N,M] is formed in the caller's workspace by one
-// HBM-bound transpose.
-namespace kore {
-}  // namespace kore
-
+// Linear-layer backward for Y = X @ W^T: dX = dY @ W and dW = dY^T @ X, two run_gemm
+// calls.  dY, W and X are read in place: W and X as N-contiguous B operands (LDS
+// transpose reads), dY^T as an M-contiguous A view of dY on the 8-wave buffer tiles.
+// Only grids too small for those tiles pack dY^T into the caller's workspace.
 namespace kore {
 namespace {
 // The two GEMMs of the backward.

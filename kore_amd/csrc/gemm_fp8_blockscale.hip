@@ -906,8 +906,12 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // the wave's own `s_waitcnt vmcnt` and no barrier is needed.  The block's scales
 // travel in the same DMA stream (4-byte loads, one activation scale per lane and the
 // weight scale), so the only memory waits in the loop are those vmcnt waits.  16-byte
-// chunks are XOR swizzled by key(r) = (r ^ (r >> 3)) & 7 so fragment reads are
-// conflict-free.
+// chunks are XOR swizzled by key(r) = (r ^ (r >> 3)) & 7, so the 16 rows one fragment
+// read touches with one chunk column sit in 16 distinct 16-byte bank slots.  That holds
+// for a pass of 16 lanes over 64 banks; rocprof's SQ_LDS_BANK_CONFLICT still reports
+// about 0.76 conflict cycles per LDS access cycle for this 16-row fragment shape (the
+// 32-row shape of the tiled kernels reads 0.03 with the same key), so the hardware
+// evidently does not serve a ds_read_b128 in such 16-lane passes.
 //
 // v_mfma_f32_16x16x128_f8f6f4 with the W fragment first: D[n][m], lane l owns column
 // m = l % 16 (one activation scale) and rows n = 4*(l/16) + i of a 16-column block

@@ -40,4 +40,4 @@ int device_cus() {
 }  // namespace kore
 
 extern "C" const char* kore_last_error(void) { return kore::g_last_error; }
-extern "C" int kore_abi_version(void) { return 100; }
+extern "C" int kore_abi_version(void) { return 200; }

@@ -259,53 +259,109 @@ at::Tensor fused_moe(const at::Tensor& hidden, const at::Tensor& w1_, const at::
 }
 
 // ---- top-1 grouped expert GEMMs (kore/tasks/moe_grouped_gemm_bf16 / _fp8); the
-// zero-padding of shapes the kernels do not take stays in the Python host ----
-at::Tensor grouped_gemm(const at::Tensor& x_, const at::Tensor& w_, const at::Tensor& ids) {
-  require_hip({x_, w_, ids});
+// zero-padding of shapes the kernels do not take stays in the Python host.  Every
+// shape, dtype and length is checked here, before any data pointer is taken, so a
+// direct torch.ops.korehip call with mismatched tensors raises instead of reading
+// past the ids, weights or scales on the device. ----
+
+// expert_ids: int32 with exactly M ids (any shape), returned as a contiguous [M].
+at::Tensor expert_ids_of(const at::Tensor& ids, int64_t M) {
+  TORCH_CHECK_VALUE(ids.defined(), "expert_ids: undefined tensor");
+  TORCH_CHECK_VALUE(ids.scalar_type() == at::kInt, "expert_ids must be int32 (got ", ids.scalar_type(), ")");
+  TORCH_CHECK_VALUE(ids.numel() == M, "expert_ids must hold one id per row: ", M, " (got ", ids.sizes(), ")");
+  return ids.reshape({M}).contiguous();
+}
+
+at::Tensor grouped_gemm(const at::Tensor& x_, const at::Tensor& w_, const at::Tensor& ids_) {
+  TORCH_CHECK_VALUE(x_.defined() && w_.defined(), "grouped_gemm: undefined tensor");
+  TORCH_CHECK_VALUE(x_.dim() == 2 && w_.dim() == 3 && w_.size(2) == x_.size(1),
+                    "grouped_gemm expects hidden[M,K], w[E,N,K] (got ", x_.sizes(), ", ", w_.sizes(), ")");
+  TORCH_CHECK_NOT_IMPLEMENTED(x_.scalar_type() == at::kBFloat16 && w_.scalar_type() == at::kBFloat16,
+                              "grouped_gemm runs bf16 operands (got ", x_.scalar_type(), ", ", w_.scalar_type(), ")");
   const int64_t M = x_.size(0), K = x_.size(1), E = w_.size(0), N = w_.size(1);
+  const at::Tensor ids = expert_ids_of(ids_, M);
+  require_hip({x_, w_, ids});
   const at::Tensor x = x_.stride(1) == 1 && x_.stride(0) % 8 == 0 ? x_ : x_.contiguous();
   const at::Tensor w = w_.contiguous();
   const c10::DeviceGuard guard(x.device());
   at::Tensor out = at::zeros({M, N}, x.options());
+  if (M == 0 || N == 0 || K == 0 || E == 0) return out;
   at::Tensor ws = workspace(kore_moe_grouped_gemm_workspace_bytes(M, E), x);
   check_rc(kore_moe_grouped_gemm(x.data_ptr(), x.stride(0), w.data_ptr(), ids.data_ptr<int32_t>(), out.data_ptr(),
                                  out.stride(0), M, N, K, E, ptr_or_null(ws), bytes_of(ws), stream_of(x)));
   return out;
 }
 
-at::Tensor grouped_gemm_fp8(const at::Tensor& xq_, const at::Tensor& wq_, const at::Tensor& xs, const at::Tensor& wsc,
-                            const at::Tensor& ids) {
-  require_hip({xq_, wq_, xs, wsc, ids});
+at::Tensor grouped_gemm_fp8(const at::Tensor& xq_, const at::Tensor& wq_, const at::Tensor& xs, const at::Tensor& wsc_,
+                            const at::Tensor& ids_) {
+  TORCH_CHECK_VALUE(xq_.defined() && wq_.defined() && xs.defined() && wsc_.defined(), "grouped_gemm_fp8: undefined tensor");
+  TORCH_CHECK_VALUE(xq_.dim() == 2 && wq_.dim() == 3 && wq_.size(2) == xq_.size(1),
+                    "grouped_gemm_fp8 expects xq[M,K], wq[E,N,K] (got ", xq_.sizes(), ", ", wq_.sizes(), ")");
+  TORCH_CHECK_NOT_IMPLEMENTED(xq_.scalar_type() == at::kFloat8_e4m3fn && wq_.scalar_type() == at::kFloat8_e4m3fn,
+                              "grouped_gemm_fp8 runs float8_e4m3fn operands (got ", xq_.scalar_type(), ", ",
+                              wq_.scalar_type(), ")");
   const int64_t M = xq_.size(0), K = xq_.size(1), E = wq_.size(0), N = wq_.size(1);
+  const int64_t xs_st = scale_stride(xs, M, "x_scale");
+  TORCH_CHECK_VALUE(wsc_.scalar_type() == at::kFloat, "w_scale must be fp32 (got ", wsc_.scalar_type(), ")");
+  TORCH_CHECK_VALUE((wsc_.dim() == 2 && wsc_.size(0) == E && wsc_.size(1) == N) ||
+                        (wsc_.dim() == 3 && wsc_.size(0) == E && wsc_.size(1) == N && wsc_.size(2) == 1),
+                    "w_scale must be [", E, ",", N, ",1] or [", E, ",", N, "] (got ", wsc_.sizes(), ")");
+  const at::Tensor ids = expert_ids_of(ids_, M);
+  require_hip({xq_, wq_, xs, wsc_, ids});
   const at::Tensor xq = xq_.stride(1) == 1 && xq_.stride(0) % 16 == 0 ? xq_ : xq_.contiguous();
   const at::Tensor wq = wq_.contiguous();
+  const at::Tensor wsc = wsc_.reshape({E, N}).contiguous();
   const c10::DeviceGuard guard(xq.device());
   at::Tensor out = at::zeros({M, N}, xq.options().dtype(at::kBFloat16));
+  if (M == 0 || N == 0 || K == 0 || E == 0) return out;
   at::Tensor ws = workspace(kore_moe_grouped_gemm_workspace_bytes(M, E), xq);
-  check_rc(kore_moe_grouped_gemm_fp8(xq.data_ptr(), xq.stride(0), wq.data_ptr(), xs.data_ptr<float>(), 1,
+  check_rc(kore_moe_grouped_gemm_fp8(xq.data_ptr(), xq.stride(0), wq.data_ptr(), xs.data_ptr<float>(), xs_st,
                                      wsc.data_ptr<float>(), ids.data_ptr<int32_t>(), out.data_ptr(), out.stride(0), M,
                                      N, K, E, ptr_or_null(ws), bytes_of(ws), stream_of(xq)));
   return out;
 }
 
 // ---- token permute / unpermute as row copies (kore/tasks/moe_permute_bf16/reference.py:56-59,
-// kore/tasks/breadth/moe_ext.py:546-571) ----
-at::Tensor gather_rows(const at::Tensor& src, const at::Tensor& idx) {
-  require_hip({src, idx});
+// kore/tasks/breadth/moe_ext.py:546-571).  Row indices outside the table are
+// range-checked by the kernel (a gathered row reads zero, a scattered row is
+// dropped); the number of rows read is checked here. ----
+
+// idx: int32 1-D, returned contiguous.
+at::Tensor row_index_of(const at::Tensor& idx) {
+  TORCH_CHECK_VALUE(idx.defined(), "row index: undefined tensor");
+  TORCH_CHECK_VALUE(idx.dim() == 1 && idx.scalar_type() == at::kInt, "row index must be int32 [n] (got ",
+                    idx.sizes(), " ", idx.scalar_type(), ")");
+  return idx.contiguous();
+}
+
+at::Tensor gather_rows(const at::Tensor& src_, const at::Tensor& idx_) {
+  TORCH_CHECK_VALUE(src_.defined() && src_.dim() == 2, "gather_rows expects src[rows, D] (got ",
+                    src_.defined() ? src_.sizes() : at::IntArrayRef{}, ")");
+  const at::Tensor idx = row_index_of(idx_);
+  require_hip({src_, idx});
+  const at::Tensor src = src_.stride(1) == 1 ? src_ : src_.contiguous();
   const int64_t eb = src.element_size();
   const c10::DeviceGuard guard(src.device());
   at::Tensor out = at::empty({idx.numel(), src.size(1)}, src.options());
-  if (idx.numel() && src.size(1))
+  if (idx.numel() && src.size(1) && src.size(0))
     check_rc(kore_gather_rows(src.data_ptr(), src.stride(0) * eb, src.size(0), idx.data_ptr<int32_t>(), idx.numel(),
                               src.size(1) * eb, out.data_ptr(), out.stride(0) * eb, stream_of(src)));
+  else if (idx.numel())
+    out.zero_();
   return out;
 }
 
-at::Tensor scatter_rows(const at::Tensor& src, const at::Tensor& idx) {
-  require_hip({src, idx});
+at::Tensor scatter_rows(const at::Tensor& src_, const at::Tensor& idx_) {
+  TORCH_CHECK_VALUE(src_.defined() && src_.dim() == 2, "scatter_rows expects src[rows, D] (got ",
+                    src_.defined() ? src_.sizes() : at::IntArrayRef{}, ")");
+  const at::Tensor idx = row_index_of(idx_);
+  TORCH_CHECK_VALUE(idx.numel() <= src_.size(0), "scatter_rows reads one src row per index: ", idx.numel(),
+                    " indices for ", src_.size(0), " rows");
+  require_hip({src_, idx});
+  const at::Tensor src = src_.stride(1) == 1 ? src_ : src_.contiguous();
   const int64_t eb = src.element_size();
   const c10::DeviceGuard guard(src.device());
-  at::Tensor out = at::zeros_like(src);
+  at::Tensor out = at::zeros_like(src, at::MemoryFormat::Contiguous);
   if (idx.numel() && src.size(1))
     check_rc(kore_scatter_rows(src.data_ptr(), src.stride(0) * eb, idx.data_ptr<int32_t>(), idx.numel(),
                                out.data_ptr(), src.size(0), src.size(1) * eb, out.stride(0) * eb, stream_of(src)));

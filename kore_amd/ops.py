@@ -37,6 +37,7 @@ try:
     from . import _C
 except ImportError as e:  # no silent fallback: the product needs its native host layer
     raise ImportError(f"kore_amd._C is not built ({e}); run `python kore_amd/build.py`") from e
+from . import _fake  # noqa: F401,E402  (shape-only kernels of torch.ops.korehip for tracing)
 
 DT_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 ACT_CODE = {"none": 0, "relu": 1, "gelu": 2, "silu": 3, "tanh": 4, "sigmoid": 5}

@@ -486,63 +486,6 @@ def write_vendor(trace_dir: str, out: str, cmd: str, iters: int) -> None:
     print(f"wrote {out}")
 
 
-def _intake(out: str, cmd: str) -> None:
-    """Run the LDS intake microbenchmark (kore_amd/probes/intake.hip): 256 workgroups,
-    one per CU, each streaming 32 stages of 64 KiB through a two-slot LDS ring, with
-    and without ds_read_b128 traffic of three times the loaded bytes (the fragment-read
-    to load ratio of the fp8 headline tile), and the reads alone."""
-    import ctypes as C
-    import time
-
-    import torch
-
-    from kore_amd.build import PROBE_LIB
-
-    lib = C.CDLL(str(PROBE_LIB))
-    f = lib.kore_probe_intake
-    f.restype = C.c_int
-    f.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_uint32, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
-    src = torch.randint(0, 255, (32 << 20,), dtype=torch.uint8, device="cuda")
-    sink = torch.zeros(256, dtype=torch.int32, device="cuda")
-    st = torch.cuda.current_stream().cuda_stream
-    nst, iters = 32, 50
-    rows = []
-    for nw in (4, 8):
-        for mode in (0, 1):
-            for reads in (0, 3 * 64 // nw, -(3 * 64 // nw)):
-                call = lambda: f(nw, mode, src.data_ptr(), src.numel(), 4096, nst, reads, sink.data_ptr(), st)
-                if call() != 0:
-                    raise RuntimeError("kore_probe_intake launch failed")
-                t0 = time.perf_counter()
-                while time.perf_counter() - t0 < 0.3:
-                    call()
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                torch.cuda.synchronize()
-                e0.record()
-                for _ in range(iters):
-                    call()
-                e1.record()
-                torch.cuda.synchronize()
-                us = e0.elapsed_time(e1) / iters * 1e3
-                load = 0.0 if reads < 0 else 65536 * nst / (us * 1e-6) / 1e9
-                rd = abs(reads) * nw * 1024 * nst / (us * 1e-6) / 1e9
-                rows.append((nw, "8 rows x 128 B" if mode == 0 else "1 KiB contiguous",
-                             "none" if reads < 0 else "direct-to-LDS", abs(reads), us, load, rd, load + rd))
-                print(f"intake waves {nw} mode {mode} reads {reads}: {us:.1f} us", flush=True)
-    lines = ["# LDS intake per CU: direct-to-LDS loads and ds_read_b128 alone and together", "",
-             "Command (from the repository root, on one MI355X):", "", "```", cmd, "```", "",
-             "256 workgroups (one per CU), 32 stages of 64 KiB each through a two-slot LDS ring, "
-             f"{iters} timed launches after 0.3 s of warm-up; rates are per CU.", "",
-             "| waves | load shape | loads | ds_read_b128 per wave and stage | us per launch | "
-             "loads into LDS (GB/s) | LDS reads (GB/s) | LDS total (GB/s) |",
-             "|---|---|---|---|---|---|---|---|"]
-    for nw, shape, ld, rds, us, load, rd, tot in rows:
-        lines.append(f"| {nw} | {shape} | {ld} | {rds} | {us:.1f} | {load:.0f} | {rd:.0f} | {tot:.0f} |")
-    with open(out, "w") as fh:
-        fh.write("\n".join(lines) + "\n")
-    print(f"wrote {out}")
-
-
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(prog="python -m kore_amd.profiling")
     sub = p.add_subparsers(dest="action", required=True)
@@ -586,9 +529,6 @@ def main(argv=None) -> int:
     vs.add_argument("--out", required=True)
     vs.add_argument("--cmd", required=True)
     vs.add_argument("--iters", type=int, default=20)
-    ik = sub.add_parser("intake", help="LDS intake microbenchmark (direct-to-LDS loads and ds_read_b128)")
-    ik.add_argument("--out", required=True)
-    ik.add_argument("--cmd", required=True)
     sub.add_parser("grounding-passes", help="print the grounding counter groups, one pass per line")
     gr = sub.add_parser("grounding")
     gr.add_argument("dirs", nargs="+")
@@ -610,8 +550,6 @@ def main(argv=None) -> int:
         _vendor(a.iters)
     elif a.action == "vendor-stats":
         write_vendor(a.dir, a.out, a.cmd, a.iters)
-    elif a.action == "intake":
-        _intake(a.out, a.cmd)
     elif a.action == "grounding-passes":
         print("\n".join(" ".join(g) for g in GROUNDING_PASSES))
     elif a.action == "grounding":

@@ -139,6 +139,30 @@ def test_grouped_gemm_fp8_invalid_ids_one_expert_determinism(gpu):
     assert bit_equal(g1, d1)
 
 
+def test_registered_grouped_ops_reject_and_stride(gpu):
+    """torch.ops.korehip.grouped_gemm_fp8 called directly (no Python layer): a short
+    expert_ids raises ValueError before anything is launched, and a strided x_scale
+    column is read with its real stride (bit-equal to the contiguous call)."""
+    M, E, N, K = 256, 4, 256, 256
+    xq, wq, xs, ws, ti = W.grouped_fp8_inputs(M, E, N, K, seed=7, device=gpu)
+    ops = torch.ops.korehip
+    with pytest.raises(ValueError, match="one id per row"):
+        ops.grouped_gemm_fp8(xq, wq, xs, ws, ti[: M // 2])
+    with pytest.raises(ValueError, match="w_scale"):
+        ops.grouped_gemm_fp8(xq, wq, xs, ws[:, : N // 2], ti)
+    ref = ops.grouped_gemm_fp8(xq, wq, xs, ws, ti)
+    wide = torch.zeros((M, 3), dtype=torch.float32, device=gpu)
+    wide[:, 1] = xs[:, 0]
+    strided = wide[:, 1:2]  # [M,1], stride 3 along M
+    assert strided.stride(0) == 3
+    assert bit_equal(ops.grouped_gemm_fp8(xq, wq, strided, ws, ti), ref)
+    hidden, w, ti16 = W.grouped_inputs(M, E, N, K, seed=7, device=gpu)
+    with pytest.raises(ValueError, match="one id per row"):
+        ops.grouped_gemm(hidden, w, ti16[:-1])
+    with pytest.raises(ValueError, match="one src row per index"):
+        ops.scatter_rows(hidden, torch.arange(M + 1, dtype=torch.int32, device=gpu))
+
+
 def _sort_idx(M, E, seed):
     _, _, ti = W.grouped_inputs(M, E, 128, 8, seed=seed, router_bias=trace32_bias(E))
     return torch.argsort(ti, stable=True).to(torch.int32)

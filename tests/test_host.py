@@ -123,7 +123,7 @@ def test_library_exports_every_declared_symbol(lib):
     from kore_amd import _lib
 
     assert set(_declared_functions()) == set(_lib.SIGNATURES)
-    assert lib.kore_abi_version() == 100
+    assert lib.kore_abi_version() == 200
 
 
 def test_capi_validation_without_gpu(lib):
@@ -302,3 +302,84 @@ def test_ops_fail_loudly_without_device_tensors():
         kore_amd.gemm(a, a.t())
     with pytest.raises(ValueError, match="HIP device"):
         torch.ops.korehip.gemm_a8w8_blockscale(a, a, a, a)
+
+
+def test_registered_grouped_ops_check_shapes_before_the_device():
+    """torch.ops.korehip.* can be called without the Python layer: the C++ operators
+    check dims, K, dtypes, the number of expert ids, the scale shapes and the rows a
+    scatter reads before anything reaches the device.  CPU tensors with a consistent
+    shape get as far as the device check."""
+    import kore_amd  # noqa: F401  (loads the extension and registers the operators)
+
+    ops = torch.ops.korehip
+    bf = torch.bfloat16
+    f8 = torch.float8_e4m3fn
+    x, w = torch.zeros((8, 64), dtype=bf), torch.zeros((2, 128, 64), dtype=bf)
+    ids = torch.zeros(8, dtype=torch.int32)
+    with pytest.raises(ValueError, match="one id per row"):
+        ops.grouped_gemm(x, w, ids[:5])                       # short expert_ids
+    with pytest.raises(ValueError, match="int32"):
+        ops.grouped_gemm(x, w, ids.to(torch.int64))
+    with pytest.raises(ValueError, match="w\\[E,N,K\\]"):
+        ops.grouped_gemm(x, torch.zeros((2, 128, 32), dtype=bf), ids)   # K mismatch
+    with pytest.raises(NotImplementedError, match="bf16"):
+        ops.grouped_gemm(x.float(), w.float(), ids)
+    with pytest.raises(ValueError, match="HIP device"):
+        ops.grouped_gemm(x, w, ids)                           # consistent: the device check
+
+    xq, wq = torch.zeros((8, 128), dtype=f8), torch.zeros((2, 128, 128), dtype=f8)
+    xs, wsc = torch.ones((8, 1)), torch.ones((2, 128, 1))
+    with pytest.raises(ValueError, match="one id per row"):
+        ops.grouped_gemm_fp8(xq, wq, xs, wsc, ids[:3])
+    with pytest.raises(ValueError, match="x_scale"):
+        ops.grouped_gemm_fp8(xq, wq, torch.ones((4, 1)), wsc, ids)       # short x_scale
+    with pytest.raises(ValueError, match="x_scale"):
+        ops.grouped_gemm_fp8(xq, wq, torch.ones((8, 2)), wsc, ids)       # not a column
+    with pytest.raises(ValueError, match="w_scale"):
+        ops.grouped_gemm_fp8(xq, wq, xs, torch.ones((2, 64)), ids)
+    with pytest.raises(ValueError, match="HIP device"):
+        ops.grouped_gemm_fp8(xq, wq, torch.ones((16, 1))[::2], wsc, ids)  # strided x_scale is accepted
+
+    src = torch.zeros((4, 16), dtype=bf)
+    with pytest.raises(ValueError, match="one src row per index"):
+        ops.scatter_rows(src, torch.arange(6, dtype=torch.int32))
+    with pytest.raises(ValueError, match="int32"):
+        ops.gather_rows(src, torch.arange(2))
+    with pytest.raises(ValueError, match="HIP device"):
+        ops.scatter_rows(src, torch.arange(4, dtype=torch.int32))
+
+
+def test_fake_kernels_trace_every_operator():
+    """Every korehip operator has a shape-only kernel, so FakeTensor tracing (the first
+    stage of torch.compile) runs without touching data pointers."""
+    import kore_amd  # noqa: F401
+    from torch.fx.experimental.proxy_tensor import make_fx
+
+    ops = torch.ops.korehip
+    bf, f8 = torch.bfloat16, torch.float8_e4m3fn
+
+    def fn(a, b, bias, xq, wq, xs, wsb, ids2, hidden, w1, w2, tw, ti, gx, gw, gid, xsr, wsr, gq, gwq, gws):
+        return (ops.gemm(a, b), ops.gemm_fused(a, b, bias, 2), ops.batched_gemm(a[None], b.t()[None]),
+                ops.gemm_backward(a, b.t(), ops.gemm(a, b)), ops.gemm_a8w8_blockscale(xq, wq, xs, wsb),
+                ops.gemm_a8w8(xq, wq, xsr, wsr), ops.moe_align(ids2, 8, 32),
+                ops.fused_moe(hidden, w1, w2, tw, ti), ops.grouped_gemm(gx, gw, gid),
+                ops.grouped_gemm_fp8(gq, gwq, xsr, gws, gid), ops.gather_rows(a, gid),
+                ops.scatter_rows(a, gid))
+
+    args = (torch.zeros(64, 128, dtype=bf), torch.zeros(128, 256, dtype=bf), torch.zeros(256, dtype=bf),
+            torch.zeros(64, 256, dtype=f8), torch.zeros(384, 256, dtype=f8), torch.ones(64, 2),
+            torch.ones(3, 2), torch.zeros(64, 2, dtype=torch.int32), torch.zeros(64, 128, dtype=bf),
+            torch.zeros(8, 512, 128, dtype=bf), torch.zeros(8, 128, 256, dtype=bf), torch.ones(64, 2),
+            torch.zeros(64, 2, dtype=torch.int32), torch.zeros(64, 128, dtype=bf),
+            torch.zeros(4, 256, 128, dtype=bf), torch.zeros(64, dtype=torch.int32), torch.ones(64, 1),
+            torch.ones(1, 384), torch.zeros(64, 256, dtype=f8), torch.zeros(4, 384, 256, dtype=f8),
+            torch.ones(4, 384, 1))
+    g = make_fx(fn, tracing_mode="fake")(*args)
+    outs = [n for n in g.graph.nodes if n.op == "call_function" and "korehip" in str(n.target)]
+    assert len(outs) == 13
+    shapes = {str(n.target): n.meta["val"] for n in outs}
+    assert tuple(shapes["korehip.gemm_fused.default"].shape) == (64, 256)
+    assert shapes["korehip.gemm_a8w8_blockscale.default"].dtype == bf
+    assert [tuple(t.shape) for t in shapes["korehip.moe_align.default"]] == [(9,), (384,), (12,)]
+    assert tuple(shapes["korehip.grouped_gemm_fp8.default"].shape) == (64, 384)
+    assert tuple(shapes["korehip.scatter_rows.default"].shape) == (64, 128)
