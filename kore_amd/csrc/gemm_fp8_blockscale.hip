@@ -906,12 +906,9 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // the wave's own `s_waitcnt vmcnt` and no barrier is needed.  The block's scales
 // travel in the same DMA stream (4-byte loads, one activation scale per lane and the
 // weight scale), so the only memory waits in the loop are those vmcnt waits.  16-byte
-// chunks are XOR swizzled by key(r) = (r ^ (r >> 3)) & 7, so the 16 rows one fragment
-// read touches with one chunk column sit in 16 distinct 16-byte bank slots.  That holds
-// for a pass of 16 lanes over 64 banks; rocprof's SQ_LDS_BANK_CONFLICT still reports
-// about 0.76 conflict cycles per LDS access cycle for this 16-row fragment shape (the
-// 32-row shape of the tiled kernels reads 0.03 with the same key), so the hardware
-// evidently does not serve a ds_read_b128 in such 16-lane passes.
+// chunks are XOR swizzled by key(r) = (r ^ (r >> 3)) & 7 (see sk_key below for why this
+// kernel keeps that key although its 16-row fragment reads take a 2-way bank conflict
+// with it: rocprof's SQ_LDS_BANK_CONFLICT reads 0.76 conflict cycles per access cycle).
 //
 // v_mfma_f32_16x16x128_f8f6f4 with the W fragment first: D[n][m], lane l owns column
 // m = l % 16 (one activation scale) and rows n = 4*(l/16) + i of a 16-column block
@@ -941,6 +938,10 @@ struct SkinnyCfg {
   static_assert(S >= 1 && S <= 3 && LPB * (S - 1) <= 63, "vmcnt range");
 };
 
+// Fragment reads are the 16-row shape (lane (r, g) reads row r of a 16-row group), which
+// this 32-row key serves with a 2-way bank conflict.  The conflict-free 16-row key swz16
+// was measured in the same process and is kept out: M=128 7% slower, M=96 4% faster,
+// M=16..64 within 3% -- the kernel's time is its L2-to-LDS operand stream, not LDS reads.
 __device__ __forceinline__ int sk_key(int r) { return (r ^ (r >> 3)) & 7; }
 
 template <typename C>

@@ -127,10 +127,21 @@ __device__ __forceinline__ float apply_act(float x) {
   }
 }
 
-// XOR swizzle of 16-byte chunks inside a 128-byte LDS row.  Rows r and r+8 get
-// different keys, so 8 consecutive rows (32 banks) and 16 consecutive rows split
-// by row parity (64 banks) both hit distinct banks for one chunk column.
+// XOR swizzle of 16-byte chunks inside a 128-byte LDS row, for the 32-row fragment
+// shape (32x32 MFMAs: lane l reads row l % 32 at chunk c(l / 32)).  Measured with an
+// in-bounds ds_read_b128 probe on MI355X (8 waves per CU, 1 KiB per wave instruction):
+// that read pattern runs at the contiguous rate, 4 cycles per instruction per CU
+// (256 bytes per clock).
 __device__ __forceinline__ int swz8(int r) { return (r ^ (r >> 3)) & 7; }
+
+// Swizzle key for the 16-row fragment shape (16x16 MFMAs: lane l reads row l % 16 of a
+// 16-row group at chunk c0 + l / 16).  With swz8 that pattern took 8 cycles per
+// instruction in the same probe (a 2-way bank conflict, also seen as rocprof's
+// SQ_LDS_BANK_CONFLICT in the kernels that used it), with this key 4, the contiguous rate.  Only r % 16 matters: any XOR that
+// is constant over a 16-row group moves every lane's chunk alike.
+__device__ __forceinline__ int swz16(int r) {
+  return ((((r >> 2) & 3) << 1) ^ ((r & 3) << 1) ^ (r & 1)) & 7;
+}
 
 // XCD-aware remap of a 1-D launch: workgroups are dispatched round-robin over the
 // 8 XCDs, so consecutive tile ids are handed to one XCD (one L2) when possible.
