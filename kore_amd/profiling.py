@@ -421,40 +421,205 @@ def read_traffic(workload: str, path: str = TRAFFIC_FILE):
     return None
 
 
-def _vendor(iters: int, min_warm_s: float = 0.5) -> None:
-    """The vendor library (hipBLASLt through torch) on the shapes where it is the bar:
-    bf16 4096^3 A.B^T, bf16 8192x4096 . 4096x8192, fp32 512x4096x4096 + bias (addmm) and
-    fp8 e4m3 2048x7168x4096 with unit per-tensor scales (_scaled_mm).  Each op is warmed
-    up for ``min_warm_s`` seconds, then called ``iters`` times.  Timing only: the vendor
-    library is run, never read."""
+def _vendor_configs(dev):
+    """``name -> (what, build)`` of the vendor library's call on every compute-bound bench
+    configuration (the reference times such a ``baseline_fn`` beside each task,
+    ``kore/tasks/_genops.py:453-464``, ``kore/tasks/aiter_ref.py:227-256``).  ``build()``
+    draws the bench's own seeded inputs and returns a list of ``(label, fn)`` variants:
+    every vendor route torch offers for the op (a fused hipBLASLt epilogue where one
+    exists, else the GEMM plus torch's elementwise kernel); the bar is the fastest."""
+    import torch
+    import torch.nn.functional as F
+
+    from kore_amd import workloads as W
+
+    f8 = torch.float8_e4m3fn
+
+    def fp8(M):
+        def build():
+            xq, wq, xs, ws = W.fp8_inputs(M, 7168, 4096, seed=0, device=dev)
+            one = torch.ones((), device=dev)
+            sa, sb = xs[:, :1].contiguous(), ws.new_ones((1, 7168))
+            v = [("_scaled_mm per-tensor (unit scales; less work than block scales)",
+                  lambda: torch._scaled_mm(xq, wq.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)),
+                 ("_scaled_mm row-wise scales",
+                  lambda: torch._scaled_mm(xq, wq.t(), scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16))]
+            # 1x128 activation / 128x128 weight block scales, where the vendor path has them
+            xsb, wsb = xs.contiguous(), ws.t().contiguous()
+            v.append(("_scaled_mm 1x128 / 128x128 block scales",
+                      lambda: torch._scaled_mm(xq, wq.t(), scale_a=xsb, scale_b=wsb, out_dtype=torch.bfloat16)))
+            return v
+        return build
+
+    def dense(n, kn=False):
+        def build():
+            if kn:
+                g = W._gen(dev, 0)
+                a = (torch.randn((n, n), generator=g, device=dev) / n ** 0.5).to(torch.bfloat16)
+                b = torch.randn((n, n), generator=g, device=dev).to(torch.bfloat16)
+            else:
+                a, b = W.dense_inputs(n, n, n, seed=0, device=dev)
+            return [("torch.matmul", lambda: torch.matmul(a, b))]
+        return build
+
+    def fused(act, M=4096, N=4096, K=4096, kn=False, dtype=torch.float16):
+        def build():
+            if kn:
+                g = W._gen(dev, 0)
+                a = (torch.randn((M, K), generator=g, device=dev) / K ** 0.5).to(dtype)
+                b = (torch.randn((K, N), generator=g, device=dev) / K ** 0.5).to(dtype)
+                bias = torch.randn((N,), generator=g, device=dev).to(dtype)
+            else:
+                a, b, bias = W.fused_inputs(M, N, K, seed=0, device=dev, dtype=dtype)
+            ew = {"gelu": lambda y: F.gelu(y, approximate="tanh"), "relu": F.relu, "silu": F.silu}[act]
+            v = [("addmm + torch elementwise", lambda: ew(torch.addmm(bias, a, b)))]
+            if act in ("gelu", "relu"):
+                v.append(("_addmm_activation (hipBLASLt epilogue)",
+                          lambda: torch._addmm_activation(bias, a, b, use_gelu=act == "gelu")))
+            return v
+        return build
+
+    def batched():
+        a, bt = W.batched_inputs(64, 1024, 1024, 128, seed=0, device=dev)
+        bkn = bt.transpose(1, 2).contiguous()  # [B,K,N] contiguous: no transposed right operand
+        return [("torch.bmm", lambda: torch.bmm(a, bkn))]
+
+    def backward():
+        x, w, dy = W.backward_inputs(8192, 4096, 4096, seed=0, device=dev)
+        dyt = dy.t().contiguous()
+        return [("two matmuls (dY^T materialised outside the timed call)",
+                 lambda: (torch.matmul(dy, w), torch.matmul(dyt, x))),
+                ("two matmuls, dY^T as a view", lambda: (torch.matmul(dy, w), torch.matmul(dy.t(), x)))]
+
+    def fp32_bias():
+        g = W._gen(dev, 0)
+        a = torch.randn((512, 4096), generator=g, device=dev) / 64.0
+        b = torch.randn((4096, 4096), generator=g, device=dev) / 64.0
+        bias = torch.randn((4096,), generator=g, device=dev)
+        return [("addmm", lambda: torch.addmm(bias, a, b))]
+
+    def a8w8(M, kind):
+        def build():
+            xq, wq, xs, ws = W.a8w8_inputs(M, 4096, 4096, kind, "pertoken", seed=0, device=dev)
+            if kind == "fp8":
+                wsr = ws.reshape(1, -1).contiguous()
+                return [("_scaled_mm row-wise scales",
+                         lambda: torch._scaled_mm(xq, wq.t(), scale_a=xs, scale_b=wsr, out_dtype=torch.bfloat16))]
+            wsr = ws.reshape(1, -1)
+            return [("torch._int_mm + scales", lambda: (torch._int_mm(xq, wq.t()).float() * xs * wsr).bfloat16())]
+        return build
+
+    return {
+        "fp8_blockscale_2048x7168x4096": fp8(2048),
+        "bf16_gemm_4096": dense(4096),
+        "bf16_gemm_1024": dense(1024),
+        "bf16_gemm_4096_kn": dense(4096, kn=True),
+        "fp16_gemm_bias_gelu_4096": fused("gelu"),
+        "fp16_gemm_bias_relu_4096": fused("relu"),
+        "fp16_gemm_bias_silu_4096": fused("silu"),
+        "bf16_batched_64x1024x1024x128": batched,
+        "bf16_gemm_backward_8192x4096x4096": backward,
+        "fp16_gemm_bias_gelu_512x4096x4096_kn": fused("gelu", 512, 4096, 4096, kn=True),
+        "bf16_gemm_bias_gelu_512x4096x4095_kn": fused("gelu", 512, 4096, 4095, kn=True, dtype=torch.bfloat16),
+        "fp32_gemm_bias_512x4096x4096": fp32_bias,
+        "fp8_blockscale_512x7168x4096": fp8(512),
+        "fp8_blockscale_128x7168x4096": fp8(128),
+        "fp8_blockscale_16x7168x4096": fp8(16),
+        "fp8_a8w8_pertoken_4096": a8w8(4096, "fp8"),
+        "int8_a8w8_4096": a8w8(4096, "int8"),
+        "fp8_a8w8_pertoken_16x4096x4096": a8w8(16, "fp8"),
+    }
+
+
+def _vendor(iters: int, out: str | None = None, cmd: str = "", only: str | None = None,
+            min_warm_s: float = 0.3) -> None:
+    """Time the vendor library on every compute-bound bench configuration, the way
+    ``bench.py`` times this build: at least ``min_warm_s`` of warm-up calls, ``iters``
+    calls between events (eager), the same calls captured in a graph and replayed, and
+    the reference drivers' cold protocol (a 256 MiB ``zero_()`` before each call, median
+    of 10).  A variant the vendor path rejects is recorded as unsupported.  Timing only:
+    the vendor library is run, never read."""
+    import statistics
     import time
 
     import torch
 
     dev = torch.device("cuda")
-    g = torch.Generator(device=dev).manual_seed(0)
-    rn = lambda *s: torch.randn(s, generator=g, device=dev)
-    a, b = rn(4096, 4096).bfloat16(), rn(4096, 4096).bfloat16()
-    a2, b2 = rn(8192, 4096).bfloat16(), rn(4096, 8192).bfloat16()
-    a3, b3, bias = rn(512, 4096), rn(4096, 4096), rn(4096)
-    x8, w8 = rn(2048, 4096).to(torch.float8_e4m3fn), rn(7168, 4096).to(torch.float8_e4m3fn)
-    one = torch.ones((), device=dev)
-    ops = [("bf16 4096^3 A.B^T", lambda: torch.matmul(a, b.t())),
-           ("bf16 8192x8192x4096", lambda: torch.matmul(a2, b2)),
-           ("fp32 512x4096x4096 + bias", lambda: torch.addmm(bias, a3, b3)),
-           ("fp8 2048x7168x4096 per-tensor",
-            lambda: torch._scaled_mm(x8, w8.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16))]
-    for name, fn in ops:
-        t0, w = time.perf_counter(), 0
-        while time.perf_counter() - t0 < min_warm_s:
-            fn()
-            w += 1
-            if w % 64 == 0:
+    flush = torch.empty(256 << 20, dtype=torch.int8, device=dev)
+    rows = []
+    for name, build in _vendor_configs(dev).items():
+        if only and name not in only.split(","):
+            continue
+        variants = build()
+        for label, fn in variants:
+            try:
+                fn()
                 torch.cuda.synchronize()
-        for _ in range(iters):
-            fn()
-        torch.cuda.synchronize()
-        print(f"profiling.vendor {name}: {w} warm-up + {iters} timed calls done", flush=True)
+            except Exception as e:  # noqa: BLE001 -- an unsupported vendor route is a result
+                rows.append((name, label, None, None, None, f"unsupported: {type(e).__name__}: {str(e)[:80]}"))
+                print(f"profiling.vendor {name} / {label}: unsupported ({type(e).__name__})", flush=True)
+                continue
+            t0, n = time.perf_counter(), 0
+            while time.perf_counter() - t0 < min_warm_s:
+                fn()
+                n += 1
+                if n % 32 == 0:
+                    torch.cuda.synchronize()
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(iters):
+                fn()
+            e.record()
+            torch.cuda.synchronize()
+            eager = s.elapsed_time(e) / iters * 1e3
+            graph = None
+            try:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    for _ in range(iters):
+                        fn()
+                g.replay()
+                torch.cuda.synchronize()
+                s.record()
+                for _ in range(3):
+                    g.replay()
+                e.record()
+                torch.cuda.synchronize()
+                graph = s.elapsed_time(e) / (3 * iters) * 1e3
+                del g
+            except Exception:  # noqa: BLE001 -- a route that cannot be captured keeps its eager time
+                graph = None
+            cold = []
+            for _ in range(10):
+                flush.zero_()
+                s.record()
+                fn()
+                e.record()
+                torch.cuda.synchronize()
+                cold.append(s.elapsed_time(e) * 1e3)
+            rows.append((name, label, eager, graph, statistics.median(cold), ""))
+            print(f"profiling.vendor {name} / {label}: eager {eager:.1f} us, graph "
+                  f"{'-' if graph is None else f'{graph:.1f}'} us, cold {statistics.median(cold):.1f} us", flush=True)
+        del variants
+        torch.cuda.empty_cache()
+    if out:
+        lines = ["# Vendor bars on the same box (hipBLASLt / torch; timed, never read)", "",
+                 "Command (from the repository root, on one MI355X):", "", "```", cmd, "```", "",
+                 f"Per variant: {iters} calls between HIP events after at least {min_warm_s} s of warm-up "
+                 "(eager), the same calls captured in a graph and replayed (graph), and the reference "
+                 "drivers' cold protocol (256 MiB `zero_()` before each call, median of 10).  "
+                 "`warm` = the lower of eager and graph, as bench.py reports this build.  The bar of a "
+                 "configuration is its fastest supported variant.", "",
+                 "| configuration | vendor variant | eager (us) | graph (us) | warm (us) | cold (us) | note |",
+                 "|---|---|---|---|---|---|---|"]
+        f = lambda v: "-" if v is None else f"{v:.1f}"  # noqa: E731
+        for name, label, eager, graph, cold, note in rows:
+            warm = None if eager is None else (min(eager, graph) if graph is not None else eager)
+            lines.append(f"| {name} | {label} | {f(eager)} | {f(graph)} | {f(warm)} | {f(cold)} | {note} |")
+        with open(out, "w") as fh:
+            fh.write("\n".join(lines) + "\n")
+        print(f"wrote {out}")
 
 
 def write_vendor(trace_dir: str, out: str, cmd: str, iters: int) -> None:
@@ -522,8 +687,11 @@ def main(argv=None) -> int:
     m.add_argument("--out", default=PMC_FILE)
     m.add_argument("--cmd", required=True)
     m.add_argument("--note", default="")
-    vd = sub.add_parser("vendor", help="run the vendor library's GEMMs on the bar shapes")
+    vd = sub.add_parser("vendor", help="time the vendor library on every compute-bound bench configuration")
     vd.add_argument("--iters", type=int, default=20)
+    vd.add_argument("--out", default=None)
+    vd.add_argument("--cmd", default="")
+    vd.add_argument("--only", default=None)
     vs = sub.add_parser("vendor-stats")
     vs.add_argument("dir")
     vs.add_argument("--out", required=True)
@@ -547,7 +715,7 @@ def main(argv=None) -> int:
     elif a.action == "pmc":
         write_pmc(a)
     elif a.action == "vendor":
-        _vendor(a.iters)
+        _vendor(a.iters, a.out, a.cmd, a.only)
     elif a.action == "vendor-stats":
         write_vendor(a.dir, a.out, a.cmd, a.iters)
     elif a.action == "grounding-passes":
