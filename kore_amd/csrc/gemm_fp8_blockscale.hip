@@ -888,6 +888,254 @@ int launch_fp8_wide(Fp8Params p, hipStream_t st) {
   return check_launch("gemm_fp8_wide_kernel");
 }
 
+// ------------------------------------------------------------------------------
+// K-split block-scale kernel: 128 x 128 tiles, 8 waves, for problems whose 128 x 128
+// grid covers at least three quarters of the CUs (M = 512 at N = 7168: 224 tiles).  The 4-wave
+// 128 x 128 tile puts one wave on each SIMD, whose promotion FMAs then serialise with
+// its own MFMAs; here the two waves of a SIMD own the same 64 x 64 outputs and split
+// the K blocks: waves 0-3 (group 0) take the even blocks, waves 4-7 (group 1) the odd
+// ones, so one wave's promotion runs under the other's MFMAs at the 4-wave tile's
+// fragment traffic per MFMA.  A stage is two consecutive K blocks (one per group) in
+// one LDS slot: A 2 x 128 rows, B 2 x 128 rows, one copy of the weight scales; two
+// slots, one barrier per stage, the xs of four blocks per 16-byte row load in a
+// two-entry ring.  LDS holds the A blocks of both slots, then their B blocks, so every
+// fragment read is a base register plus an immediate offset below 64 KiB.  Each block is promoted once, with its own xs[m, kb] * ws[nb, kb],
+// by the wave that multiplies it; the two partial sums of an output are added once
+// after the K loop (group 0's registers + group 1's, through LDS), so every output
+// is reproducible run to run.  Requires M % 128 == 0, N % 128 == 0, K % 512 == 0 and
+// K-contiguous scale rows.
+// ------------------------------------------------------------------------------
+struct KsCfg {
+  static constexpr int BM = 128, BN = 128, NW = 8, MI = 2, NI = 2, NT = MI * NI;
+  static constexpr int A_BLK = BM * 128, B_BLK = BN * 128;  // one K block
+  static constexpr int A_SLOT = 2 * A_BLK, B_SLOT = 2 * B_BLK;
+  // A block b of slot s at s * A_SLOT + b * A_BLK; B at B_BASE + s * B_SLOT + b * B_BLK;
+  // the ws copy (four blocks) of slot s at W_BASE + s * 1024; the xs ring after them
+  static constexpr int B_BASE = 2 * A_SLOT, W_BASE = B_BASE + 2 * B_SLOT;
+  static constexpr int RING = W_BASE + 2 * 1024;  // xs ring: 2 x (128 rows x 16 B)
+  static constexpr int LDS = RING + 2 * 2048;
+  static constexpr int XCH = 4 * 64 * 64 * 4;                     // epilogue: group 1's partials
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+  static_assert(XCH + 4 * 64 * 64 * 2 <= LDS, "epilogue exchange + staging fit");
+  static_assert(A_SLOT == B_SLOT && A_SLOT + 4 * 1024 < 65536, "fragment immediates below 64 KiB");
+};
+
+__global__ void __launch_bounds__(512) gemm_fp8_ksplit_kernel(const Fp8Params p) {
+  using C = KsCfg;
+  constexpr int MI = C::MI, NI = C::NI, NT = C::NT;
+  constexpr int TB = 2 * (NI - 1);  // barrier tile: the first tile of the last column
+  constexpr int LPS = 4 + 4 + 1;    // per wave and stage: 4 A and 4 B row loads, one scale load
+  constexpr int NU = NT - TB;       // the next-but-one stage's loads go out in tiles TB .. NT-1
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[C::LDS];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2, wq = wave & 3;  // K-block parity, position in the 2 x 2 wave grid
+  const int wm = wq >> 1, wn = wq & 1;
+  const int lr = lane & 31, hh = lane >> 5;
+
+  // XCD-aware raster, groups of kFp8GroupM row tiles sweeping the column tiles
+  const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int width = kFp8GroupM * p.tiles_n;
+  const int gi = bid / width;
+  const int first_m = gi * kFp8GroupM;
+  const int gsz = min(p.tiles_m - first_m, kFp8GroupM);
+  const int tl = bid - gi * width;
+  const int m0 = (first_m + tl % gsz) * C::BM;
+  const int n0 = (tl / gsz) * C::BN;
+  const int nk = p.K / 128, ns = nk / 2;  // K blocks, stages
+
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.xq + (int64_t)m0 * p.ldx, (uint32_t)(C::BM * p.ldx));
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.wq + (int64_t)n0 * p.ldw, (uint32_t)(C::BN * p.ldw));
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(p.xs + (int64_t)m0 * p.xs_m, (uint32_t)(((C::BM - 1) * p.xs_m + (nk - 1) + 1) * 4));
+  const __amdgpu_buffer_rsrc_t rw =
+      make_rsrc(p.ws + (int64_t)(n0 / 128) * p.ws_n, (uint32_t)(((int64_t)nk - 1 + 1) * 4));
+  // DMA: load q of a wave covers 8 rows of the stage's stacked A (or B) region: rows
+  // 8 * (wave + 8 q) + lane / 8 of 256 (block 2s for rows < 128, block 2s+1 above);
+  // row % 32 = 8 * (wave % 4) + lane / 8 for every q, so one chunk key per lane
+  const int lrow = lane >> 3;
+  const int dchunk = (lane & 7) ^ f8_key(8 * (wave & 3) + lrow);
+  const int drow = lrow + 8 * wave;  // tile row of loads 0 and 2 (loads 1 and 3: + 64)
+  const uint32_t a_voff = (uint32_t)(drow * p.ldx + 16 * dchunk);
+  const uint32_t b_voff = (uint32_t)(drow * p.ldw + 16 * dchunk);
+  const uint32_t a_r64 = (uint32_t)(64 * p.ldx), b_r64 = (uint32_t)(64 * p.ldw);
+  const uint32_t x_voff = (uint32_t)(min(64 * wave + lane, C::BM - 1) * p.xs_m * 4);
+
+  // load q of stage st (K blocks 2 st and 2 st + 1) into slot sl; the scale load is the
+  // xs of rows 64 w .. 64 w + 63 for blocks 4 k .. 4 k + 3 (waves 0-1, even stages)
+  // and otherwise the one copy of ws[nb, 4 k .. 4 k + 3] (identical bytes from every
+  // wave that writes it)
+  auto issue = [&](int sl, int st, int q) {
+    const uint32_t kb0 = (uint32_t)(2 * st);
+    if (q < 4) {  // A: q / 2 selects the K block, q % 2 the 64-row half
+      buf_lds(ra, a_voff, (kb0 + (uint32_t)(q >> 1)) * 128u + (uint32_t)(q & 1) * a_r64,
+              lds + sl * C::A_SLOT + (q >> 1) * C::A_BLK + (wave + 8 * (q & 1)) * 1024, 16);
+    } else if (q < 8) {
+      const int r = q - 4;
+      buf_lds(rb, b_voff, (kb0 + (uint32_t)(r >> 1)) * 128u + (uint32_t)(r & 1) * b_r64,
+              lds + C::B_BASE + sl * C::B_SLOT + (r >> 1) * C::B_BLK + (wave + 8 * (r & 1)) * 1024, 16);
+    } else {
+      const bool xload = wave < 2 && (st & 1) == 0;
+      uint8_t* dst = xload ? lds + C::RING + ((st >> 1) & 1) * 2048 + wave * 1024 : lds + C::W_BASE + sl * 1024;
+      buf_lds(xload ? rx : rw, xload ? x_voff : 0u, xload ? kb0 * 4u : (kb0 & ~3u) * 4u, dst, 16);
+    }
+  };
+
+  // fragment reads: row lr of a 32-row block, K half h, 16-byte half e
+  const int key = f8_key(lr);
+  uint32_t ab[2][2], bbv[2][2];
+  f32x16_t acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  f32x16_t part[2];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) part[1][r] = 0.0f;
+  const f32x16_t zero = {};
+  float sc_last = 0.0f, xsv_[MI] = {}, wsv_ = 0.0f;
+  i32x8_t af[MI][2], bf[2][2];
+
+  // prologue: stages 0 and 1 in flight, wait for stage 0
+#pragma unroll
+  for (int q = 0; q < LPS; ++q) issue(0, 0, q);
+#pragma unroll
+  for (int q = 0; q < LPS; ++q) issue(1, min(1, ns - 1), q);
+  wait_vmcnt<LPS>();
+  exec_barrier();
+  const int rowA0 = 64 * wm, colB0 = 64 * wn;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int o = lr * 128 + (((4 * h + 2 * hh + e) ^ key) << 4);
+      ab[h][e] = lds_offset_of(lds + grp * C::A_BLK + rowA0 * 128 + o);
+      bbv[h][e] = lds_offset_of(lds + C::B_BASE + grp * C::B_BLK + colB0 * 128 + o);
+    }
+  const uint32_t xbase = lds_offset_of(lds + C::RING + (rowA0 + lr) * 16);
+  const uint32_t wbase = lds_offset_of(lds + C::W_BASE);
+  af[0][0] = lds_frag32_imm<0>(ab[0]);
+  af[0][1] = lds_frag32_imm<0>(ab[1]);
+  af[1][0] = lds_frag32_imm<32 * 128>(ab[0]);
+  af[1][1] = lds_frag32_imm<32 * 128>(ab[1]);
+  bf[0][0] = lds_frag32_imm<0>(bbv[0]);
+  bf[0][1] = lds_frag32_imm<0>(bbv[1]);
+
+  // one stage; SL: its slot (compile-time)
+  auto stage = [&](int s, auto sl_tag) {
+    constexpr int SL = decltype(sl_tag)::value;
+    constexpr int CUR = SL * C::A_SLOT, NXT = (SL ^ 1) * C::A_SLOT;  // A_SLOT == B_SLOT
+    const int s2 = min(s + 2, ns - 1);
+    const int kb = 2 * s + grp;  // this wave's K block
+    static_for<0, NT>([&](auto tt) {
+      constexpr int t = decltype(tt)::value;
+      constexpr int j = t / MI, i = t % MI;
+      constexpr int bb = j & 1;
+      if constexpr (t == TB) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        wait_vmcnt<0>();
+        exec_barrier();
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      part[t & 1] = mma32_fp8(bf[bb][0], af[i][0], zero);
+      __builtin_amdgcn_sched_barrier(0);
+      {
+        // promote the previous tile (t == 0: the last tile of the previous stage)
+        constexpr int pi = t == 0 ? MI - 1 : (t - 1) % MI, pj = t == 0 ? NI - 1 : (t - 1) / MI;
+        const float f = t == 0 ? sc_last : xsv_[pi] * wsv_;
+        f32x16_t& a = acc[pi][pj];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) a[r] = fmaf(part[(t + 1) & 1][r], f, a[r]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      part[t & 1] = mma32_fp8(bf[bb][1], af[i][1], part[t & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (t == NT - 1) sc_last = xsv_[MI - 1] * wsv_;
+      if constexpr (t == 0) {
+        // this block's scales: xs[m, kb] from the ring, ws[nb, kb] from the slot's copy
+        const uint32_t xo = xbase + (uint32_t)(((s >> 1) & 1) * 2048 + (kb & 3) * 4);
+        xsv_[0] = lds_ldf(xo);
+        xsv_[1] = lds_ldf(xo + 32 * 16);
+        wsv_ = lds_ldf(wbase + (uint32_t)(SL * 1024 + (kb & 3) * 4));
+      }
+      if constexpr (i == 0 && j + 1 < NI) {  // B column j + 1 of this block
+        bf[bb ^ 1][0] = lds_frag32_imm<CUR + 32 * 128 * (j + 1)>(bbv[0]);
+        bf[bb ^ 1][1] = lds_frag32_imm<CUR + 32 * 128 * (j + 1)>(bbv[1]);
+      }
+      if constexpr (t == TB) {  // after the barrier: column 0 and A row tile 0 of the next stage
+        bf[bb ^ 1][0] = lds_frag32_imm<NXT>(bbv[0]);
+        bf[bb ^ 1][1] = lds_frag32_imm<NXT>(bbv[1]);
+        af[0][0] = lds_frag32_imm<NXT>(ab[0]);
+        af[0][1] = lds_frag32_imm<NXT>(ab[1]);
+      }
+      if constexpr (t == NT - 1) {
+        af[1][0] = lds_frag32_imm<NXT + 32 * 128>(ab[0]);
+        af[1][1] = lds_frag32_imm<NXT + 32 * 128>(ab[1]);
+      }
+      // loads of stage s + 2 into this slot, released at this stage's barrier
+      if constexpr (t >= TB) {
+        constexpr int u = t - TB;
+        constexpr int q0 = u * LPS / NU, q1 = (u + 1) * LPS / NU;
+#pragma unroll
+        for (int q = q0; q < q1; ++q) issue(SL, s2, q);
+      }
+    });
+  };
+  for (int s = 0; s < ns; s += 2) {
+    stage(s, std::integral_constant<int, 0>{});
+    stage(s + 1, std::integral_constant<int, 1>{});
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[MI - 1][NI - 1][r] = fmaf(part[(NT - 1) & 1][r], sc_last, acc[MI - 1][NI - 1][r]);
+  wait_vmcnt<0>();  // the clamped trailing loads must land before LDS is reused
+  __syncthreads();
+
+  // group 1 hands its partial sums to group 0 (same outputs, the other K blocks)
+  float* xch = (float*)lds + wq * (64 * 64);
+  if (grp == 1) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xch[((i * NI + j) * 16 + r) * 64 + lane] = acc[i][j][r];
+  }
+  __syncthreads();
+  using St = Stager<64, 64>;
+  using Op = MfmaOp<BF16>;
+  uint16_t* stg = (uint16_t*)(lds + C::XCH) + wq * (64 * 64);
+  if (grp == 0) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e] + xch[((i * NI + j) * 16 + 4 * g + e) * 64 + lane];
+          St::put(stg, out_row(i, lane), out_col(j, g, lane), u32x2_t{Op::pack2(v[0], v[1]), Op::pack2(v[2], v[3])});
+        }
+  }
+  __syncthreads();
+  if (grp == 0) {
+    const int mw0 = m0 + rowA0, nw0 = n0 + colB0;
+    const bool vec = p.vec_store != 0;
+    St::drain(stg, lane, [&](int row, int col, u32x4_t v) {
+      store_row8(p.y + (int64_t)(mw0 + row) * p.ldy + nw0 + col, nw0 + col, p.N, vec, v);
+    });
+  }
+}
+
+int launch_fp8_ksplit(Fp8Params p, hipStream_t st) {
+  p.tiles_m = p.M / KsCfg::BM;
+  p.tiles_n = p.N / KsCfg::BN;
+  hipLaunchKernelGGL(gemm_fp8_ksplit_kernel, dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(512), 0, st, p);
+  return check_launch("gemm_fp8_ksplit_kernel");
+}
+
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // ------------------------------------------------------------------------------
@@ -1207,6 +1455,13 @@ extern "C" int kore_gemm_a8w8_blockscale(const void* xq, int64_t ldx, const void
       return xs4 ? launch_fp8_pipe<F8Cfg<256, 128, 8, 3, true>>(p, st)
                  : launch_fp8_pipe<F8Cfg<256, 128, 8, 3, false>>(p, st);
     }
+    // 128 x 128 tiles: with contiguous scales and at least three quarters of the CUs
+    // covered, the K-split 8-wave kernel (two waves per SIMD) instead of the 4-wave one.
+    // Same process: 512 x 7168 x 4096 24.3 -> 23.4 us, 384 x 7168 x 4096 (168 tiles) 23.5
+    // -> 22.7 us, but 640 x 4096 x 4096 (160 tiles) 21.5 -> 23.1 us.  Both tiles take in
+    // 64 bytes of operands per CU per MFMA-clock at full rate, above what a CU sustains
+    // (about 40 B/clk from L2), so neither reaches the MFMA bound.
+    if (xs4 && M % 128 == 0 && tiles128 >= 3 * cus / 4) return launch_fp8_ksplit(p, st);
     return xs4 ? launch_fp8_pipe<F8Cfg<128, 128, 4, 4, true>>(p, st)
                : launch_fp8_pipe<F8Cfg<128, 128, 4, 4, false>>(p, st);
   }

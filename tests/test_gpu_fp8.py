@@ -66,6 +66,26 @@ def test_fp8_128_tiles(gpu, M, N, K):
     assert bit_equal(out, _run(gpu, xq, wq, xs, ws)), "not reproducible"
 
 
+@pytest.mark.parametrize("M,N,K", [(512, 7168, 4096), (512, 6144, 1024), (512, 7168, 1536), (256, 16384, 1024),
+                                   (512, 7168, 512)])
+def test_fp8_ksplit_tiles(gpu, M, N, K):
+    """128 x 128 tiles covering three quarters of the CUs with contiguous scales run the K-split
+    kernel: the two waves of a SIMD take the even and the odd K blocks of the same outputs
+    and their partial sums are added once after the loop.  Parity at the task tolerance and
+    the 1e-2 bound, bit-exact reruns, and power-of-two scale invariance (each block's scale
+    multiplies its own partial exactly once); K from 4 to 32 blocks (2 to 16 stages).
+    Not bit-equal to the other tile kernels: the even and odd K blocks are summed apart."""
+    xq, wq, xs, ws = W.fp8_inputs(M, N, K, seed=M + N + K, scale=0.2)
+    out = _run(gpu, xq, wq, xs, ws)
+    ref = matmul_blockscale_ref(xq, wq, xs, ws)
+    verdict(out, ref, "blockscale", "fp8", f"{M}x{N}x{K}")
+    verdict(out, ref, "blockscale_genv", "fp8", f"{M}x{N}x{K} (1e-2)")
+    pair_only(out, ref, "fp8", f"{M}x{N}x{K}")
+    assert bit_equal(_run(gpu, xq, wq, xs, ws), out), "not reproducible"
+    assert bit_equal(_run(gpu, xq, wq, xs * 4, ws), out * 4)
+    assert bit_equal(_run(gpu, xq, wq, xs, ws * 0.5), out * 0.5)
+
+
 @pytest.mark.parametrize("M,N,K", [(4000, 3072, 640), (4000, 3072, 512), (3840, 3072, 1024),
                                    (1100, 6016, 512), (1100, 6016, 640), (768, 7168, 1024), (700, 7168, 512)])
 def test_fp8_wide_tiles(gpu, M, N, K):
