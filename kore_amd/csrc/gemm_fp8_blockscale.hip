@@ -782,16 +782,20 @@ __device__ __forceinline__ void fp8_wide_wave(const Fp8Params& p, uint8_t* lds, 
       __builtin_amdgcn_sched_barrier(0);
       part[t & 1] = mma32_fp8(bf[bb][0], af[i][0], zero);
       __builtin_amdgcn_sched_barrier(0);
-      {
-        // promote the previous tile (t == 0: the last tile of the previous block)
-        constexpr int pi = t == 0 ? MI - 1 : (t - 1) % MI, pj = t == 0 ? NI - 1 : (t - 1) / MI;
-        const float f = t == 0 ? sc_last : xsv_[pi] * wsv_[pj];
-        f32x16_t& a = acc[pi][pj];
+      // promote the previous tile (t == 0: the last tile of the previous block), half
+      // on each side of the second MFMA: the FMAs fill the MFMA's dependency shadow
+      // instead of one run of 16 that waits out the first MFMA's result (0.5% on
+      // 2048 x 7168 x 4096, measured)
+      constexpr int pi = t == 0 ? MI - 1 : (t - 1) % MI, pj = t == 0 ? NI - 1 : (t - 1) / MI;
+      const float f = t == 0 ? sc_last : xsv_[pi] * wsv_[pj];
+      f32x16_t& a = acc[pi][pj];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) a[r] = fmaf(part[(t + 1) & 1][r], f, a[r]);
-      }
+      for (int r = 0; r < 8; ++r) a[r] = fmaf(part[(t + 1) & 1][r], f, a[r]);
       __builtin_amdgcn_sched_barrier(0);
       part[t & 1] = mma32_fp8(bf[bb][1], af[i][1], part[t & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int r = 8; r < 16; ++r) a[r] = fmaf(part[(t + 1) & 1][r], f, a[r]);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (t == NT - 1) sc_last = xsv_[MI - 1] * wsv_[NI - 1];
       // LDS reads: this block's scales at t == 0; B column j + 1 at tile (j, 0); after

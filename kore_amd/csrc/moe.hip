@@ -207,9 +207,11 @@ struct MoeGemmParams {
 // out[t] = x[t] @ w[e]^T (gathered rows in, bf16 rows scattered back by token).
 enum { MOE_GATEUP = 0, MOE_DOWN = 1, MOE_PLAIN = 2 };
 
-template <int MODE, int MI, int NI, int WROWS, int WCOLS>
-__device__ __forceinline__ void moe_epilogue(f32x16_t (&acc)[MI][NI], uint16_t* lds, const MoeGemmParams& p, int pos0,
-                                             int n0, int wm, int wn, int wave, int lane) {
+// get(i, j, g, e): element 4g + e of the lane's accumulator of 32x32 tile (i, j), at
+// wave-tile row acc_row<M16>(i, g, lane), column acc_col<M16>(j, g, lane) + e.
+template <int MODE, int MI, int NI, int WROWS, int WCOLS, bool M16, typename Get>
+__device__ __forceinline__ void moe_epilogue_at(Get&& get, uint16_t* lds, const MoeGemmParams& p, int pos0, int n0,
+                                                int wm, int wn, int wave, int lane) {
   using Op = MfmaOp<BF16>;
   if constexpr (MODE == MOE_GATEUP) {
     constexpr int HC = WCOLS / 2;  // h columns per wave
@@ -229,6 +231,7 @@ __device__ __forceinline__ void moe_epilogue(f32x16_t (&acc)[MI][NI], uint16_t* 
       St::put(stg_lo, row, col, u32x2_t{Op::pack2(lo[0], lo[1]), Op::pack2(lo[2], lo[3])});
     };
     if constexpr (NI == 1) {
+      static_assert(!M16, "one 32-column block: the 32x32 layout");
       // one 32-row block: rows 0-15 are gate rows, 16-31 the matching up rows, so
       // register 4g+q (g < 2) holds a gate value and register 8+4g+q its up value
 #pragma unroll
@@ -238,8 +241,8 @@ __device__ __forceinline__ void moe_epilogue(f32x16_t (&acc)[MI][NI], uint16_t* 
           float gt[4], up[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            gt[q] = acc[i][0][4 * g + q];
-            up[q] = acc[i][0][8 + 4 * g + q];
+            gt[q] = get(i, 0, g, q);
+            up[q] = get(i, 0, 2 + g, q);
           }
           put_h(out_row(i, lane), out_col(0, g, lane), gt, up);
         }
@@ -255,10 +258,10 @@ __device__ __forceinline__ void moe_epilogue(f32x16_t (&acc)[MI][NI], uint16_t* 
             float gt[4], up[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              gt[q] = acc[i][j][4 * g + q];
-              up[q] = acc[i][j + NH][4 * g + q];
+              gt[q] = get(i, j, g, q);
+              up[q] = get(i, j + NH, g, q);
             }
-            put_h(out_row(i, lane), out_col(j, g, lane), gt, up);
+            put_h(acc_row<M16>(i, g, lane), acc_col<M16>(j, g, lane), gt, up);
           }
     }
     __syncthreads();
@@ -272,36 +275,48 @@ __device__ __forceinline__ void moe_epilogue(f32x16_t (&acc)[MI][NI], uint16_t* 
   } else if constexpr (MODE == MOE_PLAIN) {
     // rows of this lane -> token (top-1: slot == token); bf16 8-byte stores of 4 columns
 #pragma unroll
-    for (int i = 0; i < MI; ++i) {
-      const int s = p.sorted[pos0 + wm * WROWS + out_row(i, lane)];
-      if (s >= p.S) continue;
-      uint16_t* dst = p.out + (int64_t)s * p.ldo + n0 + wn * WCOLS;
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
-      for (int j = 0; j < NI; ++j)
+      for (int g = 0; g < 4; ++g) {
+        const int s = p.sorted[pos0 + wm * WROWS + acc_row<M16>(i, g, lane)];
+        if (s >= p.S) continue;
+        uint16_t* dst = p.out + (int64_t)s * p.ldo + n0 + wn * WCOLS;
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-          *(u32x2_t*)(dst + out_col(j, g, lane)) =
-              u32x2_t{Op::pack2(acc[i][j][4 * g], acc[i][j][4 * g + 1]),
-                      Op::pack2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3])};
-    }
+        for (int j = 0; j < NI; ++j)
+          *(u32x2_t*)(dst + acc_col<M16>(j, g, lane)) =
+              u32x2_t{Op::pack2(get(i, j, g, 0), get(i, j, g, 1)), Op::pack2(get(i, j, g, 2), get(i, j, g, 3))};
+      }
   } else {
-    // rows of this lane: pos0 + wm*WROWS + i*32 + lane%32 -> slot; fp32 16-byte stores
+    // rows of this lane -> slot, scaled by its routing weight; fp32 16-byte stores
 #pragma unroll
-    for (int i = 0; i < MI; ++i) {
-      const int s = p.sorted[pos0 + wm * WROWS + out_row(i, lane)];
-      if (s >= p.S) continue;
-      const float wgt = p.tw[s];
-      float* dst = p.yw + (int64_t)s * p.Nout + n0 + wn * WCOLS;
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
-      for (int j = 0; j < NI; ++j)
+      for (int g = 0; g < 4; ++g) {
+        const int s = p.sorted[pos0 + wm * WROWS + acc_row<M16>(i, g, lane)];
+        if (s >= p.S) continue;
+        const float wgt = p.tw[s];
+        float* dst = p.yw + (int64_t)s * p.Nout + n0 + wn * WCOLS;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4_t v = {acc[i][j][4 * g] * wgt, acc[i][j][4 * g + 1] * wgt, acc[i][j][4 * g + 2] * wgt,
-                             acc[i][j][4 * g + 3] * wgt};
-          *(f32x4_t*)(dst + out_col(j, g, lane)) = v;
+        for (int j = 0; j < NI; ++j) {
+          const f32x4_t v = {get(i, j, g, 0) * wgt, get(i, j, g, 1) * wgt, get(i, j, g, 2) * wgt,
+                             get(i, j, g, 3) * wgt};
+          *(f32x4_t*)(dst + acc_col<M16>(j, g, lane)) = v;
         }
-    }
+      }
   }
+}
+
+template <int MODE, int MI, int NI, int WROWS, int WCOLS>
+__device__ __forceinline__ void moe_epilogue(f32x16_t (&acc)[MI][NI], uint16_t* lds, const MoeGemmParams& p, int pos0,
+                                             int n0, int wm, int wn, int wave, int lane) {
+  moe_epilogue_at<MODE, MI, NI, WROWS, WCOLS, false>([&](int i, int j, int g, int e) { return acc[i][j][4 * g + e]; },
+                                                     lds, p, pos0, n0, wm, wn, wave, lane);
+}
+template <int MODE, int MI, int NI, int WROWS, int WCOLS>
+__device__ __forceinline__ void moe_epilogue16(f32x4_t (&c4)[MI][NI][4], uint16_t* lds, const MoeGemmParams& p,
+                                               int pos0, int n0, int wm, int wn, int wave, int lane) {
+  moe_epilogue_at<MODE, MI, NI, WROWS, WCOLS, true>([&](int i, int j, int g, int e) { return c4[i][j][g][e]; }, lds,
+                                                    p, pos0, n0, wm, wn, wave, lane);
 }
 
 template <int MODE, int BM, int BN, int WM, int WN>
@@ -368,13 +383,20 @@ __global__ void __launch_bounds__(kEngineThreads)
 // Prefill path on the buffer-load pipelined engine: A rows (gathered tokens for
 // gate_up, H planes for down) and B rows (interleaved gate/up rows of w1[e], rows of
 // w2[e]) become per-lane byte offsets of buffer resources, fixed for the whole K loop.
-template <int MODE, int BM, int BN>
-__global__ void __launch_bounds__(256)
+// NWV = 8: 16x16x32 MFMAs on a 2 x 4 wave grid (two waves per SIMD); NWV = 4: 32x32x16
+// MFMAs on 2 x 2.  Fused MoE E=8 top-2 D=4096 I=14336, same process: T=4096 3.93 ->
+// 3.83 ms, T=16384 13.43 -> 12.94 ms with both projections on 8 waves (gate_up alone
+// is bit-equal to the 4-wave kernel; down, with two A planes per sub-step, sums in
+// another order).  The plain grouped GEMM stays on 4 waves: on 8 it measured 117 ->
+// 124 us at M=4096, E=32, N=2048, K=4096 (jagged routing) and 204 -> 211 us at
+// 8192 x 16 x 1536 x 4096.
+template <int MODE, int BM, int BN, int NWV>
+__global__ void __launch_bounds__(64 * NWV)
     moe_buf_kernel(const MoeGemmParams p) {
   constexpr int AP = (MODE == MOE_DOWN) ? 2 : 1;
   // grouped (plain) GEMM: an expert's weight tile is read by that expert's row blocks
   // only, running side by side on one XCD (L2), so its loads are non-temporal
-  using E = BufPipeEngine<BF16, BM, BN, 2, 2, AP, B_KC, MODE == MOE_PLAIN ? kCpolNT : kCpolDefault>;
+  using E = BufPipeEngine<BF16, BM, BN, 2, NWV / 2, AP, B_KC, MODE == MOE_PLAIN ? kCpolNT : kCpolDefault, NWV == 8>;
   constexpr int MI = E::MI, NI = E::NI;
   __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -448,10 +470,17 @@ __global__ void __launch_bounds__(256)
     }
   }
 
-  f32x16_t acc[MI][NI];
-  E::zero(acc);
-  eng.mainloop(lds, p.K, acc);
-  moe_epilogue<MODE, MI, NI, E::WROWS, E::WCOLS>(acc, lds, p, pos0, n0, wm, wn, wave, lane);
+  if constexpr (E::M16) {
+    f32x4_t acc[MI][NI][4];
+    E::zero16(acc);
+    eng.mainloop16(lds, p.K, acc);
+    moe_epilogue16<MODE, MI, NI, E::WROWS, E::WCOLS>(acc, lds, p, pos0, n0, wm, wn, wave, lane);
+  } else {
+    f32x16_t acc[MI][NI];
+    E::zero(acc);
+    eng.mainloop(lds, p.K, acc);
+    moe_epilogue<MODE, MI, NI, E::WROWS, E::WCOLS>(acc, lds, p, pos0, n0, wm, wn, wave, lane);
+  }
 }
 
 // Down projection grid: workgroup b runs on XCD b % 8 (round-robin dispatch), so XCD x
@@ -657,7 +686,8 @@ int launch_moe_buf(MoeGemmParams p, int64_t cap, hipStream_t st) {
   p.max_mblocks = (int)(cap / BM);
   const int64_t blocks = (int64_t)p.max_mblocks * p.ntiles;
   if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "fused_moe: grid too large");
-  hipLaunchKernelGGL((moe_buf_kernel<MODE, BM, BN>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+  constexpr int NWV = MODE == MOE_PLAIN ? 4 : 8;
+  hipLaunchKernelGGL((moe_buf_kernel<MODE, BM, BN, NWV>), dim3((unsigned)blocks), dim3(64 * NWV), 0, st, p);
   return check_launch(MODE == MOE_GATEUP ? "moe_gateup_buf_kernel" : "moe_down_buf_kernel");
 }
 
