@@ -85,7 +85,7 @@ def moe_ref(hidden, w1, w2, topk_weight, topk_ids) -> torch.Tensor:
     x = hidden.float()
     w1f = w1.float()
     w2f = w2.float()
-    out = torch.zeros((T, D), dtype=torch.float32, device=hidden.device)  # CPU, or a device fp32 reference
+    out = torch.zeros((T, D), dtype=torch.float32)
     ids = topk_ids.long()
     tw = topk_weight.float()
     for e in range(E):
