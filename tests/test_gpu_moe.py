@@ -66,6 +66,26 @@ def test_fused_moe_prefill_tiles(gpu, T, E, topk, D, I):
     verdict(out, ref, "north_star", "bf16", f"prefill tiles T{T} (1e-2)")
 
 
+@pytest.mark.parametrize("D", [512, 384])
+def test_fused_moe_prefill_skewed(gpu, D):
+    """256-row prefill tiles under skewed routing: one expert takes about two thirds of
+    the 6000 slots (15 blocks, so its rows are split over several column-sweeping
+    groups), experts 2, 4 and 7 receive nothing (empty experts between busy ones), the
+    rest a few blocks each; D = 512 runs the two-plane down on 128x256 tiles, D = 384
+    the 128x128 register-staged tiles."""
+    T, E, topk, I = 3000, 8, 2, 384
+    counts = torch.tensor([16053.0, 105.0, 0.0, 2724.0, 0.0, 88.0, 4102.0, 0.0])
+    bias = torch.log(counts + 1e-6)
+    bias[counts == 0] = float("-inf")
+    hidden, w1, w2, tw, ti = W.moe_inputs(T, E, topk, D, I, seed=7, wscale=0.05, router_bias=bias)
+    used = torch.bincount(ti.flatten(), minlength=E)
+    assert used[2] == 0 and used[4] == 0 and used[7] == 0 and used[0] > 6 * 256
+    out = kore_amd.fused_moe(*[t.to(gpu) for t in (hidden, w1, w2, tw, ti)])
+    ref = moe_ref(hidden, w1, w2, tw, ti)
+    verdict(out, ref, "fused_moe", "bf16", f"prefill skewed T{T} D{D}")
+    verdict(out, ref, "north_star", "bf16", f"prefill skewed T{T} D{D} (1e-2)")
+
+
 @pytest.mark.parametrize("T,E,topk,D,I", [(300, 4, 1, 256, 384), (500, 8, 2, 512, 256), (200, 4, 2, 384, 640),
                                           (1024, 32, 2, 768, 512)])
 def test_fused_moe_128row_blocks(gpu, T, E, topk, D, I):
