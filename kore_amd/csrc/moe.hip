@@ -213,6 +213,9 @@ template <int MODE, int MI, int NI, int WROWS, int WCOLS, bool M16, typename Get
 __device__ __forceinline__ void moe_epilogue_at(Get&& get, uint16_t* lds, const MoeGemmParams& p, int pos0, int n0,
                                                 int wm, int wn, int wave, int lane) {
   using Op = MfmaOp<BF16>;
+  // a lane's rows in a 32-row block: one (32x32 layout: groups g = 0..3 share it) or two
+  // (16x16 sub-tiles: g = 2 sm + sn, row set by sm)
+  constexpr int NR = M16 ? 2 : 1, GPR = 4 / NR;
   if constexpr (MODE == MOE_GATEUP) {
     constexpr int HC = WCOLS / 2;  // h columns per wave
     using St = Stager<WROWS, HC>;
@@ -277,31 +280,35 @@ __device__ __forceinline__ void moe_epilogue_at(Get&& get, uint16_t* lds, const 
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int s = p.sorted[pos0 + wm * WROWS + acc_row<M16>(i, g, lane)];
+      for (int r = 0; r < NR; ++r) {
+        const int s = p.sorted[pos0 + wm * WROWS + acc_row<M16>(i, r * GPR, lane)];
         if (s >= p.S) continue;
         uint16_t* dst = p.out + (int64_t)s * p.ldo + n0 + wn * WCOLS;
 #pragma unroll
         for (int j = 0; j < NI; ++j)
-          *(u32x2_t*)(dst + acc_col<M16>(j, g, lane)) =
-              u32x2_t{Op::pack2(get(i, j, g, 0), get(i, j, g, 1)), Op::pack2(get(i, j, g, 2), get(i, j, g, 3))};
+#pragma unroll
+          for (int g = r * GPR; g < (r + 1) * GPR; ++g)
+            *(u32x2_t*)(dst + acc_col<M16>(j, g, lane)) =
+                u32x2_t{Op::pack2(get(i, j, g, 0), get(i, j, g, 1)), Op::pack2(get(i, j, g, 2), get(i, j, g, 3))};
       }
   } else {
     // rows of this lane -> slot, scaled by its routing weight; fp32 16-byte stores
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int s = p.sorted[pos0 + wm * WROWS + acc_row<M16>(i, g, lane)];
+      for (int r = 0; r < NR; ++r) {
+        const int s = p.sorted[pos0 + wm * WROWS + acc_row<M16>(i, r * GPR, lane)];
         if (s >= p.S) continue;
         const float wgt = p.tw[s];
         float* dst = p.yw + (int64_t)s * p.Nout + n0 + wn * WCOLS;
 #pragma unroll
-        for (int j = 0; j < NI; ++j) {
-          const f32x4_t v = {get(i, j, g, 0) * wgt, get(i, j, g, 1) * wgt, get(i, j, g, 2) * wgt,
-                             get(i, j, g, 3) * wgt};
-          *(f32x4_t*)(dst + acc_col<M16>(j, g, lane)) = v;
-        }
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+          for (int g = r * GPR; g < (r + 1) * GPR; ++g) {
+            const f32x4_t v = {get(i, j, g, 0) * wgt, get(i, j, g, 1) * wgt, get(i, j, g, 2) * wgt,
+                               get(i, j, g, 3) * wgt};
+            *(f32x4_t*)(dst + acc_col<M16>(j, g, lane)) = v;
+          }
       }
   }
 }
