@@ -43,6 +43,7 @@ struct TileParams {
   int batch;  // number of batches (the persistent short-K kernel walks all of them)
   int kb;     // valid K-rows of an N-contiguous B on the direct-to-LDS engines (rows
               // from kb on fall outside the buffer resource and read as zero)
+  int kreal;  // K-tail mode of the buffer engine: the true K (K is then rounded up to 64)
   int act;
   int vec_store;  // 16-byte C stores allowed (ldc % 8 == 0, aligned)
   int bias_vec;   // bias is 8-byte aligned: 4-wide bias loads allowed
@@ -184,6 +185,7 @@ template <typename E, int BM, int BN, int BL>
 __device__ __forceinline__ void setup_operands(E& eng, const TileParams& p, int batch, int m0, int n0, int wave,
                                                int lane) {
   const int rows_a = min(BM, p.M - m0), rows_b = min(BN, p.N - n0);
+  const int kv = p.kreal > 0 ? p.kreal : p.K;  // K the operands hold
   if constexpr (E::AMC) {
     // M-contiguous A (element (m, k) at a[k * lda + m], M % 8 == 0): K-rows of the tile's
     // BM columns; chunks past M re-read the last one (their rows are never stored)
@@ -197,7 +199,7 @@ __device__ __forceinline__ void setup_operands(E& eng, const TileParams& p, int 
     }
   } else {
     const uint16_t* A = p.a + batch * p.sa + (int64_t)m0 * p.lda;
-    eng.ra = make_rsrc(A, (uint32_t)(((int64_t)(rows_a - 1) * p.lda + p.K) * 2));
+    eng.ra = make_rsrc(A, (uint32_t)(((int64_t)(rows_a - 1) * p.lda + kv) * 2));
 #pragma unroll
     for (int j = 0; j < E::AJ; ++j) {
       const int r = E::a_row(wave, lane, j);
@@ -206,7 +208,7 @@ __device__ __forceinline__ void setup_operands(E& eng, const TileParams& p, int 
   }
   if constexpr (BL == B_KC) {
     const uint16_t* B = p.b + batch * p.sb + (int64_t)n0 * p.ldb;
-    eng.rb = make_rsrc(B, (uint32_t)(((int64_t)(rows_b - 1) * p.ldb + p.K) * 2));
+    eng.rb = make_rsrc(B, (uint32_t)(((int64_t)(rows_b - 1) * p.ldb + kv) * 2));
 #pragma unroll
     for (int j = 0; j < E::BJ; ++j) {
       const int r = E::b_row(wave, lane, j);
@@ -233,7 +235,8 @@ __device__ __forceinline__ void setup_operands(E& eng, const TileParams& p, int 
 // reads with the nc_x16 chunk swizzle.  NWV = 4 (N-contiguous B over several rounds of the
 // CUs, see launch_buf): 4 waves of 128 x 128 on 32x32x16 with the nc_x swizzle.  AL = A_MC: A
 // is M-contiguous (a transposed view) and read like an N-contiguous B (8 waves only).
-template <typename T, int BM, int BN, int BL, int NWV, int AL>
+// KT: K tails (K % 64 != 0) read in place on the 16x16 engine (mainloop16<true>).
+template <typename T, int BM, int BN, int BL, int NWV, int AL, bool KT = false>
 __global__ void __launch_bounds__(64 * NWV)
     gemm_buf_kernel(const TileParams p) {
   using E = BufPipeEngine<T, BM, BN, 2, NWV / 2, 1, BL, kCpolDefault, NWV == 8 || BL == B_KC, AL>;
@@ -245,12 +248,18 @@ __global__ void __launch_bounds__(64 * NWV)
   tile_coords(p, BM, BN, batch, m0, n0);
   E eng;
   setup_operands<E, BM, BN, BL>(eng, p, batch, m0, n0, wave, lane);
+  if constexpr (KT) {  // last stage at K - 64 (bytes along a row / over N-contiguous K-rows)
+    eng.a_klast = (uint32_t)((p.kreal - kBK) * 2);
+    eng.b_klast = BL == B_NC ? (uint32_t)((int64_t)(p.kreal - kBK) * p.ldb * 2) : eng.a_klast;
+    eng.kdup = p.K - p.kreal;
+  }
   if constexpr (E::M16) {
     f32x4_t acc[MI][NI][4];
     E::zero16(acc);
-    eng.mainloop16(lds, p.K, acc);
+    eng.template mainloop16<KT>(lds, p.K, acc);
     dense_epilogue16<T, MI, NI, E::WROWS, E::WCOLS>(acc, lds, p, m0, n0, wm, wn, wave, lane, p.c + batch * p.sc);
   } else {
+    static_assert(!KT, "K tails run on the 16x16 engine");
     f32x16_t acc[MI][NI];
     E::zero(acc);
     eng.mainloop(lds, p.K, acc);
@@ -934,7 +943,7 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 template <typename T, int BL, int BM, int BN>
 int launch_tile(const GemmDesc& d, hipStream_t stream) {
-  TileParams p;
+  TileParams p{};
   p.a = (const uint16_t*)d.a;
   p.b = (const uint16_t*)d.b;
   p.bias = (const uint16_t*)d.bias;
@@ -962,9 +971,11 @@ int launch_tile(const GemmDesc& d, hipStream_t stream) {
 }
 
 
-template <typename T, int BM, int BN, int BL, int AL = A_KC>
+// KT: K % 64 != 0, rows of any 2-byte alignment, read in place (K-tail mode of the
+// 16x16 engine: the loop runs over K rounded up to 64, the last stage starts at K - 64).
+template <typename T, int BM, int BN, int BL, int AL = A_KC, bool KT = false>
 int launch_buf(const GemmDesc& d, hipStream_t stream) {
-  TileParams p;
+  TileParams p{};
   p.a = (const uint16_t*)d.a;
   p.b = (const uint16_t*)d.b;
   p.bias = (const uint16_t*)d.bias;
@@ -992,6 +1003,12 @@ int launch_buf(const GemmDesc& d, hipStream_t stream) {
     hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 8, A_MC>), dim3((unsigned)blocks), dim3(512), 0, stream, p);
     return check_launch("gemm_buf_kernel");
   }
+  if constexpr (KT) {
+    p.kreal = (int)d.K;
+    p.K = (int)((d.K + kBK - 1) / kBK * kBK);
+    hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 8, A_KC, true>), dim3((unsigned)blocks), dim3(512), 0, stream, p);
+    return check_launch("gemm_buf_kernel");
+  }
   // 8 waves on 16x16x32 MFMAs, except for an N-contiguous B whose grid needs more than one
   // round of the CUs: there the 4-wave 32x32x16 tile measured 1-4% faster under the cold
   // protocol (8192 x 4096 x 4096: 221 against 224-228 us; 8192 x 8192 x 4096: 427-429
@@ -1010,7 +1027,7 @@ int launch_buf(const GemmDesc& d, hipStream_t stream) {
 
 template <typename T, int BM, int BN, int WM, int WN, int NSLOT, int BL>
 int launch_deep(const GemmDesc& d, hipStream_t stream) {
-  TileParams p;
+  TileParams p{};
   p.a = (const uint16_t*)d.a;
   p.b = (const uint16_t*)d.b;
   p.bias = (const uint16_t*)d.bias;
@@ -1042,7 +1059,7 @@ int launch_deep(const GemmDesc& d, hipStream_t stream) {
 // Persistent short-K launch: one 128 KiB-LDS workgroup per CU, at most one per tile.
 template <typename T, int BL>
 int launch_shortk(const GemmDesc& d, hipStream_t stream) {
-  TileParams p;
+  TileParams p{};
   p.a = (const uint16_t*)d.a;
   p.b = (const uint16_t*)d.b;
   p.bias = nullptr;
@@ -1082,7 +1099,7 @@ int launch_shortk(const GemmDesc& d, hipStream_t stream) {
 template <typename T>
 int launch_ring(const GemmDesc& d, hipStream_t stream) {
   constexpr int BM = 32, BN = 128, NSLOT = 7;
-  TileParams p;
+  TileParams p{};
   p.a = (const uint16_t*)d.a;
   p.b = (const uint16_t*)d.b;
   p.bias = (const uint16_t*)d.bias;
@@ -1296,6 +1313,21 @@ int dispatch_typed(const GemmDesc& d, Ws& ws, hipStream_t stream) {
   // engine, read in place through LDS transpose reads; smaller grids pack A instead.
   const bool a_mc = d.sam == 1 && d.sak % 8 == 0 && aligned16(d.a) && d.sa % 8 == 0 && d.M % 8 == 0 &&
                     d.K % 64 == 0 && d.K > 256 && d.sak * 2 * d.K + 512 < (1ll << 31);
+  // K tails (K % 64 != 0, e.g. 4095) on the 256x256 grid: the 16x16 engine reads A and B
+  // in place -- direct-to-LDS loads take rows at any 2-byte alignment -- and its last
+  // stage starts at K - 64, with the columns it repeats zeroed in LDS (mainloop16<true>),
+  // instead of a pack pass over A (4096 x 4096 x 4095 with the task's [K,N] B: 16 us).
+  if (d.K % 64 != 0 && d.K > 64 && d.sak == 1 && fits32 && pick_tile(d) == TILE_256x256 &&
+      d.sam * 2 * 256 + d.K * 2 < (1ll << 31)) {
+    const bool kc = d.sbk == 1 && d.sbn * 2 * 256 + d.K * 2 < (1ll << 31);
+    const bool nc = d.sbn == 1 && d.sbk % 8 == 0 && aligned16(d.b) && d.sb % 8 == 0 && d.N % 8 == 0 &&
+                    d.sbk * 2 * d.K + d.N * 2 < (1ll << 31);
+    if (kc || nc) {
+      if (ws.plan) return KORE_OK;
+      return kc ? launch_buf<T, 256, 256, B_KC, A_KC, true>(d, stream)
+                : launch_buf<T, 256, 256, B_NC, A_KC, true>(d, stream);
+    }
+  }
   if (a_mc && fits32 && pick_tile(d) == TILE_256x256 &&
       ((b_kc && d.sbn * 2 * 256 + d.K * 2 < (1ll << 31)) || (b_nc && d.sbk * 2 * d.K + d.N * 2 < (1ll << 31)))) {
     if (ws.plan) return KORE_OK;

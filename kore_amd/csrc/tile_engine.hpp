@@ -444,6 +444,32 @@ struct BufPipeEngine {
   uint32_t a_voff[AJ], b_voff[BJ];      // bytes: row * row_stride + 16 * chunk
   uint32_t b_kstep;                     // NC: bytes of B between consecutive 64-row K stages
   uint32_t a_kstep;                     // A_MC: bytes of A between consecutive 64-row K stages
+  // K tail (mainloop16<true>, K % 64 != 0): the last stage is read from K - 64 (a_klast,
+  // b_klast: scalar byte offsets of A / K-contiguous B and of an N-contiguous B) instead
+  // of 64 (nk - 1), so no load passes K; its first kdup = 64 nk - K columns, which the
+  // stage before already covered, are zeroed in LDS in both operands before any read.
+  uint32_t a_klast, b_klast;
+  int kdup;
+
+  static constexpr bool nk_tail_ok() { return AP == 1 && !AMC; }
+
+  // Zero K columns [0, kdup) of both operands of the stage at st (every thread takes part).
+  __device__ __forceinline__ void zero_dup(uint16_t* st) const {
+    static_assert(AP == 1 && !AMC, "K tails: one K-contiguous A plane");
+    const int tid = threadIdx.x;
+    for (int idx = tid; idx < BM * kdup; idx += NW * 64) {
+      const int r = idx / kdup, k = idx - r * kdup;
+      st[r * kBK + (((k >> 3) ^ row_key(r)) << 3) + (k & 7)] = 0;
+    }
+    if constexpr (NC) {
+      for (int idx = tid; idx < kdup * BN; idx += NW * 64) st[B_OFF + idx] = 0;  // whole K-rows
+    } else {
+      for (int idx = tid; idx < BN * kdup; idx += NW * 64) {
+        const int r = idx / kdup, k = idx - r * kdup;
+        st[B_OFF + r * kBK + (((k >> 3) ^ row_key(r)) << 3) + (k & 7)] = 0;
+      }
+    }
+  }
 
   __device__ __forceinline__ void issue_one(uint16_t* lds, int slot, uint32_t soff, uint32_t soffb, int wave,
                                             int q) {
@@ -593,6 +619,8 @@ struct BufPipeEngine {
 #pragma unroll
         for (int g = 0; g < 4; ++g) c4[i][j][g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
+  // KT: K tail mode (K here is the padded length 64 nk; see a_klast / kdup).
+  template <bool KT = false>
   __device__ __forceinline__ void mainloop16(uint16_t* lds, int K, f32x4_t (&c4)[MI][NI][4]) {
     using Op = MfmaOp<T>;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -665,16 +693,30 @@ struct BufPipeEngine {
     constexpr int NMMA = AP * MI * NI * 4;  // MFMAs per sub-step
     constexpr int NRD = NFA + NFB;          // fragment reads per sub-step
     static_assert(NRD <= NMMA && LPS <= NMMA && LPS <= 32, "interleave needs enough MFMAs; vmcnt range");
+    static_assert(!KT || nk_tail_ok(), "K tails: one K-contiguous A plane");
     const uint32_t kmax = (uint32_t)(nk - 1) * (kBK * 2);
-    auto soff_of = [&](int stage) { return min((uint32_t)stage * (kBK * 2), kmax); };
-    auto soffb_of = [&](int stage) { return NC ? (uint32_t)min(stage, nk - 1) * b_kstep : soff_of(stage); };
+    auto soff_of = [&](int stage) -> uint32_t {
+      if constexpr (KT) return stage >= nk - 1 ? a_klast : (uint32_t)stage * (kBK * 2);
+      else return min((uint32_t)stage * (kBK * 2), kmax);
+    };
+    auto soffb_of = [&](int stage) -> uint32_t {
+      if constexpr (KT && NC) return stage >= nk - 1 ? b_klast : (uint32_t)stage * b_kstep;
+      else return NC ? (uint32_t)min(stage, nk - 1) * b_kstep : soff_of(stage);
+    };
     auto soffa_of = [&](int stage) { return AMC ? (uint32_t)min(stage, nk - 1) * a_kstep : soff_of(stage); };
 #pragma unroll
-    for (int q = 0; q < LPS; ++q) issue_one(lds, 0, 0u, 0u, wave, q);
+    for (int q = 0; q < LPS; ++q) issue_one(lds, 0, soffa_of(0), soffb_of(0), wave, q);
 #pragma unroll
     for (int q = 0; q < LPS; ++q) issue_one(lds, 1, soffa_of(1), soffb_of(1), wave, q);
     wait_vmcnt<LPS>();
     exec_barrier();
+    if constexpr (KT) {
+      if (nk == 1) {  // the only stage is the last one
+        zero_dup(lds);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        exec_barrier();
+      }
+    }
     // A fragments are single-buffered: A block (pl, i, half sm) of the next sub-step is
     // read right after its last MFMA in this one (tile j = NI - 1, sub-tile g = 2 sm + 1),
     // at least (MI - 1) * NI * 4 MFMAs before its first use; B fragments are double-
@@ -694,6 +736,13 @@ struct BufPipeEngine {
           asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
           wait_vmcnt<0>();
           exec_barrier();
+          if constexpr (KT) {
+            if (s == nk - 2) {  // stage s + 1 is the last: zero its repeated columns first
+              zero_dup(lds + (slot ^ 1) * STAGE);
+              asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+              exec_barrier();
+            }
+          }
         }
         const int rslot = ks == 0 ? slot : (slot ^ 1);
         const int rks = ks == 0 ? 1 : 0;

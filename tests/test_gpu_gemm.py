@@ -63,11 +63,38 @@ def test_gemm_ring_small(gpu, M, N, K, dtype, op):
                                    (513, 1000, 200), (4096, 4096, 4096)])
 def test_gemm_reference_task_shapes(gpu, M, N, K):
     """gemm_bf16 task.yaml shapes (kore/tasks/gemm_bf16/task.yaml:8-14) with the task's
-    natural N-contiguous B, plus a ragged shape; K = 4095 takes the packed path (A padded
-    into the caller's workspace, B read in place up to its last real K-row)."""
+    natural N-contiguous B, plus a ragged shape; K = 4095 takes the in-place K-tail path
+    (A rows read at 2-byte alignment, last stage from K - 64)."""
     a, b = _ref_style_inputs(M, N, K, seed=1)
     out = kore_amd.gemm(a.to(gpu), b.to(gpu))
     verdict(out, matmul_ref(a, b), "gemm", "bf16", f"{M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("K", [4095, 4033, 1000, 127, 65])
+@pytest.mark.parametrize("layout", ["kn", "bt"])
+def test_gemm_k_tail_in_place(gpu, K, layout):
+    """K % 64 != 0 on the 256x256 grid (3072 x 4096: 192 tiles): the 16x16 engine reads A
+    and B in place (rows at 2-byte alignment when K is odd) and starts its last 64-wide
+    stage at K - 64; the 64 * ceil(K / 64) - K columns that stage shares with the one
+    before (1 for K = 4095 and 127, 63 for 4033 and 65, 24 for 1000) are zeroed in LDS in
+    both operands.  Column K - 64, inside that shared region, holds 4 in every row of A
+    and every column of B (16 per output, against outputs of about unit size), so
+    counting it twice, or missing it, fails the oracle check.  B: the task's [K,N] layout (kn) or W.t() of a [N,K] W (bt, rows of K
+    elements)."""
+    M, N = 3072, 4096
+    g = torch.Generator().manual_seed(K)
+    a = (torch.randn((M, K), generator=g) / K ** 0.5).to(torch.bfloat16)
+    w = torch.randn((N, K), generator=g).to(torch.bfloat16)
+    a[:, K - 64] = 4.0
+    w[:, K - 64] = 4.0
+    b = w.t().contiguous() if layout == "kn" else w.t()
+    bd = w.t().contiguous().to(gpu) if layout == "kn" else w.to(gpu).t()
+    out = kore_amd.gemm(a.to(gpu), bd)
+    ref = matmul_ref(a, b)
+    verdict(out, ref, "gemm", "bf16", f"K tail {K} {layout}")
+    pair_only(out, ref, "bf16", f"K tail {K} {layout}")
+    out2 = kore_amd.gemm(a.to(gpu), bd)
+    assert bit_equal(out, out2), "determinism"
 
 
 @pytest.mark.parametrize("M,N,K,dtype,op", [(4096, 4096, 4096, torch.bfloat16, "gemm_bias_gelu"),

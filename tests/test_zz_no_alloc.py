@@ -83,8 +83,9 @@ def test_noalloc_rejects_oversized_scratch(gpu):
     lib = _lib.load()
     cap = lib.kore_gemm_noalloc_scratch_bytes()
     assert cap == 64 << 20
-    # 8200 x 1024 x 4095 with an unaligned K: A packs to 8200 x 4096 bf16 (65.6 MB > 64 MiB)
-    a = torch.zeros((8200, 4095), dtype=torch.bfloat16, device=gpu)
+    # 8200 x 1024 x 4095 with A an M-contiguous view and an unaligned K: A packs to
+    # 8200 x 4096 bf16 (65.6 MB > 64 MiB)
+    a = torch.zeros((4095, 8200), dtype=torch.bfloat16, device=gpu).t()
     b = torch.zeros((4095, 1024), dtype=torch.bfloat16, device=gpu)
     rc, c = _noalloc(a, b, None, "none")
     assert rc == 4, rc
