@@ -43,6 +43,7 @@ struct F32Params {
   int act;
   int vec_store;
   int kb;  // ring kernel, N-contiguous B: K-rows that exist (rows from kb on read as 0)
+  int kreal;  // ring kernel K-tail mode: the true K (K is then rounded up to 32)
 };
 
 constexpr int kF32BK = 64;          // K values per stage
@@ -421,7 +422,10 @@ int launch_pack32(const float* in, int64_t sr, int64_t sk, float* out, int64_t R
 // ---------------------------------------------------------------------------------
 constexpr int kF32RK = 32;  // K floats per ring stage
 
-template <int BM, int BN, int NSLOT, bool BNC>
+// KT: K % 32 != 0 read in place (rows at 4-byte alignment): the loop runs over K rounded
+// up to 32, the last stage is read from K - 32 (no load passes K), and the columns it
+// shares with the stage before are zeroed in LDS in both operands once it has landed.
+template <int BM, int BN, int NSLOT, bool BNC, bool KT = false>
 __global__ void __launch_bounds__(256) gemm_f32_ring_kernel(const F32Params p) {
   constexpr int WM = BM / 2, WN = BN / 2, MI = WM / 32, NI = WN / 32;
   static_assert(MI >= 1 && NI >= 1, "wave tile");
@@ -440,14 +444,15 @@ __global__ void __launch_bounds__(256) gemm_f32_ring_kernel(const F32Params p) {
   const int m0 = (bid % p.tiles_m) * BM, n0 = (bid / p.tiles_m) * BN;
   const int rows_a = min(BM, p.M - m0), rows_b = min(BN, p.N - n0);
   const int nk = p.K / kF32RK;
+  const int kv = KT ? p.kreal : p.K;  // K the operands hold
 
   // buffer resources and per-lane byte offsets (rows past the tile re-read its last row,
   // chunks past N re-read the last chunk: they only feed outputs that are never stored)
   const __amdgpu_buffer_rsrc_t ra =
-      make_rsrc(p.a + (int64_t)m0 * p.lda, (uint32_t)(((int64_t)(rows_a - 1) * p.lda + p.K) * 4));
+      make_rsrc(p.a + (int64_t)m0 * p.lda, (uint32_t)(((int64_t)(rows_a - 1) * p.lda + kv) * 4));
   const __amdgpu_buffer_rsrc_t rb =
       BNC ? make_rsrc(p.b + n0, (uint32_t)(((int64_t)(p.kb - 1) * p.ldb + rows_b) * 4))
-          : make_rsrc(p.b + (int64_t)n0 * p.ldb, (uint32_t)(((int64_t)(rows_b - 1) * p.ldb + p.K) * 4));
+          : make_rsrc(p.b + (int64_t)n0 * p.ldb, (uint32_t)(((int64_t)(rows_b - 1) * p.ldb + kv) * 4));
   uint32_t a_voff[AJ], b_voff[BJ];
 #pragma unroll
   for (int j = 0; j < AJ; ++j) {
@@ -465,15 +470,37 @@ __global__ void __launch_bounds__(256) gemm_f32_ring_kernel(const F32Params p) {
     }
   }
   const uint32_t b_kstep = BNC ? (uint32_t)(kF32RK * p.ldb * 4) : (uint32_t)(kF32RK * 4);
+  // K tail: the last stage's scalar offsets (from K - 32) and its columns [0, kdup)
+  const uint32_t a_klast = (uint32_t)((kv - kF32RK) * 4);
+  const uint32_t b_klast = BNC ? (uint32_t)((int64_t)(kv - kF32RK) * p.ldb * 4) : a_klast;
+  const int kdup = p.K - kv;
   auto issue = [&](int slot, int stage) {
     const int st = min(stage, nk - 1);  // past the end: re-load the last stage into a free slot
+    const bool last = KT && st == nk - 1;
+    const uint32_t sa_off = last ? a_klast : (uint32_t)st * (kF32RK * 4);
+    const uint32_t sb_off = last ? b_klast : (uint32_t)st * b_kstep;
     float* base = lds + slot * STAGE;
 #pragma unroll
-    for (int j = 0; j < AJ; ++j)
-      buf_lds16(ra, a_voff[j], (uint32_t)st * (kF32RK * 4), (uint16_t*)(base + (wave + 4 * j) * 256));
+    for (int j = 0; j < AJ; ++j) buf_lds16(ra, a_voff[j], sa_off, (uint16_t*)(base + (wave + 4 * j) * 256));
 #pragma unroll
-    for (int j = 0; j < BJ; ++j)
-      buf_lds16(rb, b_voff[j], (uint32_t)st * b_kstep, (uint16_t*)(base + A_FL + (wave + 4 * j) * 256));
+    for (int j = 0; j < BJ; ++j) buf_lds16(rb, b_voff[j], sb_off, (uint16_t*)(base + A_FL + (wave + 4 * j) * 256));
+  };
+  // zero K columns [0, kdup) of both operands of the stage in slot sl (rows of 32 floats
+  // hold chunk c at position c ^ swz8(row); an N-contiguous B stages whole K-rows)
+  auto zero_dup = [&](int sl) {
+    float* base = lds + sl * STAGE;
+    for (int idx = tid; idx < BM * kdup; idx += 256) {
+      const int r = idx / kdup, k = idx - r * kdup;
+      base[r * kF32RK + 4 * ((k >> 2) ^ swz8(r)) + (k & 3)] = 0.0f;
+    }
+    if constexpr (BNC) {
+      for (int idx = tid; idx < kdup * BN; idx += 256) base[A_FL + idx] = 0.0f;
+    } else {
+      for (int idx = tid; idx < BN * kdup; idx += 256) {
+        const int r = idx / kdup, k = idx - r * kdup;
+        base[A_FL + r * kF32RK + 4 * ((k >> 2) ^ swz8(r)) + (k & 3)] = 0.0f;
+      }
+    }
   };
 
   // fragment offsets: row R + lr of a 32-row block (R % 32 == 0) has
@@ -505,6 +532,13 @@ __global__ void __launch_bounds__(256) gemm_f32_ring_kernel(const F32Params p) {
   for (int s = 0; s < nk; ++s) {
     wait_vmcnt<(NSLOT - 2) * LPS>();
     exec_barrier();
+    if constexpr (KT) {
+      if (s == nk - 1) {  // the last stage has landed: zero its repeated columns before any read
+        zero_dup(slot);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        exec_barrier();
+      }
+    }
     issue(slot == 0 ? NSLOT - 1 : slot - 1, s + NSLOT - 1);
     const float* sa = lds + slot * STAGE + rowA0 * kF32RK;
     const float* sb = lds + slot * STAGE + A_FL;
@@ -566,13 +600,13 @@ __global__ void __launch_bounds__(256) gemm_f32_ring_kernel(const F32Params p) {
   }
 }
 
-template <int BM, int BN, int NSLOT, bool BNC>
+template <int BM, int BN, int NSLOT, bool BNC, bool KT = false>
 int launch_f32_ring(F32Params p, hipStream_t st) {
   p.tiles_m = (p.M + BM - 1) / BM;
   p.tiles_n = (p.N + BN - 1) / BN;
   const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n;
   if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "gemm fp32: grid too large");
-  hipLaunchKernelGGL((gemm_f32_ring_kernel<BM, BN, NSLOT, BNC>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((gemm_f32_ring_kernel<BM, BN, NSLOT, BNC, KT>), dim3((unsigned)blocks), dim3(256), 0, st, p);
   return check_launch("gemm_f32_ring_kernel");
 }
 
@@ -635,6 +669,34 @@ int launch_gemm_f32(const GemmF32Args& d, Ws& ws, hipStream_t st) {
     return b_kc ? pick_f32<false>(p, st) : pick_f32<true>(p, st);
   }
   if (!fits) return set_error(KORE_EUNSUPPORTED, "gemm fp32: dimension >= 2^31");
+  // Large K tails (K % 64 != 0, e.g. 4095) with K-contiguous A and a K-contiguous or an
+  // aligned N-contiguous B: the ring kernel reads the rows in place (direct-to-LDS loads
+  // take any 4-byte offset) and starts its last 32-float stage at K - 32, the columns it
+  // shares with the stage before zeroed in LDS (KT); no pack pass.
+  const bool b_ktc = d.sbk == 1 && d.sbn >= d.K && d.sbn * 4 * 64 + d.K * 4 < (1ll << 31);
+  const bool b_ktn = b_nc && d.sbk * 4 * d.K + d.N * 4 < (1ll << 31);
+  if (d.K % kF32BK != 0 && d.K > kF32RK && d.sak == 1 && d.sam >= d.K && d.sam * 4 * 64 + d.K * 4 < (1ll << 31) &&
+      (b_ktc || b_ktn) && d.M * d.N * d.K >= (1ll << 26)) {
+    if (ws.plan) return KORE_OK;
+    F32Params p{};
+    p.a = (const float*)d.a;
+    p.b = (const float*)d.b;
+    p.bias = (const float*)d.bias;
+    p.c = (float*)d.c;
+    p.M = (int)d.M;
+    p.N = (int)d.N;
+    p.K = (int)((d.K + kF32RK - 1) / kF32RK * kF32RK);
+    p.kreal = (int)d.K;
+    p.kb = (int)d.K;
+    p.lda = d.sam;
+    p.ldb = b_ktn ? d.sbk : d.sbn;
+    p.ldc = d.scm;
+    p.act = d.act;
+    p.vec_store = d.scm % 4 == 0 && al16(d.c);
+    const bool many = (d.M + 127) / 128 * ((d.N + 63) / 64) >= 200;
+    if (b_ktn) return many ? launch_f32_ring<64, 64, 3, true, true>(p, st) : launch_f32_ring<64, 64, 8, true, true>(p, st);
+    return many ? launch_f32_ring<64, 64, 3, false, true>(p, st) : launch_f32_ring<64, 64, 8, false, true>(p, st);
+  }
   // Large problems in other layouts: pack A to [M, Kp] and B to [N, Kp] (K-contiguous,
   // zero K tail) in the caller's workspace, then the MFMA kernel.
   const int64_t Kp = (d.K + kF32BK - 1) / kF32BK * kF32BK;

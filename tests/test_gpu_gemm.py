@@ -324,6 +324,33 @@ def test_gemm_fp32_generic_mfma(gpu, M, N, K, op, a_t, b_layout):
     verdict(out, ref, "gemm_fusion_fp32", "fp32", f"fp32 generic {op} {M}x{N}x{K} a_t={a_t} {b_layout}")
 
 
+@pytest.mark.parametrize("K", [4095, 1000, 96, 33])
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+def test_gemm_fp32_k_tail_in_place(gpu, K, layout):
+    """fp32 K % 64 != 0 at 512 x 4096 (the gen_gemm_*_fp32 shape class): the ring kernel
+    reads A and B in place (rows at 4-byte alignment when K % 4 != 0) and starts its last
+    32-float stage at K - 32; the 32 * ceil(K / 32) - K columns it shares with the stage
+    before (1, 8, 0 and 31 here) are zeroed in LDS in both operands.  Column K - 32 holds 4
+    in every row of A and column of B, so a twice-counted or missing product (16 per
+    output) fails the fp32 gate."""
+    M, N = 512, 4096
+    g = torch.Generator().manual_seed(K + 7)
+    a = torch.randn((M, K), generator=g) / K ** 0.5
+    w = torch.randn((N, K), generator=g)
+    a[:, K - 32] = 4.0
+    w[:, K - 32] = 4.0
+    bias = torch.randn((N,), generator=g)
+    if layout == "kn":
+        b = w.t().contiguous()
+        bd = b.to(gpu)
+    else:
+        b, bd = w.t(), w.to(gpu).t()
+    out = kore_amd.gemm_fused(a.to(gpu), bd, bias.to(gpu), "none")
+    ref = gemm_fusion_ref(a, b, bias, "none")
+    verdict(out, ref, "gemm_fusion_fp32", "fp32", f"fp32 K tail {K} {layout}")
+    pair_only(out, ref, "fp32", f"fp32 K tail {K} {layout}")
+
+
 def test_batched_packed_path(gpu):
     """A batched problem with an odd K runs the packed path per batch."""
     from oracle.gemm import batched_gemm_ref
@@ -501,8 +528,8 @@ def test_gemm_fusion_fp32_ops(gpu, op):
 @pytest.mark.parametrize("bt", [False, True])
 def test_gemm_fp32_task_shapes(gpu, M, N, K, bt):
     """The fp32 task shapes, with b N-contiguous (the task's layout) or a W.t() view;
-    K = 4095 packs A and B (zero K tail) into the workspace for the MFMA kernel.  Rows are
-    sampled for the oracle."""
+    K = 4095 runs the ring kernel's in-place K-tail mode.  Rows are sampled for the
+    oracle."""
     g = torch.Generator(device=gpu).manual_seed(K)
     sc = 1.0 / K ** 0.5
     a = torch.randn((M, K), generator=g, device=gpu) * sc
