@@ -151,8 +151,9 @@ def test_capi_validation_without_gpu(lib):
 
 def test_gemm_workspace_queries_without_gpu(lib):
     """The workspace a call needs is planned on the host by the same dispatch that
-    launches it: zero for the in-place engines, the packed operands for a K tail with
-    unaligned rows, the fp32 split-K partials for a decode-sized M.  A workspace smaller
+    launches it: zero for the in-place engines (fp32 K tails included), the packed
+    operands for a K tail on a grid too small for the bf16 K-tail mode or a transposed
+    operand, the split-K partials for a decode-sized M.  A workspace smaller
     than the query fails with KORE_EWORKSPACE before anything is launched."""
     fake = ctypes.c_void_p(256)
     # 4096^3, A and B = W.t() K-contiguous: the engines read both in place
@@ -173,8 +174,10 @@ def test_gemm_workspace_queries_without_gpu(lib):
     # short of the packed operands is rejected
     rc = lib.kore_gemm(0, 0, fake, 4095, 1, fake, 1024, 1, None, fake, 1024, 512, 1024, 4095, fake, packed - 257, None)
     assert rc == 4
-    # fp32 K tail: A packed to [M, Kp] fp32
-    f32 = lib.kore_gemm_workspace_bytes(2, 0, fake, 4095, 1, fake, 1024, 1, None, fake, 1024, 512, 1024, 4095)
+    # fp32 K tail with K-contiguous A: the ring kernel's K-tail mode reads it in place
+    assert lib.kore_gemm_workspace_bytes(2, 0, fake, 4095, 1, fake, 1024, 1, None, fake, 1024, 512, 1024, 4095) == 0
+    # fp32 with an M-contiguous A (a transposed view) and a K tail: A packed to [M, Kp] fp32
+    f32 = lib.kore_gemm_workspace_bytes(2, 0, fake, 1, 512, fake, 1024, 1, None, fake, 1024, 512, 1024, 4095)
     assert f32 >= 512 * 4096 * 4
     # batched with B[i] = [N, K] K-contiguous: in place
     assert lib.kore_batched_gemm_workspace_bytes(0, fake, 1024 * 128, 128, 1, fake, 1024 * 128, 128, 1, fake,

@@ -35,7 +35,7 @@ def _noalloc(a, b, bias, act):
     return rc, c
 
 
-def _inputs(M, N, K, dtype, layout, bias, seed, dev):
+def _inputs(M, N, K, dtype, layout, bias, seed, dev, a_t=False):
     g = torch.Generator().manual_seed(seed)
     sc = 1.0 / K ** 0.5
     a = (torch.randn((M, K), generator=g) * sc).to(dtype)
@@ -46,7 +46,8 @@ def _inputs(M, N, K, dtype, layout, bias, seed, dev):
         w = (torch.randn((N, K), generator=g) * sc).to(dtype)
         b, bd = w.t(), w.to(dev).t()
     bs = torch.randn((N,), generator=g).to(dtype) if bias else None
-    return a, b, bs, a.to(dev), bd, (bs.to(dev) if bias else None)
+    ad = a.t().contiguous().to(dev).t() if a_t else a.to(dev)  # a_t: A as an M-contiguous view
+    return a, b, bs, ad, bd, (bs.to(dev) if bias else None)
 
 
 # (first problem, second smaller problem), dtype, B layout, bias, act, path
@@ -55,7 +56,7 @@ CASES = [
     (((384, 768, 999), (256, 640, 999)), torch.float16, "nk", True, "gelu", "packed A and B"),
     (((1, 2048, 4096), (1, 1024, 4096)), torch.bfloat16, "kn", False, "none", "split-K"),
     (((4, 4096, 4096), (2, 2048, 2048)), torch.float16, "nk", True, "silu", "split-K"),
-    (((512, 1024, 4095), (300, 600, 1023)), torch.float32, "kn", True, "relu", "fp32 packed"),
+    (((512, 1024, 4095), (300, 600, 1023)), torch.float32, "kn_at", True, "relu", "fp32 packed"),
     (((256, 256, 512), (128, 128, 256)), torch.bfloat16, "nk", False, "none", "no scratch"),
 ]
 
@@ -64,7 +65,8 @@ CASES = [
 def test_noalloc_matches_kore_gemm(gpu, shapes, dtype, layout, bias, act, path):
     outs = []
     for i, (M, N, K) in enumerate(shapes):
-        a, b, bs, ad, bd, bsd = _inputs(M, N, K, dtype, layout, bias, seed=M + N + K + i, dev=gpu)
+        a, b, bs, ad, bd, bsd = _inputs(M, N, K, dtype, layout.removesuffix("_at"), bias, seed=M + N + K + i,
+                                        dev=gpu, a_t=layout.endswith("_at"))
         rc, c = _noalloc(ad, bd, bsd, act)
         _lib.check(rc)
         outs.append((c, ad, bd, bsd, a, b, bs, (M, N, K)))
