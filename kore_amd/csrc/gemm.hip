@@ -1009,19 +1009,12 @@ int launch_buf(const GemmDesc& d, hipStream_t stream) {
     hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 8, A_KC, true>), dim3((unsigned)blocks), dim3(512), 0, stream, p);
     return check_launch("gemm_buf_kernel");
   }
-  // 8 waves on 16x16x32 MFMAs, except for an N-contiguous B whose grid needs more than one
-  // round of the CUs: there the 4-wave 32x32x16 tile measured 1-4% faster under the cold
-  // protocol (8192 x 4096 x 4096: 221 against 224-228 us; 8192 x 8192 x 4096: 427-429
-  // against 445 us), while 8 waves were 3-4% faster warm; on one round 8 waves win both
-  // (4096^3: cold 105-108 against 111 us, bit-equal).
-  if constexpr (BL == B_KC) {
-    hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 8, A_KC>), dim3((unsigned)blocks), dim3(512), 0, stream, p);
-  } else {
-    if (blocks <= device_cus())
-      hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 8, A_KC>), dim3((unsigned)blocks), dim3(512), 0, stream, p);
-    else
-      hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 4, A_KC>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
-  }
+  // 8 waves on 16x16x32 MFMAs for either B layout.  An N-contiguous B over more than one
+  // round of the CUs used to keep the 4-wave 32x32x16 tile, 1-4% faster cold than the
+  // 8-wave one of that time; with the 16-row swizzle and the full-stage load lead the
+  // 8-wave tile wins there too (same process, bit-equal, cold: 8192 x 8192 x 4096 429.9
+  // -> 409.6 us, 8192 x 4096 x 4096 223.4 -> 215.2 us; warm 418.3 -> 392.8, 211.9 -> 199.3).
+  hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 8, A_KC>), dim3((unsigned)blocks), dim3(512), 0, stream, p);
   return check_launch("gemm_buf_kernel");
 }
 
