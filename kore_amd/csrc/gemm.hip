@@ -268,8 +268,9 @@ __global__ void __launch_bounds__(64 * NWV)
 }
 
 // Mid-size problems (a few hundred tiles, long K) on the deep ring engine: NSLOT - 1
-// K stages in flight per CU instead of one or two.  Either B layout, K % 64 == 0.
-template <typename T, int BM, int BN, int WM, int WN, int NSLOT, int BL>
+// K stages in flight per CU instead of one or two.  Either B layout, K % 64 == 0 (KT:
+// K tails read in place, the ring engine's K-tail mode).
+template <typename T, int BM, int BN, int WM, int WN, int NSLOT, int BL, bool KT = false>
 __global__ void __launch_bounds__(256) gemm_deep_kernel(const TileParams p) {
   using E = RingEngine<T, BM, BN, WM, WN, NSLOT, BL>;
   __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
@@ -278,9 +279,14 @@ __global__ void __launch_bounds__(256) gemm_deep_kernel(const TileParams p) {
   tile_coords(p, BM, BN, batch, m0, n0);
   E eng;
   setup_operands<E, BM, BN, BL>(eng, p, batch, m0, n0, wave, lane);
+  if constexpr (KT) {  // last stage at K - 64 (bytes along a row / over N-contiguous K-rows)
+    eng.a_klast = (uint32_t)((p.kreal - kBK) * 2);
+    eng.b_klast = BL == B_NC ? (uint32_t)((int64_t)(p.kreal - kBK) * p.ldb * 2) : eng.a_klast;
+    eng.kdup = p.K - p.kreal;
+  }
   f32x16_t acc[E::MI][E::NI];
   E::zero(acc);
-  eng.mainloop(lds, p.K, acc);
+  eng.template mainloop<KT>(lds, p.K, acc);
   dense_epilogue<T, E::MI, E::NI, E::WROWS, E::WCOLS>(acc, lds, p, m0, n0, wave / WN, wave % WN, wave, lane,
                                                       p.c + batch * p.sc);
 }
@@ -1018,7 +1024,7 @@ int launch_buf(const GemmDesc& d, hipStream_t stream) {
   return check_launch("gemm_buf_kernel");
 }
 
-template <typename T, int BM, int BN, int WM, int WN, int NSLOT, int BL>
+template <typename T, int BM, int BN, int WM, int WN, int NSLOT, int BL, bool KT = false>
 int launch_deep(const GemmDesc& d, hipStream_t stream) {
   TileParams p{};
   p.a = (const uint16_t*)d.a;
@@ -1044,7 +1050,11 @@ int launch_deep(const GemmDesc& d, hipStream_t stream) {
   p.bias_vec = d.bias != nullptr && ((uintptr_t)d.bias & 7u) == 0;
   const int64_t blocks = (int64_t)p.tiles_per_batch * d.batch;
   if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "gemm: grid too large");
-  hipLaunchKernelGGL((gemm_deep_kernel<T, BM, BN, WM, WN, NSLOT, BL>), dim3((unsigned)blocks), dim3(256), 0, stream,
+  if constexpr (KT) {  // the loop over K rounded up to 64; the true K for the last stage
+    p.kreal = (int)d.K;
+    p.K = (int)((d.K + kBK - 1) / kBK * kBK);
+  }
+  hipLaunchKernelGGL((gemm_deep_kernel<T, BM, BN, WM, WN, NSLOT, BL, KT>), dim3((unsigned)blocks), dim3(256), 0, stream,
                      p);
   return check_launch("gemm_deep_kernel");
 }
@@ -1239,6 +1249,17 @@ int launch_engine(const GemmDesc& d, hipStream_t stream) {
   }
 }
 
+// K tails on the deep ring (tile shapes below 256x256), read in place.
+template <typename T, int BL>
+int launch_deep_kt(const GemmDesc& d, hipStream_t stream) {
+  switch (pick_tile(d)) {
+    case TILE_256x128: return launch_deep<T, 256, 128, 2, 2, 3, BL, true>(d, stream);
+    case TILE_128x128: return launch_deep<T, 128, 128, 2, 2, 4, BL, true>(d, stream);
+    case TILE_64x128: return launch_deep<T, 64, 128, 2, 2, 6, BL, true>(d, stream);
+    default: return launch_deep<T, 32, 128, 1, 4, 7, BL, true>(d, stream);
+  }
+}
+
 // Layouts the engines cannot read in place (rows not 16-byte aligned, e.g. K = 4095;
 // transposed or strided operands): A, and B unless it is N-contiguous with aligned
 // K-rows, are packed K-contiguous with the K tail zero-padded to a multiple of 64
@@ -1319,6 +1340,18 @@ int dispatch_typed(const GemmDesc& d, Ws& ws, hipStream_t stream) {
       if (ws.plan) return KORE_OK;
       return kc ? launch_buf<T, 256, 256, B_KC, A_KC, true>(d, stream)
                 : launch_buf<T, 256, 256, B_NC, A_KC, true>(d, stream);
+    }
+  }
+  // The same for mid-size grids (at least 128 tiles of 128x128, K >= 256) on the deep
+  // ring engine's K-tail mode, at the tile shape pick_tile chooses.
+  if (d.K % 64 != 0 && d.K >= 256 && d.sak == 1 && fits32 && d.sam * 2 * 256 + d.K * 2 < (1ll << 31) &&
+      ((d.M + 127) / 128) * ((d.N + 127) / 128) * d.batch >= 128) {
+    const bool kc = d.sbk == 1 && d.sbn * 2 * 256 + d.K * 2 < (1ll << 31);
+    const bool nc = d.sbn == 1 && d.sbk % 8 == 0 && aligned16(d.b) && d.sb % 8 == 0 && d.N % 8 == 0 &&
+                    d.sbk * 2 * d.K + d.N * 2 < (1ll << 31);
+    if (kc || nc) {
+      if (ws.plan) return KORE_OK;
+      return kc ? launch_deep_kt<T, B_KC>(d, stream) : launch_deep_kt<T, B_NC>(d, stream);
     }
   }
   if (a_mc && fits32 && pick_tile(d) == TILE_256x256 &&

@@ -934,6 +934,28 @@ struct RingEngine {
   __amdgpu_buffer_rsrc_t ra, rb;
   uint32_t a_voff[AJ], b_voff[BJ];
   uint32_t b_kstep;  // NC: bytes of B between consecutive 64-row K stages
+  // K tail (mainloop<true>, K % 64 != 0): the last stage is read from K - 64 (scalar byte
+  // offsets a_klast, b_klast) and its first kdup columns, which the stage before already
+  // covered, are zeroed in LDS in both operands once it has landed.
+  uint32_t a_klast, b_klast;
+  int kdup;
+
+  // Zero K columns [0, kdup) of both operands of the stage at st (every thread takes part).
+  __device__ __forceinline__ void zero_dup(uint16_t* st) const {
+    const int tid = threadIdx.x;
+    for (int idx = tid; idx < BM * kdup; idx += NW * 64) {
+      const int r = idx / kdup, k = idx - r * kdup;
+      st[r * kBK + (((k >> 3) ^ swz8(r)) << 3) + (k & 7)] = 0;
+    }
+    if constexpr (NC) {
+      for (int idx = tid; idx < kdup * BN; idx += NW * 64) st[B_OFF + idx] = 0;  // whole K-rows
+    } else {
+      for (int idx = tid; idx < BN * kdup; idx += NW * 64) {
+        const int r = idx / kdup, k = idx - r * kdup;
+        st[B_OFF + r * kBK + (((k >> 3) ^ swz8(r)) << 3) + (k & 7)] = 0;
+      }
+    }
+  }
 
   __device__ __forceinline__ void issue(uint16_t* lds, int slot, uint32_t soff, uint32_t soffb, int wave) const {
     uint16_t* st = lds + slot * STAGE;
@@ -959,12 +981,14 @@ struct RingEngine {
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
   }
 
-  // K must be a positive multiple of 64.
+  // K must be a positive multiple of 64 (KT: the padded length, see a_klast / kdup).
+  template <bool KT = false>
   __device__ __forceinline__ void mainloop(uint16_t* lds, int K, f32x16_t (&acc)[MI][NI]) {
-    mainloop_range(lds, 0, K, acc);
+    mainloop_range<KT>(lds, 0, K, acc);
   }
 
   // Multiply K elements [k_begin, k_end) (multiples of 64, k_end > k_begin).
+  template <bool KT = false>
   __device__ __forceinline__ void mainloop_range(uint16_t* lds, int k_begin, int k_end, f32x16_t (&acc)[MI][NI]) {
     using Op = MfmaOp<T>;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -986,14 +1010,27 @@ struct RingEngine {
     }
     if constexpr (NC) nc_frag_offsets<BN, NI>(lane, rowB0, offNC);
     const int nk = (k_end - k_begin) / kBK, kb0 = k_begin / kBK;
-    auto soff_of = [&](int stage) { return (uint32_t)(kb0 + min(stage, nk - 1)) * (kBK * 2); };
-    auto soffb_of = [&](int stage) { return NC ? (uint32_t)(kb0 + min(stage, nk - 1)) * b_kstep : soff_of(stage); };
+    auto soff_of = [&](int stage) -> uint32_t {
+      if (KT && stage >= nk - 1) return a_klast;
+      return (uint32_t)(kb0 + min(stage, nk - 1)) * (kBK * 2);
+    };
+    auto soffb_of = [&](int stage) -> uint32_t {
+      if (KT && NC && stage >= nk - 1) return b_klast;
+      return NC ? (uint32_t)(kb0 + min(stage, nk - 1)) * b_kstep : soff_of(stage);
+    };
 #pragma unroll
     for (int s = 0; s < NSLOT - 1; ++s) issue(lds, s, soff_of(s), soffb_of(s), wave);
     int slot = 0;
     for (int s = 0; s < nk; ++s) {
       wait_vmcnt<(NSLOT - 2) * LPS>();
       exec_barrier();
+      if constexpr (KT) {
+        if (s == nk - 1) {  // the last stage has landed: zero its repeated columns before any read
+          zero_dup(lds + slot * STAGE);
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          exec_barrier();
+        }
+      }
       const int nslot = slot == 0 ? NSLOT - 1 : slot - 1;  // slot of stage s - 1
       issue(lds, nslot, soff_of(s + NSLOT - 1), soffb_of(s + NSLOT - 1), wave);
       const uint16_t* sA = lds + slot * STAGE + rowA0 * kBK;

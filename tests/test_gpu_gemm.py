@@ -97,6 +97,35 @@ def test_gemm_k_tail_in_place(gpu, K, layout):
     assert bit_equal(out, out2), "determinism"
 
 
+@pytest.mark.parametrize("M,N,K,dtype,op", [(512, 4096, 4095, torch.float16, "gemm_bias_gelu"),
+                                             (512, 4096, 1000, torch.bfloat16, "gemm"),
+                                             (512, 4096, 257, torch.bfloat16, "gemm_relu"),
+                                             (2048, 2048, 2047, torch.float16, "gemm"),
+                                             (1536, 4096, 1001, torch.bfloat16, "gemm_bias_silu")])
+@pytest.mark.parametrize("layout", ["kn", "bt"])
+def test_gemm_k_tail_deep_ring(gpu, M, N, K, dtype, op, layout):
+    """K % 64 != 0 on mid-size grids runs the deep ring engine's K-tail mode at the tile
+    pick_tile chooses (64x128 for 512 x 4096, 128x128 for 2048^2, 256x128 for 1536 x
+    4096): both operands read in place, the last stage from K - 64, the repeated columns
+    zeroed in LDS.  Column K - 64 holds 4 in every row of A and column of B (16 per
+    output), so counting it twice or missing it fails the oracle check; fused epilogues
+    on the same path."""
+    g = torch.Generator().manual_seed(M + K)
+    a = (torch.randn((M, K), generator=g) / K ** 0.5).to(dtype)
+    w = torch.randn((N, K), generator=g).to(dtype)
+    a[:, K - 64] = 4.0
+    w[:, K - 64] = 4.0
+    bias = torch.randn((N,), generator=g).to(dtype)
+    b = w.t().contiguous() if layout == "kn" else w.t()
+    bd = w.t().contiguous().to(gpu) if layout == "kn" else w.to(gpu).t()
+    has_bias, act = kore_amd.GEMM_FUSION_OPS.get(op, (False, "none"))
+    out = kore_amd.gemm_fused(a.to(gpu), bd, bias.to(gpu) if has_bias else None, act)
+    ref = gemm_fusion_ref(a, b, bias if has_bias else None, act)
+    dt = "bf16" if dtype == torch.bfloat16 else "fp16"
+    verdict(out, ref, "gemm_fusion", dt, f"deep K tail {op} {M}x{N}x{K} {layout}")
+    pair_only(out, ref, dt, f"deep K tail {op} {M}x{N}x{K} {layout}")
+
+
 @pytest.mark.parametrize("M,N,K,dtype,op", [(4096, 4096, 4096, torch.bfloat16, "gemm_bias_gelu"),
                                              (3000, 4104, 1024, torch.float16, "gemm_bias_silu"),
                                              (2048, 7168, 4096, torch.bfloat16, "gemm"),
