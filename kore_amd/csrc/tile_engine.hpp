@@ -451,8 +451,6 @@ struct BufPipeEngine {
   uint32_t a_klast, b_klast;
   int kdup;
 
-  static constexpr bool nk_tail_ok() { return AP == 1 && !AMC; }
-
   // Zero K columns [0, kdup) of both operands of the stage at st (every thread takes part).
   __device__ __forceinline__ void zero_dup(uint16_t* st) const {
     static_assert(AP == 1 && !AMC, "K tails: one K-contiguous A plane");
@@ -693,7 +691,6 @@ struct BufPipeEngine {
     constexpr int NMMA = AP * MI * NI * 4;  // MFMAs per sub-step
     constexpr int NRD = NFA + NFB;          // fragment reads per sub-step
     static_assert(NRD <= NMMA && LPS <= NMMA && LPS <= 32, "interleave needs enough MFMAs; vmcnt range");
-    static_assert(!KT || nk_tail_ok(), "K tails: one K-contiguous A plane");
     const uint32_t kmax = (uint32_t)(nk - 1) * (kBK * 2);
     auto soff_of = [&](int stage) -> uint32_t {
       if constexpr (KT) return stage >= nk - 1 ? a_klast : (uint32_t)stage * (kBK * 2);
@@ -987,7 +984,8 @@ struct RingEngine {
     mainloop_range<KT>(lds, 0, K, acc);
   }
 
-  // Multiply K elements [k_begin, k_end) (multiples of 64, k_end > k_begin).
+  // Multiply K elements [k_begin, k_end) (multiples of 64, k_end > k_begin; KT: the whole K,
+  // k_begin == 0).
   template <bool KT = false>
   __device__ __forceinline__ void mainloop_range(uint16_t* lds, int k_begin, int k_end, f32x16_t (&acc)[MI][NI]) {
     using Op = MfmaOp<T>;
