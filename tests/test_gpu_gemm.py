@@ -391,6 +391,25 @@ def test_batched_packed_path(gpu):
     verdict(out, batched_gemm_ref(a, b), "gemm", "bf16", "batched packed 4x512x384x999")
 
 
+@pytest.mark.parametrize("B,M,N,K", [(4, 1024, 1024, 1023), (4, 2048, 2048, 2047)])
+def test_batched_k_tail_in_place(gpu, B, M, N, K):
+    """Batched problems with K % 64 != 0 on the K-tail modes, per-batch operand offsets
+    included: 4 x 1024^2 (256 tiles of 128x128: deep ring) and 4 x 2048^2 (256 tiles of
+    256x256: the 16x16 engine); column K - 64 of every batch holds 4 in A and B, so a
+    twice-counted or missing shared column fails the check."""
+    from oracle.gemm import batched_gemm_ref
+
+    g = torch.Generator().manual_seed(B + K)
+    a = (torch.randn((B, M, K), generator=g) / K ** 0.5).bfloat16()
+    b = torch.randn((B, N, K), generator=g).bfloat16()
+    a[:, :, K - 64] = 4.0
+    b[:, :, K - 64] = 4.0
+    out = kore_amd.batched_gemm(a.to(gpu), b.to(gpu))
+    ref = batched_gemm_ref(a, b)
+    verdict(out, ref, "gemm", "bf16", f"batched K tail {B}x{M}x{N}x{K}")
+    pair_only(out, ref, "bf16", f"batched K tail {B}x{M}x{N}x{K}")
+
+
 def test_gemm_metric_4096_bt(gpu):
     a, b = W.dense_inputs(4096, 4096, 4096, seed=0)
     out = kore_amd.gemm(a.to(gpu), b.to(gpu))
