@@ -68,9 +68,10 @@ int kore_abi_version(void);
  *   A element (m,k) at a[m*lda_m + k*lda_k]; B element (k,n) at b[k*ldb_k + n*ldb_n];
  *   C element (m,n) at c[m*ldc_m + n]; bias may be NULL (no bias), else [N] contiguous.
  * Any strides are accepted; the MFMA fast path needs unit stride along K for A and
- * along K or N for B, 16-byte aligned rows and K % 8 == 0.  Other layouts (e.g. the
- * K = 4095 tails) are packed into `workspace` first when the problem is large, or run
- * a slower generic kernel when it is small; decode-sized M splits K and sums fp32
+ * along K or N for B and 16-byte aligned rows.  K tails (e.g. K = 4095) with A K-contiguous
+ * are read in place on grids of >= 128 tiles of 128x128 (rows at any 2-byte alignment);
+ * other layouts are packed into `workspace` first when the problem is large, or run a
+ * slower generic kernel when it is small; decode-sized M splits K and sums fp32
  * partials held in `workspace`.  M, N >= 1, K >= 0 (K == 0 gives act(bias); a and b
  * may then be NULL).  `workspace` must hold kore_gemm_workspace_bytes(<same args>).
  * Replaces: gemm(a, b)            kore/tasks/gemm_bf16/seed_triton.py:64-86
