@@ -69,7 +69,8 @@ int kore_abi_version(void);
  *   C element (m,n) at c[m*ldc_m + n]; bias may be NULL (no bias), else [N] contiguous.
  * Any strides are accepted; the MFMA fast path needs unit stride along K for A and
  * along K or N for B and 16-byte aligned rows.  K tails (e.g. K = 4095) with A K-contiguous
- * are read in place on grids of >= 128 tiles of 128x128 (rows at any 2-byte alignment);
+ * are read in place on large problems (16-bit: >= 128 tiles of 128x128 and K >= 256, or a
+ * 256x256 grid; fp32: M*N*K >= 2^26), rows at any 2-byte alignment;
  * other layouts are packed into `workspace` first when the problem is large, or run a
  * slower generic kernel when it is small; decode-sized M splits K and sums fp32
  * partials held in `workspace`.  M, N >= 1, K >= 0 (K == 0 gives act(bias); a and b
