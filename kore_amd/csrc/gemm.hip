@@ -229,13 +229,12 @@ __device__ __forceinline__ void setup_operands(E& eng, const TileParams& p, int 
 // Buffer-load pipelined variant for K-contiguous A, K % 64 == 0 and either B layout:
 // K-contiguous B (the A.B^T / A.W^T layouts) or N-contiguous B (natural [K, N], N % 8 ==
 // 0), whose fragments come out of LDS through transpose reads.
-// NWV = 8: 16x16x32 MFMAs on 8 waves (2 x 4, 128 x 64 each, two per SIMD); same process,
-// bit-equal, 4096^3 bf16 102 -> 100 us and fp16 + gelu 113-115 -> 112 us against 4 waves of
-// 128 x 128 (K-contiguous B).  An N-contiguous B reaches the 16x16 fragments through transpose
-// reads with the nc_x16 chunk swizzle.  NWV = 4 (N-contiguous B over several rounds of the
-// CUs, see launch_buf): 4 waves of 128 x 128 on 32x32x16 with the nc_x swizzle.  AL = A_MC: A
-// is M-contiguous (a transposed view) and read like an N-contiguous B (8 waves only).
-// KT: K tails (K % 64 != 0) read in place on the 16x16 engine (mainloop16<true>).
+// 16x16x32 MFMAs.  NWV = 4 (K-contiguous B): 2 x 2 waves of 128 x 128, one per SIMD, the
+// accumulators held in place in the 256 AGPRs (mma16_acc).  NWV = 8 (N-contiguous B): 2 x 4
+// waves of 128 x 64, two per SIMD; an N-contiguous B reaches the 16x16 fragments through
+// transpose reads with the nc_x16 chunk swizzle.  AL = A_MC: A is M-contiguous (a transposed
+// view) and read like an N-contiguous B (8 waves only).  KT: K tails (K % 64 != 0) read in
+// place (mainloop16<true>).
 template <typename T, int BM, int BN, int BL, int NWV, int AL, bool KT = false>
 __global__ void __launch_bounds__(64 * NWV)
     gemm_buf_kernel(const TileParams p) {
@@ -1009,18 +1008,25 @@ int launch_buf(const GemmDesc& d, hipStream_t stream) {
     hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 8, A_MC>), dim3((unsigned)blocks), dim3(512), 0, stream, p);
     return check_launch("gemm_buf_kernel");
   }
+  // K-contiguous B: 4 waves of 128 x 128 with the accumulators in place in AGPRs (one
+  // wave per SIMD; same process, bit-equal, against the 8-wave tile: 4096^3 bf16 95.8 ->
+  // 91.9 us, fp16 + bias + gelu 109.2 -> 106.1 us, 8192 x 4096 x 4096 189.9 -> 184.0 us).
+  // N-contiguous B: 8 waves on 16x16x32 MFMAs.  Over more than one round of the CUs it
+  // used to keep the 4-wave 32x32x16 tile, 1-4% faster cold than the 8-wave one of that
+  // time; with the 16-row swizzle and the full-stage load lead the 8-wave tile wins there
+  // too (same process, bit-equal, cold: 8192 x 8192 x 4096 429.9 -> 409.6 us, 8192 x 4096 x
+  // 4096 223.4 -> 215.2 us; warm 418.3 -> 392.8, 211.9 -> 199.3).
+  // K tails keep 8 waves for both layouts (3072 x 4096 x 1000 with K-contiguous B: 34.8 us
+  // against 36.5 us on 4 waves; 4096 x 4096 x 4095 within 1%).
   if constexpr (KT) {
     p.kreal = (int)d.K;
     p.K = (int)((d.K + kBK - 1) / kBK * kBK);
     hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 8, A_KC, true>), dim3((unsigned)blocks), dim3(512), 0, stream, p);
     return check_launch("gemm_buf_kernel");
   }
-  // 8 waves on 16x16x32 MFMAs for either B layout.  An N-contiguous B over more than one
-  // round of the CUs used to keep the 4-wave 32x32x16 tile, 1-4% faster cold than the
-  // 8-wave one of that time; with the 16-row swizzle and the full-stage load lead the
-  // 8-wave tile wins there too (same process, bit-equal, cold: 8192 x 8192 x 4096 429.9
-  // -> 409.6 us, 8192 x 4096 x 4096 223.4 -> 215.2 us; warm 418.3 -> 392.8, 211.9 -> 199.3).
-  hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, 8, A_KC>), dim3((unsigned)blocks), dim3(512), 0, stream, p);
+  constexpr int NWV = BL == B_KC ? 4 : 8;
+  hipLaunchKernelGGL((gemm_buf_kernel<T, BM, BN, BL, NWV, A_KC>), dim3((unsigned)blocks), dim3(64 * NWV), 0, stream,
+                     p);
   return check_launch("gemm_buf_kernel");
 }
 

@@ -55,6 +55,39 @@ template <> struct MfmaOp<BF16> {
     return __builtin_bit_cast(float, (uint32_t)v << 16);
   }
 };
+// 16x16x32 MFMA accumulating in place in AGPRs (inline asm: srcC and vdst are the same
+// registers).  With 256 AGPRs of accumulators (one wave per SIMD, 128 x 128 wave tiles)
+// the builtin's separate result lets the register allocator rotate every accumulator
+// through fresh AGPRs and copy it back once per stage (about 500 v_accvgpr moves per
+// 128 MFMAs); the tied form keeps each tile in place.  The compiler does not see these
+// as MFMAs, so the caller provides the wait states around them: the first product of each
+// accumulator is mma16_acc0 (no VALU write precedes it), and at least 7 wait states
+// separate the last of these from any VALU read of the accumulators (mma16_acc_fence
+// below gives 24).
+template <typename T> __device__ __forceinline__ void mma16_acc(f32x4_t& c, u32x4_t a, u32x4_t b);
+template <> __device__ __forceinline__ void mma16_acc<BF16>(f32x4_t& c, u32x4_t a, u32x4_t b) {
+  asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+template <> __device__ __forceinline__ void mma16_acc<F16>(f32x4_t& c, u32x4_t a, u32x4_t b) {
+  asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+// First product of an accumulator: the same MFMA with an inline-constant zero for srcC, so
+// no VALU instruction writes the accumulators before the MFMAs read them.
+template <typename T> __device__ __forceinline__ void mma16_acc0(f32x4_t& c, u32x4_t a, u32x4_t b);
+template <> __device__ __forceinline__ void mma16_acc0<BF16>(f32x4_t& c, u32x4_t a, u32x4_t b) {
+  asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
+}
+template <> __device__ __forceinline__ void mma16_acc0<F16>(f32x4_t& c, u32x4_t a, u32x4_t b) {
+  asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
+}
+// Wait states around a run of mma16_acc (scheduling fences keep other instructions from
+// moving across).
+__device__ __forceinline__ void mma16_acc_fence() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 template <> struct MfmaOp<F16> {
   static __device__ __forceinline__ f32x16_t mma32(u32x4_t a, u32x4_t b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),

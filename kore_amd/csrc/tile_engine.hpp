@@ -714,54 +714,82 @@ struct BufPipeEngine {
         exec_barrier();
       }
     }
-    // A fragments are single-buffered: A block (pl, i, half sm) of the next sub-step is
-    // read right after its last MFMA in this one (tile j = NI - 1, sub-tile g = 2 sm + 1),
-    // at least (MI - 1) * NI * 4 MFMAs before its first use; B fragments are double-
-    // buffered and read over the first MFMAs.  This keeps 32 VGPRs free, which the
-    // register allocator otherwise finds by moving accumulators through AGPR copies.
-    u32x4_t fa[NFA], fb[2][NFB], fa_unused[NFA];
+    // 8 waves: A fragments are single-buffered: A block (pl, i, half sm) of the next
+    // sub-step is read right after its last MFMA in this one (tile j = NI - 1, sub-tile
+    // g = 2 sm + 1), at least (MI - 1) * NI * 4 MFMAs before its first use; B fragments
+    // are double-buffered and read over the first MFMAs.  This keeps 32 VGPRs free, which
+    // the register allocator otherwise finds by moving accumulators through AGPR copies.
+    // 4 waves (FA2, one wave per SIMD, 128 x 128 wave tiles, K-contiguous operands): the
+    // accumulators fill the 256 AGPRs and stay in place (mma16_acc), so A is double-
+    // buffered too and every read of the next sub-step goes out over its first MFMAs.
+    constexpr bool FA2 = NW == 4 && !NC && !AMC && AP == 1;
+    u32x4_t fa[FA2 ? 2 : 1][NFA], fb[2][NFB], fa_unused[NFA];
 #pragma unroll
-    for (int f = 0; f < NRD; ++f) read_one(0, 0, f, fa, fb[0]);
-    for (int s = 0; s < nk; ++s) {
+    for (int f = 0; f < NRD; ++f) read_one(0, 0, f, fa[0], fb[0]);
+    // sub-step ks of stage s: its MFMAs, the next sub-step's fragment reads and (ks == 1)
+    // the direct loads of stage s + 2
+    // (first: the very first sub-step, whose MFMAs start the accumulators)
+    auto substep = [&](int s, auto ksc, auto firstc) {
+      constexpr int ks = decltype(ksc)::value, c = ks;
+      constexpr bool first = decltype(firstc)::value;
       const int slot = s & 1;
       const uint32_t soff2 = soffa_of(s + 2), soffb2 = soffb_of(s + 2);
+      const int rslot = ks == 0 ? slot : (slot ^ 1);
+      const int rks = ks == 0 ? 1 : 0;
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const int c = ks;
-        if (ks == 1) {
-          // every wave has read this slot's fragments and landed stage s + 1
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-          wait_vmcnt<0>();
-          exec_barrier();
-          if constexpr (KT) {
-            if (s == nk - 2) {  // stage s + 1 is the last: zero its repeated columns first
-              zero_dup(lds + (slot ^ 1) * STAGE);
-              asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-              exec_barrier();
-            }
-          }
-        }
-        const int rslot = ks == 0 ? slot : (slot ^ 1);
-        const int rks = ks == 0 ? 1 : 0;
-#pragma unroll
-        for (int m = 0; m < NMMA; ++m) {
-          __builtin_amdgcn_sched_barrier(0);
-          const int pl = m / (MI * NI * 4), i = (m / (NI * 4)) % MI, j = (m / 4) % NI, g = m & 3;
-          const int sm = g >> 1, sn = g & 1;
-          c4[i][j][g] = Op::mma16(fb[c][j * 2 + sn], fa[(pl * MI + i) * 2 + sm], c4[i][j][g]);
-          if (j == NI - 1 && (g & 1)) read_one(rslot, rks, (pl * MI + i) * 2 + sm, fa, fb[c ^ 1]);
-          if (m < NFB) read_one(rslot, rks, NFA + m, fa_unused, fb[c ^ 1]);
-          // every load of stage s+2 goes out in sub-step 1, right after the barrier that frees
-          // its slot, spread over the MFMAs: a full stage of lead before the vmcnt(0) wait of
-          // stage s+1.  Issuing half of them in the next stage's sub-step 0 instead (half a
-          // stage of lead) measured slower in the same process, bit-equal outputs: 4096^3 bf16
-          // 100.3 against 103.2 us, 8192x4096x4096 195.6 against 204.0 us.
-          constexpr int EV = NMMA / LPS > 0 ? NMMA / LPS : 1;
-          if (ks == 1 && m % EV == 0 && m / EV < LPS) issue_one(lds, slot, soff2, soffb2, wave, m / EV);
-        }
+      for (int m = 0; m < NMMA; ++m) {
         __builtin_amdgcn_sched_barrier(0);
+        const int pl = m / (MI * NI * 4), i = (m / (NI * 4)) % MI, j = (m / 4) % NI, g = m & 3;
+        const int sm = g >> 1, sn = g & 1;
+        if constexpr (FA2) {
+          if constexpr (first) mma16_acc0<T>(c4[i][j][g], fb[c][j * 2 + sn], fa[c][(pl * MI + i) * 2 + sm]);
+          else mma16_acc<T>(c4[i][j][g], fb[c][j * 2 + sn], fa[c][(pl * MI + i) * 2 + sm]);
+          if (m < NRD) read_one(rslot, rks, m, fa[c ^ 1], fb[c ^ 1]);
+        } else {
+          c4[i][j][g] = Op::mma16(fb[c][j * 2 + sn], fa[0][(pl * MI + i) * 2 + sm], c4[i][j][g]);
+          if (j == NI - 1 && (g & 1)) read_one(rslot, rks, (pl * MI + i) * 2 + sm, fa[0], fb[c ^ 1]);
+          if (m < NFB) read_one(rslot, rks, NFA + m, fa_unused, fb[c ^ 1]);
+        }
+        // every load of stage s+2 goes out in sub-step 1, right after the barrier that frees
+        // its slot, spread over the MFMAs: a full stage of lead before the vmcnt(0) wait of
+        // stage s+1.  Issuing half of them in the next stage's sub-step 0 instead (half a
+        // stage of lead) measured slower in the same process, bit-equal outputs: 4096^3 bf16
+        // 100.3 against 103.2 us, 8192x4096x4096 195.6 against 204.0 us.
+        constexpr int EV = NMMA / LPS > 0 ? NMMA / LPS : 1;
+        if (ks == 1 && m % EV == 0 && m / EV < LPS) issue_one(lds, slot, soff2, soffb2, wave, m / EV);
       }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    // every wave has read stage s's slot (through sub-step 0) and landed stage s + 1
+    auto sync = [&](int s) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      wait_vmcnt<0>();
+      exec_barrier();
+      if constexpr (KT) {
+        if (s == nk - 2) {  // stage s + 1 is the last: zero its repeated columns first
+          zero_dup(lds + ((s & 1) ^ 1) * STAGE);
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          exec_barrier();
+        }
+      }
+    };
+    // The loop runs from barrier to barrier (sub-step 1 of stage s, then sub-step 0 of
+    // stage s + 1), so its head follows an lgkmcnt(0) wait.  With the head at sub-step 0
+    // the compiler's wait-count analysis merged the loop's two entries into an
+    // lgkmcnt(1) wait before the first MFMA of every stage, a full LDS latency with
+    // one wave per SIMD (same process, bit-equal, 4096^3 bf16 on 4 waves: 93.6 -> 92.7 us).
+    using K0 = std::integral_constant<int, 0>;
+    using K1 = std::integral_constant<int, 1>;
+    using F0 = std::integral_constant<bool, false>;
+    substep(0, K0(), std::integral_constant<bool, FA2>());
+    for (int s = 0; s < nk - 1; ++s) {
+      sync(s);
+      substep(s, K1(), F0());
+      substep(s + 1, K0(), F0());
     }
+    sync(nk - 1);
+    substep(nk - 1, K1(), F0());
+    if constexpr (FA2) mma16_acc_fence();
     wait_vmcnt<0>();  // drain the clamped trailing loads before LDS is reused
     __syncthreads();
   }
