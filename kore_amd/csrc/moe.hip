@@ -390,20 +390,19 @@ __global__ void __launch_bounds__(kEngineThreads)
 // Prefill path on the buffer-load pipelined engine: A rows (gathered tokens for
 // gate_up, H planes for down) and B rows (interleaved gate/up rows of w1[e], rows of
 // w2[e]) become per-lane byte offsets of buffer resources, fixed for the whole K loop.
-// NWV = 8: 16x16x32 MFMAs on a 2 x 4 wave grid (two waves per SIMD); NWV = 4: 32x32x16
-// MFMAs on 2 x 2.  Fused MoE E=8 top-2 D=4096 I=14336, same process: T=4096 3.93 ->
-// 3.83 ms, T=16384 13.43 -> 12.94 ms with both projections on 8 waves (gate_up alone
-// is bit-equal to the 4-wave kernel; down, with two A planes per sub-step, sums in
-// another order).  The plain grouped GEMM stays on 4 waves: on 8 it measured 117 ->
-// 124 us at M=4096, E=32, N=2048, K=4096 (jagged routing) and 204 -> 211 us at
-// 8192 x 16 x 1536 x 4096.
+// 16x16x32 MFMAs on a 2 x 2 wave grid, one wave per SIMD, with the accumulators held in
+// place in AGPRs (mma16_acc).  Fused MoE E=8 top-2 D=4096 I=14336, same process,
+// bit-equal: T=4096 3.75 -> 3.58 ms against the former 2 x 4 grid of 8 waves (two per
+// SIMD), which had itself replaced 4 waves of 32x32x16 MFMAs (T=4096 3.93 -> 3.83 ms);
+// T=1024 within 1%.  The plain grouped GEMM: 117 us either way at M=4096, E=32, N=2048,
+// K=4096 (jagged routing), 204.5 -> 202.2 us at 8192 x 16 x 1536 x 4096.
 template <int MODE, int BM, int BN, int NWV>
 __global__ void __launch_bounds__(64 * NWV)
     moe_buf_kernel(const MoeGemmParams p) {
   constexpr int AP = (MODE == MOE_DOWN) ? 2 : 1;
   // grouped (plain) GEMM: an expert's weight tile is read by that expert's row blocks
   // only, running side by side on one XCD (L2), so its loads are non-temporal
-  using E = BufPipeEngine<BF16, BM, BN, 2, NWV / 2, AP, B_KC, MODE == MOE_PLAIN ? kCpolNT : kCpolDefault, NWV == 8>;
+  using E = BufPipeEngine<BF16, BM, BN, 2, NWV / 2, AP, B_KC, MODE == MOE_PLAIN ? kCpolNT : kCpolDefault, true>;
   constexpr int MI = E::MI, NI = E::NI;
   __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -494,17 +493,10 @@ __global__ void __launch_bounds__(64 * NWV)
     }
   }
 
-  if constexpr (E::M16) {
-    f32x4_t acc[MI][NI][4];
-    E::zero16(acc);
-    eng.mainloop16(lds, p.K, acc);
-    moe_epilogue16<MODE, MI, NI, E::WROWS, E::WCOLS>(acc, lds, p, pos0, n0, wm, wn, wave, lane);
-  } else {
-    f32x16_t acc[MI][NI];
-    E::zero(acc);
-    eng.mainloop(lds, p.K, acc);
-    moe_epilogue<MODE, MI, NI, E::WROWS, E::WCOLS>(acc, lds, p, pos0, n0, wm, wn, wave, lane);
-  }
+  f32x4_t acc[MI][NI][4];
+  E::zero16(acc);
+  eng.mainloop16(lds, p.K, acc);
+  moe_epilogue16<MODE, MI, NI, E::WROWS, E::WCOLS>(acc, lds, p, pos0, n0, wm, wn, wave, lane);
 }
 
 // Down projection grid: workgroup b runs on XCD b % 8 (round-robin dispatch), so XCD x
@@ -710,7 +702,7 @@ int launch_moe_buf(MoeGemmParams p, int64_t cap, hipStream_t st) {
   p.max_mblocks = (int)(cap / BM);
   const int64_t blocks = (int64_t)p.max_mblocks * p.ntiles;
   if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "fused_moe: grid too large");
-  constexpr int NWV = MODE == MOE_PLAIN ? 4 : 8;
+  constexpr int NWV = 4;
   hipLaunchKernelGGL((moe_buf_kernel<MODE, BM, BN, NWV>), dim3((unsigned)blocks), dim3(64 * NWV), 0, st, p);
   return check_launch(MODE == MOE_GATEUP ? "moe_gateup_buf_kernel" : "moe_down_buf_kernel");
 }

@@ -719,10 +719,10 @@ struct BufPipeEngine {
     // g = 2 sm + 1), at least (MI - 1) * NI * 4 MFMAs before its first use; B fragments
     // are double-buffered and read over the first MFMAs.  This keeps 32 VGPRs free, which
     // the register allocator otherwise finds by moving accumulators through AGPR copies.
-    // 4 waves (FA2, one wave per SIMD, 128 x 128 wave tiles, K-contiguous operands): the
-    // accumulators fill the 256 AGPRs and stay in place (mma16_acc), so A is double-
+    // 4 waves (FA2, one wave per SIMD, K-contiguous operands): the accumulators (up to the
+    // 256 AGPRs of a 128 x 128 wave tile) stay in place (mma16_acc), so A is double-
     // buffered too and every read of the next sub-step goes out over its first MFMAs.
-    constexpr bool FA2 = NW == 4 && !NC && !AMC && AP == 1;
+    constexpr bool FA2 = NW == 4 && !NC && !AMC;
     u32x4_t fa[FA2 ? 2 : 1][NFA], fb[2][NFB], fa_unused[NFA];
 #pragma unroll
     for (int f = 0; f < NRD; ++f) read_one(0, 0, f, fa[0], fb[0]);
@@ -742,7 +742,7 @@ struct BufPipeEngine {
         const int pl = m / (MI * NI * 4), i = (m / (NI * 4)) % MI, j = (m / 4) % NI, g = m & 3;
         const int sm = g >> 1, sn = g & 1;
         if constexpr (FA2) {
-          if constexpr (first) mma16_acc0<T>(c4[i][j][g], fb[c][j * 2 + sn], fa[c][(pl * MI + i) * 2 + sm]);
+          if (first && pl == 0) mma16_acc0<T>(c4[i][j][g], fb[c][j * 2 + sn], fa[c][(pl * MI + i) * 2 + sm]);
           else mma16_acc<T>(c4[i][j][g], fb[c][j * 2 + sn], fa[c][(pl * MI + i) * 2 + sm]);
           if (m < NRD) read_one(rslot, rks, m, fa[c ^ 1], fb[c ^ 1]);
         } else {
