@@ -5,10 +5,10 @@
 // Large grids (>= 192 tiles of 256x256, K % 64 == 0): gemm_buf_kernel on the buffer
 // engine (BufPipeEngine, tile_engine.hpp).  Operands go straight from global memory into
 // LDS with buffer_load ... lds (no VGPR staging), two 64-wide K stages in flight, one
-// barrier per stage.  K-contiguous B runs 8 waves (2 x 4, 128 x 64 each, two per SIMD) on
-// 16x16x32 MFMAs; an N-contiguous B (natural [K,N]) or an M-contiguous A (a transposed
-// view) is staged as K-rows and read back with the LDS transpose read
-// ds_read_b64_tr_b16.  LDS rows are 128 bytes with an XOR swizzle of the 16-byte chunks.
+// barrier per stage, 16x16x32 MFMAs.  K-contiguous B runs 4 waves (2 x 2, 128 x 128 each,
+// one per SIMD, the accumulators held in place in AGPRs); an N-contiguous B (natural [K,N])
+// or an M-contiguous A (a transposed view) runs 8 waves (2 x 4, 128 x 64 each, two per
+// SIMD), staged as K-rows and read back with the LDS transpose read ds_read_b64_tr_b16.  LDS rows are 128 bytes with an XOR swizzle of the 16-byte chunks.
 // The MFMA is issued with the B fragment as the first operand, so each lane holds 4
 // N-consecutive outputs of one row; the epilogue applies bias and the activation in fp32,
 // packs, stages the wave's tile in LDS and writes C with 16-byte row-contiguous stores.

@@ -294,9 +294,10 @@ namespace kore {
 // ---------------------------------------------------------------------------------
 // Buffer-load pipelined engine (the production dense/grouped GEMM main loop).
 //
-// 4 waves (one per SIMD, 128x128 wave tiles, AGPR accumulators), two 64-wide K
-// stages, one barrier per K step; the next stage's loads are spread over the MFMAs
-// and fragments are read one 16-wide sub-step ahead.  The direct-to-LDS loads are
+// 4 waves (one per SIMD, wave tiles up to 128x128, accumulators in AGPRs) or 8 waves
+// (two per SIMD), two 64-wide K stages, one barrier per K step; the next stage's loads
+// are spread over the MFMAs and fragments are read one sub-step (32 K for the 16x16x32
+// MFMAs, 16 K for 32x32x16) ahead.  The direct-to-LDS loads are
 // buffer_load_dwordx4 ... lds with a buffer resource per operand, a per-lane byte
 // offset fixed at setup (row and swizzled chunk) and the K advance in the scalar
 // offset -- no per-load vector address arithmetic, which otherwise costs more issue
