@@ -151,6 +151,31 @@ def test_gemm_nc_buffer_engine(gpu, M, N, K, dtype, op, strided):
     pair_only(out, ref, dt, f"nc {op} {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("M,N,K,dtype,op", [(4000, 3900, 4096, torch.bfloat16, "gemm_bias_gelu"),
+                                             (3000, 4104, 1024, torch.float16, "gemm_bias_silu"),
+                                             (2048, 7168, 4096, torch.bfloat16, "gemm"),
+                                             (3841, 3336, 512, torch.float16, "gemm_relu")])
+@pytest.mark.parametrize("strided", [False, True])
+def test_gemm_kc_buffer_engine(gpu, M, N, K, dtype, op, strided):
+    """K-contiguous B (a W[N,K].t() view) at >= 192 tiles of 256x256 runs the 4-wave tile with
+    its accumulators in AGPRs: ragged M and N, fused epilogues, and W rows wider than K (row
+    stride K + 64) read in place."""
+    has_bias, act = kore_amd.GEMM_FUSION_OPS.get(op, (False, "none"))
+    g = torch.Generator().manual_seed(M + N + K + 1)
+    sc = 1.0 / K ** 0.5
+    a = (torch.randn((M, K), generator=g) * sc).to(dtype)
+    wfull = (torch.randn((N, K + 64), generator=g) * sc).to(dtype)
+    w = wfull[:, 32:32 + K] if strided else wfull[:, :K].contiguous()
+    bias = torch.randn((N,), generator=g).to(dtype) if has_bias else None
+    wd = wfull.to(gpu)[:, 32:32 + K] if strided else w.to(gpu)
+    assert wd.stride(1) == 1 and wd.stride(0) == (K + 64 if strided else K)
+    out = kore_amd.gemm_fused(a.to(gpu), wd.t(), bias.to(gpu) if has_bias else None, act)
+    ref = gemm_fusion_ref(a, w.t(), bias, act)
+    dt = "bf16" if dtype == torch.bfloat16 else "fp16"
+    verdict(out, ref, "gemm_fusion", dt, f"kc {op} {M}x{N}x{K} strided={strided}")
+    pair_only(out, ref, dt, f"kc {op} {M}x{N}x{K}")
+
+
 @pytest.mark.parametrize("M,N,K,dtype,op", [(2048, 2048, 2048, torch.bfloat16, "gemm"),
                                              (1024, 4096, 4096, torch.float16, "gemm_bias_gelu"),
                                              (256, 14336, 4096, torch.bfloat16, "gemm_bias_silu"),
