@@ -241,7 +241,7 @@ int kore_fused_moe(const void* hidden, int64_t ldh, const void* w1, const void* 
  * Top-1 grouped (segmented) expert GEMM (bf16):
  *   out[m, :] = x[m, :] @ w[expert_ids[m]]^T,  fp32 accumulate, bf16 out in token order
  *   x [M,K] row stride ldx; w [E,N,K] contiguous; expert_ids [M] int32 (ids outside
- *   [0,E) leave their row unwritten); out [M,N] row stride ldo.  Tokens are sorted
+ *   [0,E) get a zero row); out [M,N] row stride ldo.  Tokens are sorted
  *   and block-aligned per expert on the device (the sort/align kernel above), then one
  *   grouped MFMA launch covers every expert.  `workspace` must hold
  *   kore_moe_grouped_gemm_workspace_bytes(M, E) bytes.  Requires N % 128 == 0 and
@@ -261,7 +261,8 @@ int kore_moe_grouped_gemm(const void* x, int64_t ldx, const void* w, const int32
  *   out[m, :] = xs[m] * ws[e, :] * (xq[m, :] . wq[e, :, :]^T),  e = expert_ids[m]
  *   xq [M,K] fp8 (row stride ldx bytes), wq [E,N,K] fp8 contiguous, xs per token
  *   (xs[m * xs_stride]), ws [E,N] fp32 contiguous (per expert, per output channel),
- *   fp32 accumulation, one bf16 rounding; rows with ids outside [0,E) are unwritten.
+ *   fp32 accumulation, one bf16 rounding; rows with ids outside [0,E) are zeroed when ldo % 8
+ *   == 0 and out is 16-byte aligned, else left unwritten.
  *   Same workspace as kore_moe_grouped_gemm.  Requires N % 128 == 0, K % 128 == 0 and
  *   16-byte aligned rows (KORE_EUNSUPPORTED / KORE_EINVAL otherwise).
  * Replaces: grouped_gemm_fp8(xq, wq, x_scale, w_scale, expert_ids)

@@ -47,13 +47,16 @@ constexpr int kAlignMaxE = 1024;
 // the last term from per-wave expert counts and a scan of the wave's ids, so the order
 // inside an expert is ascending slot order, as in the oracle.  The workgroups split the padding
 // sentinels, the tail past the last expert and the block owners between them;
-// workgroup 0 writes the offsets.
+// workgroup 0 writes the offsets.  With zrows set (the top-1 grouped GEMMs, slot = output
+// row) a slot whose id is outside [0, E) zeroes its output row (zcols bf16 values, a
+// multiple of 8, 16-byte aligned rows), so the caller need not clear the whole output.
 constexpr int kChunk = 256;
 
 __global__ void __launch_bounds__(kChunk)
     moe_align_chunk_kernel(const int32_t* __restrict__ ids, int S, int E, int block, int R,
                            int32_t* __restrict__ offsets, int32_t* __restrict__ sorted,
-                           int32_t* __restrict__ block_expert, int cap) {
+                           int32_t* __restrict__ block_expert, int cap, uint16_t* __restrict__ zrows,
+                           int64_t ldz, int zcols) {
   __shared__ int hist[kAlignMaxE], pre[kAlignMaxE], base[kAlignMaxE];
   __shared__ int wcnt[kChunk / 64][kAlignMaxE];  // per-wave expert counts of a sub-chunk
   __shared__ __attribute__((aligned(16))) int cid[kChunk];
@@ -132,6 +135,10 @@ __global__ void __launch_bounds__(kChunk)
     const int my_s = (first + r) * kChunk + tid;
     const int my_e = r == 0 ? my_e0 : (my_s < S ? ids[my_s] : -1);
     const bool valid = my_e >= 0 && my_e < E;
+    if (!valid && zrows != nullptr && my_s < S) {
+      uint4* row = (uint4*)(zrows + (int64_t)my_s * ldz);
+      for (int c = 0; c < zcols / 8; ++c) row[c] = uint4{0u, 0u, 0u, 0u};
+    }
     cid[tid] = my_e;
     if (valid) atomicAdd(&wcnt[wave][my_e], 1);
     __syncthreads();
@@ -719,12 +726,13 @@ int g_force_generic = 0;
 
 // Sort/align of S slots: the chunked kernel, one workgroup per 256 slots.
 int launch_align(const int32_t* ids, int64_t S, int64_t E, int block, int32_t* offsets, int32_t* sorted,
-                 int32_t* block_expert, int64_t cap, hipStream_t st) {
+                 int32_t* block_expert, int64_t cap, hipStream_t st, uint16_t* zrows = nullptr, int64_t ldz = 0,
+                 int zcols = 0) {
   const int64_t chunks = std::max<int64_t>(1, (S + kChunk - 1) / kChunk);
   const int R = (int)((chunks + 255) / 256);  // sub-chunks per workgroup: at most 256 workgroups
   const int grid = (int)((chunks + R - 1) / R);
   hipLaunchKernelGGL(moe_align_chunk_kernel, dim3((unsigned)grid), dim3(kChunk), 0, st, ids, (int)S, (int)E, block, R,
-                     offsets, sorted, block_expert, (int)cap);
+                     offsets, sorted, block_expert, (int)cap, zrows, ldz, zcols);
   return check_launch("moe_align_chunk_kernel");
 }
 }  // namespace
@@ -939,7 +947,8 @@ extern "C" int kore_moe_grouped_gemm(const void* x, int64_t ldx, const void* w, 
                      kore_moe_grouped_gemm_workspace_bytes(M, E));
   hipStream_t st = (hipStream_t)stream;
   const int64_t cap = align_capacity(M, E, BM);
-  int rc = launch_align(expert_ids, M, E, BM, ws.offsets, ws.sorted, ws.block_expert, cap, st);
+  int rc = launch_align(expert_ids, M, E, BM, ws.offsets, ws.sorted, ws.block_expert, cap, st, (uint16_t*)out, ldo,
+                        (int)N);
   if (rc) return rc;
   MoeGemmParams p{};
   p.x = (const uint16_t*)x;
@@ -995,7 +1004,10 @@ extern "C" int kore_moe_grouped_gemm_fp8(const void* xq, int64_t ldx, const void
   const GroupedWorkspace w = carve_grouped(workspace, M, E, BM);
   const int64_t cap = align_capacity(M, E, BM);
   hipStream_t st = (hipStream_t)stream;
-  int rc = launch_align(expert_ids, M, E, BM, w.offsets, w.sorted, w.block_expert, cap, st);
+  // rows of invalid ids are zeroed by the align kernel with 16-byte stores when out allows them
+  const bool zok = ldo % 8 == 0 && ((uintptr_t)out & 15u) == 0;
+  int rc = launch_align(expert_ids, M, E, BM, w.offsets, w.sorted, w.block_expert, cap, st,
+                        zok ? (uint16_t*)out : nullptr, ldo, (int)N);
   if (rc) return rc;
   GroupedA8Args a{};
   a.xq = xq;

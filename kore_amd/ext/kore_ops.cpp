@@ -284,8 +284,9 @@ at::Tensor grouped_gemm(const at::Tensor& x_, const at::Tensor& w_, const at::Te
   const at::Tensor x = x_.stride(1) == 1 && x_.stride(0) % 8 == 0 ? x_ : x_.contiguous();
   const at::Tensor w = w_.contiguous();
   const c10::DeviceGuard guard(x.device());
-  at::Tensor out = at::zeros({M, N}, x.options());
-  if (M == 0 || N == 0 || K == 0 || E == 0) return out;
+  // the library zeroes the rows of ids outside [0, E); every other row is written
+  at::Tensor out = at::empty({M, N}, x.options());
+  if (M == 0 || N == 0 || K == 0 || E == 0) return out.zero_();
   at::Tensor ws = workspace(kore_moe_grouped_gemm_workspace_bytes(M, E), x);
   check_rc(kore_moe_grouped_gemm(x.data_ptr(), x.stride(0), w.data_ptr(), ids.data_ptr<int32_t>(), out.data_ptr(),
                                  out.stride(0), M, N, K, E, ptr_or_null(ws), bytes_of(ws), stream_of(x)));
@@ -312,8 +313,10 @@ at::Tensor grouped_gemm_fp8(const at::Tensor& xq_, const at::Tensor& wq_, const 
   const at::Tensor wq = wq_.contiguous();
   const at::Tensor wsc = wsc_.reshape({E, N}).contiguous();
   const c10::DeviceGuard guard(xq.device());
-  at::Tensor out = at::zeros({M, N}, xq.options().dtype(at::kBFloat16));
-  if (M == 0 || N == 0 || K == 0 || E == 0) return out;
+  // contiguous bf16 rows (N % 128 == 0 here): the library zeroes the rows of ids outside
+  // [0, E) and writes every other row
+  at::Tensor out = at::empty({M, N}, xq.options().dtype(at::kBFloat16));
+  if (M == 0 || N == 0 || K == 0 || E == 0) return out.zero_();
   at::Tensor ws = workspace(kore_moe_grouped_gemm_workspace_bytes(M, E), xq);
   check_rc(kore_moe_grouped_gemm_fp8(xq.data_ptr(), xq.stride(0), wq.data_ptr(), xs.data_ptr<float>(), xs_st,
                                      wsc.data_ptr<float>(), ids.data_ptr<int32_t>(), out.data_ptr(), out.stride(0), M,
