@@ -1561,6 +1561,87 @@ __global__ void __launch_bounds__(256) gemm_a8w8_generic_kernel(const A8GenericP
   }
 }
 
+// int8 a8w8 on the dense 4-wave tile (BufPipeEngine, as the bf16 GEMM): int8 rows are
+// 128-byte stage rows like the 16-bit ones (K = 128 per stage), the 16x16x64 int8 MFMA reads
+// the same 16-byte chunks as the 16x16x32 bf16 one, and the int32 accumulators stay in place
+// in AGPRs.  Epilogue as the row-scale pipe kernel: float(acc) * xs[m] * ws[n], one bf16
+// rounding.  Requires N % 256 == 0, K % 128 == 0, 16-byte aligned rows.
+__global__ void __launch_bounds__(256) gemm_i8_buf_kernel(const Fp8Params p) {
+  using E = BufPipeEngine<INT8, 256, 256, 2, 2, 1, B_KC, kCpolDefault, true, A_KC>;
+  constexpr int MI = E::MI, NI = E::NI;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / E::WN, wn = wave % E::WN;
+  const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int width = kFp8GroupM * p.tiles_n;
+  const int grp = bid / width;
+  const int first_m = grp * kFp8GroupM;
+  const int gsz = min(p.tiles_m - first_m, kFp8GroupM);
+  const int tl = bid - grp * width;
+  const int m0 = (first_m + tl % gsz) * 256, n0 = (tl / gsz) * 256;
+  const int rows_a = min(256, p.M - m0);
+  E eng;
+  eng.ra = make_rsrc(p.xq + (int64_t)m0 * p.ldx, (uint32_t)((int64_t)(rows_a - 1) * p.ldx + p.K));
+#pragma unroll
+  for (int j = 0; j < E::AJ; ++j) {
+    const int r = E::a_row(wave, lane, j);
+    eng.a_voff[j] = (uint32_t)((int64_t)min(r, rows_a - 1) * p.ldx + 16 * E::chunk(r, lane));
+  }
+  eng.rb = make_rsrc(p.wq + (int64_t)n0 * p.ldw, (uint32_t)(255 * p.ldw + p.K));
+#pragma unroll
+  for (int j = 0; j < E::BJ; ++j) {
+    const int r = E::b_row(wave, lane, j);
+    eng.b_voff[j] = (uint32_t)((int64_t)r * p.ldw + 16 * E::chunk(r, lane));
+  }
+  f32x4_t acc[MI][NI][4];
+  E::zero16(acc);
+  eng.mainloop16(lds, p.K / 2, acc);  // K in 16-bit units: 64 per 128-byte stage
+
+  using St = Stager<E::WROWS, E::WCOLS>;
+  using Op = MfmaOp<BF16>;
+  uint16_t* stg = lds + wave * (E::WROWS * E::WCOLS);
+  const int mw0 = m0 + wm * E::WROWS, nw0 = n0 + wn * E::WCOLS;
+#pragma unroll
+  for (int j = 0; j < NI; ++j)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int nl = acc_col<true>(j, g, lane);
+      float wcol[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wcol[e] = p.ws[(int64_t)(nw0 + nl + e) * p.ws_n];
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int ml = acc_row<true>(i, g, lane);
+        const float xr = p.xs[(int64_t)min(mw0 + ml, p.M - 1) * p.xs_m];
+        // reinterpret the whole 4-register tuple (casting single extracted elements of an
+        // inline-asm AGPR result miscompiled: every element read the first register)
+        const i32x4_t ai = __builtin_bit_cast(i32x4_t, acc[i][j][g]);
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = (float)ai[e];
+          v[e] = v[e] * xr * wcol[e];
+        }
+        St::put(stg, ml, nl, u32x2_t{Op::pack2(v[0], v[1]), Op::pack2(v[2], v[3])});
+      }
+    }
+  __syncthreads();
+  const bool vec = p.vec_store != 0;
+  St::drain(stg, lane, [&](int row, int col, u32x4_t v) {
+    const int gm = mw0 + row, gn = nw0 + col;
+    if (gm < p.M) store_row8(p.y + (int64_t)gm * p.ldy + gn, gn, p.N, vec, v);
+  });
+}
+
+int launch_i8_buf(Fp8Params p, hipStream_t st) {
+  p.tiles_m = (p.M + 255) / 256;
+  p.tiles_n = p.N / 256;
+  const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n;
+  if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "gemm_a8w8: grid too large");
+  hipLaunchKernelGGL(gemm_i8_buf_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p);
+  return check_launch("gemm_i8_buf_kernel");
+}
+
 template <int MODE>
 int launch_a8w8(const Fp8Params& p0, bool skinny, hipStream_t st) {
   Fp8Params p = p0;
@@ -1581,6 +1662,12 @@ int launch_a8w8(const Fp8Params& p0, bool skinny, hipStream_t st) {
   const int64_t tiles256 = (int64_t)(p.M + 255) / 256 * (p.N / 256);
   const int64_t tiles256x128 = (int64_t)(p.M + 255) / 256 * (p.N / 128);
   const int64_t tiles128 = (int64_t)(p.M + 127) / 128 * (p.N / 128);
+  if constexpr (MODE == Q_ROW_I8) {
+    // the dense 4-wave tile with int32 accumulators in AGPRs (same process, bit-equal:
+    // 4096^3 65.6 -> 56.6 us, 8192 x 4096 x 4096 128.4 -> 112.1 us, 2048 x 7168 x 4096
+    // 60.2 -> 51.6 us, cold 4096^3 67.4 -> 59.2 us against the 8-wave pipe kernel)
+    if (p.N % 256 == 0 && tiles256 >= 192) return launch_i8_buf(p, st);
+  }
   if (p.N % 256 == 0 && tiles256 >= 192) return launch_fp8_pipe<F8Cfg<256, 256, 8, 2, false, MODE>>(p, st);
   if (tiles256x128 >= 192 || tiles128 > device_cus())
     return launch_fp8_pipe<F8Cfg<256, 128, 8, 3, false, MODE>>(p, st);

@@ -35,6 +35,7 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // the MFMA opcode and the final conversion.
 struct BF16 {};
 struct F16 {};
+struct INT8 {};  // int8 operands (a8w8): bytes staged like the 16-bit ones, i32 accumulators
 
 template <typename T> struct MfmaOp;
 template <> struct MfmaOp<BF16> {
@@ -71,6 +72,12 @@ template <> __device__ __forceinline__ void mma16_acc<BF16>(f32x4_t& c, u32x4_t 
 template <> __device__ __forceinline__ void mma16_acc<F16>(f32x4_t& c, u32x4_t a, u32x4_t b) {
   asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
 }
+// int8 on the same layout: v_mfma_i32_16x16x64_i8 takes 16 bytes per lane (row l % 16, K
+// bytes 16 (l / 16) .. + 15 of a 64-byte sub-step, the chunks the 16-bit engines read) and
+// accumulates int32 bit patterns in the f32x4_t registers.
+template <> __device__ __forceinline__ void mma16_acc<INT8>(f32x4_t& c, u32x4_t a, u32x4_t b) {
+  asm("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
 // First product of an accumulator: the same MFMA with an inline-constant zero for srcC, so
 // no VALU instruction writes the accumulators before the MFMAs read them.
 template <typename T> __device__ __forceinline__ void mma16_acc0(f32x4_t& c, u32x4_t a, u32x4_t b);
@@ -79,6 +86,9 @@ template <> __device__ __forceinline__ void mma16_acc0<BF16>(f32x4_t& c, u32x4_t
 }
 template <> __device__ __forceinline__ void mma16_acc0<F16>(f32x4_t& c, u32x4_t a, u32x4_t b) {
   asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
+}
+template <> __device__ __forceinline__ void mma16_acc0<INT8>(f32x4_t& c, u32x4_t a, u32x4_t b) {
+  asm("v_mfma_i32_16x16x64_i8 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
 }
 // Wait states around a run of mma16_acc (scheduling fences keep other instructions from
 // moving across).
