@@ -1561,13 +1561,16 @@ __global__ void __launch_bounds__(256) gemm_a8w8_generic_kernel(const A8GenericP
   }
 }
 
-// int8 a8w8 on the dense 4-wave tile (BufPipeEngine, as the bf16 GEMM): int8 rows are
-// 128-byte stage rows like the 16-bit ones (K = 128 per stage), the 16x16x64 int8 MFMA reads
-// the same 16-byte chunks as the 16x16x32 bf16 one, and the int32 accumulators stay in place
-// in AGPRs.  Epilogue as the row-scale pipe kernel: float(acc) * xs[m] * ws[n], one bf16
-// rounding.  Requires N % 256 == 0, K % 128 == 0, 16-byte aligned rows.
-__global__ void __launch_bounds__(256) gemm_i8_buf_kernel(const Fp8Params p) {
-  using E = BufPipeEngine<INT8, 256, 256, 2, 2, 1, B_KC, kCpolDefault, true, A_KC>;
+// a8w8 (per-token / per-channel scales) on the dense 4-wave tile (BufPipeEngine, as the bf16
+// GEMM): 8-bit rows are 128-byte stage rows like the 16-bit ones (K = 128 per stage) and the
+// accumulators stay in place in AGPRs.  int8: 16x16x64 MFMAs on the same 16-byte chunks as
+// the 16x16x32 bf16 ones (mainloop16), int32 accumulators; fp8: 16x16x128 MFMAs on both
+// chunks of a stage (mainloop_f8).  Epilogue as the row-scale pipe kernel: float(acc) *
+// xs[m] * ws[n], one bf16 rounding.  Requires N % 256 == 0, K % 128 == 0, 16-byte aligned rows.
+template <int MODE>
+__global__ void __launch_bounds__(256) gemm_a8w8_buf_kernel(const Fp8Params p) {
+  constexpr bool I8 = MODE == Q_ROW_I8;
+  using E = BufPipeEngine<std::conditional_t<I8, INT8, FP8>, 256, 256, 2, 2, 1, B_KC, kCpolDefault, true, A_KC>;
   constexpr int MI = E::MI, NI = E::NI;
   __shared__ __attribute__((aligned(16))) uint16_t lds[E::LDS_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1595,7 +1598,8 @@ __global__ void __launch_bounds__(256) gemm_i8_buf_kernel(const Fp8Params p) {
   }
   f32x4_t acc[MI][NI][4];
   E::zero16(acc);
-  eng.mainloop16(lds, p.K / 2, acc);  // K in 16-bit units: 64 per 128-byte stage
+  if constexpr (I8) eng.mainloop16(lds, p.K / 2, acc);  // K in 16-bit units: 64 per 128-byte stage
+  else eng.mainloop_f8(lds, p.K / 2, acc);
 
   using St = Stager<E::WROWS, E::WCOLS>;
   using Op = MfmaOp<BF16>;
@@ -1613,13 +1617,13 @@ __global__ void __launch_bounds__(256) gemm_i8_buf_kernel(const Fp8Params p) {
       for (int i = 0; i < MI; ++i) {
         const int ml = acc_row<true>(i, g, lane);
         const float xr = p.xs[(int64_t)min(mw0 + ml, p.M - 1) * p.xs_m];
-        // reinterpret the whole 4-register tuple (casting single extracted elements of an
-        // inline-asm AGPR result miscompiled: every element read the first register)
+        // int8: reinterpret the whole 4-register tuple (casting single extracted elements of
+        // an inline-asm AGPR result miscompiled: every element read the first register)
         const i32x4_t ai = __builtin_bit_cast(i32x4_t, acc[i][j][g]);
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          v[e] = (float)ai[e];
+          v[e] = I8 ? (float)ai[e] : acc[i][j][g][e];
           v[e] = v[e] * xr * wcol[e];
         }
         St::put(stg, ml, nl, u32x2_t{Op::pack2(v[0], v[1]), Op::pack2(v[2], v[3])});
@@ -1633,13 +1637,14 @@ __global__ void __launch_bounds__(256) gemm_i8_buf_kernel(const Fp8Params p) {
   });
 }
 
-int launch_i8_buf(Fp8Params p, hipStream_t st) {
+template <int MODE>
+int launch_a8w8_buf(Fp8Params p, hipStream_t st) {
   p.tiles_m = (p.M + 255) / 256;
   p.tiles_n = p.N / 256;
   const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n;
   if (blocks > 0x7fffffff) return set_error(KORE_EUNSUPPORTED, "gemm_a8w8: grid too large");
-  hipLaunchKernelGGL(gemm_i8_buf_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p);
-  return check_launch("gemm_i8_buf_kernel");
+  hipLaunchKernelGGL((gemm_a8w8_buf_kernel<MODE>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+  return check_launch("gemm_a8w8_buf_kernel");
 }
 
 template <int MODE>
@@ -1662,12 +1667,15 @@ int launch_a8w8(const Fp8Params& p0, bool skinny, hipStream_t st) {
   const int64_t tiles256 = (int64_t)(p.M + 255) / 256 * (p.N / 256);
   const int64_t tiles256x128 = (int64_t)(p.M + 255) / 256 * (p.N / 128);
   const int64_t tiles128 = (int64_t)(p.M + 127) / 128 * (p.N / 128);
-  if constexpr (MODE == Q_ROW_I8) {
-    // the dense 4-wave tile with int32 accumulators in AGPRs (same process, bit-equal:
-    // 4096^3 65.6 -> 56.6 us, 8192 x 4096 x 4096 128.4 -> 112.1 us, 2048 x 7168 x 4096
-    // 60.2 -> 51.6 us, cold 4096^3 67.4 -> 59.2 us against the 8-wave pipe kernel)
-    if (p.N % 256 == 0 && tiles256 >= 192) return launch_i8_buf(p, st);
-  }
+  // the dense 4-wave tile with the accumulators in AGPRs, where K is deep enough to carry
+  // its prologue and its 4-wave epilogue (same process, bit-equal, against the 8-wave pipe
+  // kernel).  int8: 4096^3 65.6 -> 56.6 us, 8192 x 4096 x 4096 128.4 -> 112.1 us,
+  // 2048 x 7168 x 4096 58.5 -> 50.7 us, 4096 x 8192 x 2048 73.5 -> 68.3 us; K = 1024 slower
+  // (4096^2 x 1024 24.9 -> 25.3 us).  fp8: 4096^3 55.6 -> 54.9 us, 8192 x 4096 x 4096
+  // 110.1 -> 107.1 us, cold 4096^3 57.9 -> 56.4 us; K = 3072 and below slower (4096^2 x
+  // 2048 34.0 -> 36.2 us).
+  const int kmin_buf = MODE == Q_ROW_I8 ? 2048 : 4096;
+  if (p.N % 256 == 0 && tiles256 >= 192 && p.K >= kmin_buf) return launch_a8w8_buf<MODE>(p, st);
   if (p.N % 256 == 0 && tiles256 >= 192) return launch_fp8_pipe<F8Cfg<256, 256, 8, 2, false, MODE>>(p, st);
   if (tiles256x128 >= 192 || tiles128 > device_cus())
     return launch_fp8_pipe<F8Cfg<256, 128, 8, 3, false, MODE>>(p, st);

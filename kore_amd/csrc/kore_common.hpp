@@ -36,6 +36,7 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 struct BF16 {};
 struct F16 {};
 struct INT8 {};  // int8 operands (a8w8): bytes staged like the 16-bit ones, i32 accumulators
+struct FP8 {};   // fp8 (OCP e4m3) operands on the same byte layout (BufPipeEngine::mainloop_f8)
 
 template <typename T> struct MfmaOp;
 template <> struct MfmaOp<BF16> {
@@ -89,6 +90,14 @@ template <> __device__ __forceinline__ void mma16_acc0<F16>(f32x4_t& c, u32x4_t 
 }
 template <> __device__ __forceinline__ void mma16_acc0<INT8>(f32x4_t& c, u32x4_t a, u32x4_t b) {
   asm("v_mfma_i32_16x16x64_i8 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
+}
+// fp8 (OCP e4m3) 16x16x128 on AGPR accumulators in place, 32 bytes per lane (two 16-byte
+// chunks); first product with a zero srcC, as above.
+__device__ __forceinline__ void mma16_f8_acc(f32x4_t& c, i32x8_t a, i32x8_t b) {
+  asm("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mma16_f8_acc0(f32x4_t& c, i32x8_t a, i32x8_t b) {
+  asm("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
 }
 // Wait states around a run of mma16_acc (scheduling fences keep other instructions from
 // moving across).

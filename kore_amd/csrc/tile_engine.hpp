@@ -794,6 +794,104 @@ struct BufPipeEngine {
     wait_vmcnt<0>();  // drain the clamped trailing loads before LDS is reused
     __syncthreads();
   }
+  // fp8 (e4m3) operands on the same byte layout (4 waves, K-contiguous A and B): one
+  // 16x16x128 MFMA per 16x16 sub-tile and 128-byte stage.  Lane l of a fragment holds the
+  // two 16-byte chunks the 16x16x32 engine reads in its two sub-steps (K bytes 16 (l / 16)
+  // + [0, 16) and 64 + 16 (l / 16) + [0, 16)); A and B take the same K permutation, so each
+  // MFMA still sums all 128 products of a stage.  One barrier per stage, early in it (stage
+  // s + 1 landed, every wave done reading stage s), then the direct loads of stage s + 2 into
+  // the slot stage s leaves; each fragment of the next stage is read right after its last
+  // use in this one (A blocks after their row of tiles, B blocks in the last row; 32-byte
+  // fragments of two stages do not fit the registers).  K in 16-bit units (64 per stage).
+  __device__ __forceinline__ void mainloop_f8(uint16_t* lds, int K, f32x4_t (&c4)[MI][NI][4]) {
+    static_assert(NW == 4 && !NC && !AMC && AP == 1 && M16, "fp8 main loop: 4 waves, K-contiguous operands");
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    const int r16 = lane & 15, g4 = lane >> 4;
+    const int rowA0 = wm * WROWS, rowB0 = wn * WCOLS;
+    int offA[2][2][2], offB[2][2][2];
+#pragma unroll
+    for (int par = 0; par < 2; ++par)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const int ra = rowA0 + 32 * par + 16 * h + r16, rb = rowB0 + 32 * par + 16 * h + r16;
+          offA[par][h][ks] = (16 * h + r16) * kBK + (((4 * ks + g4) ^ row_key(ra)) << 3);
+          offB[par][h][ks] = (16 * h + r16) * kBK + (((4 * ks + g4) ^ row_key(rb)) << 3);
+        }
+    constexpr int NFA = MI * 2, NFB = NI * 2;
+    auto read_f = [&](int slot, int f, i32x8_t& dst) {
+      const uint16_t* base;
+      const int* o;
+      if (f < NFA) {
+        const int i = f / 2, h = f & 1;
+        base = lds + slot * STAGE + (rowA0 + 32 * i) * kBK;
+        o = offA[i & 1][h];
+      } else {
+        const int j = (f - NFA) / 2, h = (f - NFA) & 1;
+        base = lds + slot * STAGE + B_OFF + (rowB0 + 32 * j) * kBK;
+        o = offB[j & 1][h];
+      }
+      const u32x4_t lo = *(const u32x4_t*)(base + o[0]), hi = *(const u32x4_t*)(base + o[1]);
+      dst = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    };
+    const int nk = K / kBK;
+    if (nk == 0) return;
+    constexpr int NMMA = MI * NI * 4;
+    static_assert(NFB <= NMMA && LPS <= NMMA && LPS <= 32, "interleave needs enough MFMAs; vmcnt range");
+    const uint32_t kmax = (uint32_t)(nk - 1) * (kBK * 2);
+    auto soff_of = [&](int stage) { return min((uint32_t)stage * (kBK * 2), kmax); };
+#pragma unroll
+    for (int q = 0; q < LPS; ++q) issue_one(lds, 0, 0u, 0u, wave, q);
+#pragma unroll
+    for (int q = 0; q < LPS; ++q) issue_one(lds, 1, soff_of(1), soff_of(1), wave, q);
+    wait_vmcnt<LPS>();
+    exec_barrier();
+    i32x8_t fa[NFA], fb[NFB];
+#pragma unroll
+    for (int f = 0; f < NFA; ++f) read_f(0, f, fa[f]);
+#pragma unroll
+    for (int f = 0; f < NFB; ++f) read_f(0, NFA + f, fb[f]);
+    // stage s: its MFMAs, the reads of stage s + 1 and the direct loads of stage s + 2 (into
+    // the slot stage s leaves).  The barrier comes after BARM MFMAs (they hide the
+    // lgkmcnt(0) wait for the last fragment reads of the stage before), the loads every EV
+    // MFMAs from there: the last of
+    // them leaves NMMA - BARM - (LPS - 1) EV MFMAs of lead before the next barrier.  A
+    // barrier at the phase's start with loads spread over all of it measured slower (same
+    // process, bit-equal: 4096^3 58.7 against 54.9 us); EV = 1 too (57.5 us).
+    constexpr int BARM = 4, EV = 2;
+    static_assert(BARM < NI * 4 - 3 && BARM + (LPS - 1) * EV < NMMA, "barrier before the first read");
+    auto phase = [&](int s, auto firstc) {
+      constexpr bool first = decltype(firstc)::value;
+      const int slot = s & 1, nslot = slot ^ 1;
+      const uint32_t soff2 = soff_of(s + 2);
+#pragma unroll
+      for (int m = 0; m < NMMA; ++m) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (m == BARM) {
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          wait_vmcnt<0>();
+          exec_barrier();
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        const int i = m / (NI * 4), j = (m / 4) % NI, g = m & 3;
+        const int sm = g >> 1, sn = g & 1;
+        if constexpr (first) mma16_f8_acc0(c4[i][j][g], fb[j * 2 + sn], fa[i * 2 + sm]);
+        else mma16_f8_acc(c4[i][j][g], fb[j * 2 + sn], fa[i * 2 + sm]);
+        if (j == NI - 1 && (g & 1)) read_f(nslot, i * 2 + sm, fa[i * 2 + sm]);
+        if (i == MI - 1 && g >= 2) read_f(nslot, NFA + j * 2 + sn, fb[j * 2 + sn]);
+        if (m >= BARM && (m - BARM) % EV == 0 && (m - BARM) / EV < LPS)
+          issue_one(lds, slot, soff2, soff2, wave, (m - BARM) / EV);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    phase(0, std::integral_constant<bool, true>());
+    for (int s = 1; s < nk; ++s) phase(s, std::integral_constant<bool, false>());
+    mma16_acc_fence();
+    wait_vmcnt<0>();  // drain the clamped trailing loads before LDS is reused
+    __syncthreads();
+  }
 };
 
 }  // namespace kore
