@@ -122,6 +122,28 @@ def test_a8w8_adversarial(gpu, kind, regime):
     verdict(out, matmul_a8w8_ref(xq, wq, s, ws), "a8w8", kind, f"{kind} {regime}")
 
 
+@pytest.mark.parametrize("kind,M,N,K", [("fp8", 3000, 4096, 4096), ("fp8", 2048, 7168, 8192),
+                                        ("int8", 3000, 4096, 2048), ("int8", 4000, 3840, 4096)])
+def test_a8w8_buffer_tile(gpu, kind, M, N, K):
+    """The dense 4-wave 256x256 tile (N % 256 == 0, at least 192 tiles, K from 4096 for fp8
+    and 2048 for int8): ragged M, and operands given as padded-row views, which must give
+    the contiguous operands' output bit for bit; the oracle on a row sample."""
+    xq, wq, xs, ws = W.a8w8_inputs(M, N, K, kind, "pertoken", seed=K + M)
+    xg, wg, xsg, wsg = xq.to(gpu), wq.to(gpu), xs.to(gpu), ws.to(gpu)
+    y = kore_amd.gemm_a8w8(xg, wg, xsg, wsg)
+    xp = torch.zeros(M, K + 128, dtype=xq.dtype, device=gpu)
+    xp[:, :K] = xg
+    wp = torch.zeros(N, K + 256, dtype=wq.dtype, device=gpu)
+    wp[:, :K] = wg
+    assert bit_equal(kore_amd.gemm_a8w8(xp[:, :K], wp[:, :K], xsg, wsg), y)
+    rows = torch.unique(torch.cat([torch.arange(0, M, max(1, M // 64)), torch.arange(M - 40, M)]))
+    ref = matmul_a8w8_ref(xq[rows], wq, xs[rows], ws)
+    out = y.cpu()[rows]
+    label = f"{kind} buffer tile {M}x{N}x{K}"
+    verdict(out, ref, "a8w8", kind, label)
+    verdict(out, ref, "north_star", kind, label + " (1e-2)")
+
+
 def test_a8w8_rejects_bad_inputs(gpu):
     xq, wq, xs, ws = W.a8w8_inputs(8, 128, 128, "fp8", "pertoken")
     with pytest.raises(ValueError):
