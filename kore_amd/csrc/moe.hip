@@ -415,9 +415,9 @@ __global__ void __launch_bounds__(64 * NWV)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / E::WN, wn = wave % E::WN;
 
-  const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
   int mb, nt;
   if constexpr (MODE == MOE_PLAIN) {
+    const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
     mb = bid % p.max_mblocks;
     nt = bid / p.max_mblocks;
   } else {
@@ -431,7 +431,20 @@ __global__ void __launch_bounds__(64 * NWV)
     // of up to 8 and down groups of up to 12 measured slower at T=16384 (13.44 ms).
     constexpr int GMAX = MODE == MOE_GATEUP ? 6 : 8;
     const int nT = p.ntiles;
-    if (bid >= (p.offsets[p.E] / BM) * nT) return;  // uniform: the whole workgroup leaves
+    // The grid is sized for the largest possible slot list; the live tiles are the first
+    // nreal logical ids.  They are spread over the XCDs by their own count (workgroup b
+    // runs on XCD b % 8, so the first n8 workgroups take contiguous eighths of them);
+    // remapped over the whole grid, the live ids filled the first XCDs' ranges and left
+    // the last ones short.  Same process, bit-equal, E=8 top-2 D=4096 I=14336: T=1024
+    // 1.472 -> 1.412 ms, T=2048 2.176 -> 2.035, T=4096 3.631 -> 3.601-3.634, T=8192
+    // 6.579 -> 6.509, T=16384 12.68 -> 12.61.  Skipping the 128-row halves that hold only
+    // padding (a per-workgroup scan of the experts' live blocks) measured slower: T=4096
+    // 3.85 ms.
+    const int nreal = (p.offsets[p.E] / BM) * nT;
+    const int n8 = (nreal + 7) & ~7;
+    if ((int)blockIdx.x >= n8) return;  // uniform: the whole workgroup leaves
+    const int bid = xcd_remap((int)blockIdx.x, n8);
+    if (bid >= nreal) return;
     int lo = 0, hi = p.E;  // largest e < E with offsets[e] / BM * nT <= bid (an expert with rows)
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
