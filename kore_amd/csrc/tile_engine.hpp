@@ -854,12 +854,12 @@ struct BufPipeEngine {
 #pragma unroll
     for (int f = 0; f < NFB; ++f) read_f(0, NFA + f, fb[f]);
     // stage s: its MFMAs, the reads of stage s + 1 and the direct loads of stage s + 2 (into
-    // the slot stage s leaves).  The barrier comes after BARM MFMAs (they hide the
-    // lgkmcnt(0) wait for the last fragment reads of the stage before), the loads every EV
-    // MFMAs from there: the last of
-    // them leaves NMMA - BARM - (LPS - 1) EV MFMAs of lead before the next barrier.  A
-    // barrier at the phase's start with loads spread over all of it measured slower (same
-    // process, bit-equal: 4096^3 58.7 against 54.9 us); EV = 1 too (57.5 us).
+    // the slot stage s leaves).  The barrier comes after BARM MFMAs, which hide the
+    // lgkmcnt(0) wait for the last fragment reads of the stage before, and before the first
+    // read of stage s + 1 (MFMA NI * 4 - 3).  The loads follow every EV MFMAs, so the last
+    // leaves NMMA - BARM - (LPS - 1) EV MFMAs of lead before the next barrier.  A barrier at
+    // the stage's start with the loads spread over all of it measured slower (same process,
+    // bit-equal: 4096^3 58.7 against 54.9 us); EV = 1 too (57.5 us).
     constexpr int BARM = 4, EV = 2;
     static_assert(BARM < NI * 4 - 3 && BARM + (LPS - 1) * EV < NMMA, "barrier before the first read");
     auto phase = [&](int s, auto firstc) {
