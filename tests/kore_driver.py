@@ -135,6 +135,24 @@ def _tasks() -> dict[str, Task]:
             lambda a: oq.matmul_blockscale_ref(*a),
             lambda a: _dequant_matmul(*a),
             atol=5e-1, rtol=5e-2, snr=25.0),
+        # gemm_fp8_a8w8_pertoken / gemm_int8_a8w8 (task.yaml: primary 4096^3, snr 25):
+        # dynamic per-token x scales [M,1], per-channel w scales [1,N]; the vendor path is
+        # hipBLASLt's row-scaled fp8 GEMM / the int8 GEMM with the scales applied after it
+        # (the tasks' own baseline, AITER gemm_a8w8, is absent here)
+        "gemm_fp8_a8w8_pertoken": Task(
+            "gemm", {"M": 4096, "N": 4096, "K": 4096},
+            lambda s, seed, dev: tuple(x.to(dev) for x in W.a8w8_inputs(s["M"], s["N"], s["K"], "fp8", "pertoken",
+                                                                         seed=seed)),
+            lambda a: oq.matmul_a8w8_ref(*a),
+            lambda a: torch._scaled_mm(a[0], a[1].t(), scale_a=a[2], scale_b=a[3], out_dtype=torch.bfloat16),
+            atol=5e-1, rtol=5e-2, snr=25.0),
+        "gemm_int8_a8w8": Task(
+            "gemm", {"M": 4096, "N": 4096, "K": 4096},
+            lambda s, seed, dev: tuple(x.to(dev) for x in W.a8w8_inputs(s["M"], s["N"], s["K"], "int8", "pertoken",
+                                                                         seed=seed)),
+            lambda a: oq.matmul_a8w8_ref(*a),
+            lambda a: (torch._int_mm(a[0], a[1].t()).float() * a[2] * a[3]).bfloat16(),
+            atol=5e-1, rtol=5e-2, snr=25.0),
         "fused_moe_silu_bf16": Task(
             "fused_moe", {"M": 256, "E": 32, "topk": 8, "D": 1024, "I": 768},
             lambda s, seed, dev: tuple(x.to(dev) for x in W.moe_inputs(s["M"], s["E"], s["topk"], s["D"], s["I"],

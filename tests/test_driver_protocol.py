@@ -41,7 +41,8 @@ def test_task_table_matches_candidates():
         assert f"def {t.entry}(" in path.read_text(), (name, t.entry)
 
 
-@pytest.mark.parametrize("task", ["gemm_bf16", "gemm_backward_bf16", "gen_gemm_bias_gelu_fp16"])
+@pytest.mark.parametrize("task", ["gemm_bf16", "gemm_backward_bf16", "gen_gemm_bias_gelu_fp16",
+                                  "gemm_fp8_a8w8_pertoken", "gemm_int8_a8w8"])
 def test_task_inputs_and_oracle_shapes(task):
     t = kd._tasks()[task]
     shape = {"M": 64, "N": 48, "K": 32}

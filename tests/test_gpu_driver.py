@@ -28,7 +28,9 @@ def _run(argv):
                                         ("gemm_fp8_a8w8_blockscale", "M=128,N=256,K=256"),
                                         ("genv_batched_gemm_bf16", "B=4,M=256,N=256,K=128"),
                                         ("fused_moe_silu_bf16", "M=32,E=8,topk=2,D=256,I=256"),
-                                        ("gemm_backward_bf16", "M=256,N=256,K=256")])
+                                        ("gemm_backward_bf16", "M=256,N=256,K=256"),
+                                        ("gemm_fp8_a8w8_pertoken", "M=300,N=512,K=1024"),
+                                        ("gemm_int8_a8w8", "M=300,N=512,K=1024")])
 def test_driver_correctness(gpu, task, shape):
     out = _run([task, "--shape", shape])
     v = kd.parse(out, kd._tasks()[task].snr)
@@ -54,7 +56,9 @@ def test_driver_bench_mode(gpu):
 
 @pytest.mark.parametrize("task,shape", [("fused_moe_silu_bf16", "M=64,E=8,topk=2,D=256,I=512"),
                                         ("gemm_fp8_a8w8_blockscale", "M=128,N=256,K=512"),
-                                        ("gemm_backward_bf16", "M=256,N=128,K=256")])
+                                        ("gemm_backward_bf16", "M=256,N=128,K=256"),
+                                        ("gemm_fp8_a8w8_pertoken", "M=256,N=512,K=512"),
+                                        ("gemm_int8_a8w8", "M=256,N=512,K=512")])
 def test_driver_reference_impls(gpu, task, shape):
     """The vendor-path implementations timed against the candidates compute the task:
     each agrees with the CPU oracle under the task's gate."""
