@@ -1688,11 +1688,11 @@ int launch_a8w8(const Fp8Params& p0, bool skinny, hipStream_t st) {
   // the dense 4-wave tile with the accumulators in AGPRs, where K is deep enough to carry
   // its prologue and its 4-wave epilogue (same process, bit-equal, against the 8-wave pipe
   // kernel).  int8: 4096^3 65.6 -> 56.6 us, 8192 x 4096 x 4096 128.4 -> 112.1 us,
-  // 2048 x 7168 x 4096 58.5 -> 50.7 us, 4096 x 8192 x 2048 73.5 -> 68.3 us; K = 1024 slower
-  // (4096^2 x 1024 24.9 -> 25.3 us).  fp8: 4096^3 55.6 -> 54.9 us, 8192 x 4096 x 4096
-  // 110.1 -> 107.1 us, cold 4096^3 57.9 -> 56.4 us; K = 3072 and below slower (4096^2 x
-  // 2048 34.0 -> 36.2 us).
-  const int kmin_buf = MODE == Q_ROW_I8 ? 2048 : 4096;
+  // 2048 x 7168 x 4096 58.5 -> 50.7 us, 4096 x 8192 x 2048 73.5 -> 68.3 us, 8192^2 x 1024
+  // 83.1 -> 78.6 us, 4096^2 x 1024 23.2 -> 22.5 us.  fp8: 4096^3 55.6 -> 52.0 us, 4096^2 x
+  // 3072 44.4 -> 41.0 us, 4096 x 8192 x 2048 61.8 -> 57.7 us, 4096^2 x 2048 32.7 -> 30.9 us;
+  // at K = 1024 a tie (4096^2 21.4 either way, 3072 x 4096 19.3 against 19.6 us).
+  const int kmin_buf = MODE == Q_ROW_I8 ? 1024 : 2048;
   if (p.N % 256 == 0 && tiles256 >= 192 && p.K >= kmin_buf) return launch_a8w8_buf<MODE>(p, st);
   if (p.N % 256 == 0 && tiles256 >= 192) return launch_fp8_pipe<F8Cfg<256, 256, 8, 2, false, MODE>>(p, st);
   if (tiles256x128 >= 192 || tiles128 > device_cus())

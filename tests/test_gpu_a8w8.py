@@ -123,10 +123,11 @@ def test_a8w8_adversarial(gpu, kind, regime):
 
 
 @pytest.mark.parametrize("kind,M,N,K", [("fp8", 3000, 4096, 4096), ("fp8", 2048, 7168, 8192),
-                                        ("int8", 3000, 4096, 2048), ("int8", 4000, 3840, 4096)])
+                                        ("fp8", 3000, 4096, 2048), ("int8", 3000, 4096, 2048),
+                                        ("int8", 4000, 3840, 4096), ("int8", 3500, 4096, 1024)])
 def test_a8w8_buffer_tile(gpu, kind, M, N, K):
-    """The dense 4-wave 256x256 tile (N % 256 == 0, at least 192 tiles, K from 4096 for fp8
-    and 2048 for int8): ragged M, and operands given as padded-row views, which must give
+    """The dense 4-wave 256x256 tile (N % 256 == 0, at least 192 tiles, K from 2048 for fp8
+    and 1024 for int8): ragged M, and operands given as padded-row views, which must give
     the contiguous operands' output bit for bit; the oracle on a row sample."""
     xq, wq, xs, ws = W.a8w8_inputs(M, N, K, kind, "pertoken", seed=K + M)
     xg, wg, xsg, wsg = xq.to(gpu), wq.to(gpu), xs.to(gpu), ws.to(gpu)
